@@ -1,0 +1,265 @@
+"""Python mirror of the C ABI in include/g2b_attn.h and include/g2b_synth.h.
+
+It follows the reference's own seam (/root/reference/src/l5_model.c:513-578
+plus the KV allocation of alloc_rt/free_rt, :113-149): a context per model
+shape, KV buffers in the reference [layer][ctx][row] layout, and a per-layer
+call that rotates q and k, appends k/v at `pos`, and writes the attention
+output over q.  Errors come back as ``G2BError`` carrying the C code; the
+library never falls back to the CPU and this module refuses to load without
+the compiled library.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBPATH = os.path.join(HERE, "libg2b_attn.so")
+
+G2B_OK, G2B_EINVAL, G2B_EPOS, G2B_ENOKV, G2B_ENOMEM, G2B_EDEVICE, G2B_ESWAP, G2B_EUNSUP = (
+    0, -1, -2, -3, -4, -5, -6, -7)
+ARCH_LLAMA, ARCH_QWEN2, ARCH_QWEN3 = 0, 1, 2
+
+# Every symbol the headers declare (checked by tests/test_abi.py).
+EXPORTS = [
+    "g2b_ctx_create", "g2b_ctx_destroy", "g2b_ctx_set_stream", "g2b_ctx_stream",
+    "g2b_strerror", "g2b_ctx_last_error", "g2b_kv_row_bytes", "g2b_kv_bytes",
+    "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows",
+    "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
+    "g2b_rope_table", "g2b_sync",
+    "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
+    "g2b_ctx_profile", "g2b_ctx_profile_read",
+]
+
+
+class G2BError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (code {code})")
+        self.code = code
+
+
+class _Shape(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("rope_theta", C.c_float), ("arch", C.c_int32),
+                ("kv_q8", C.c_int32)]
+
+
+class _Seq(C.Structure):
+    _fields_ = [("pos", C.c_int32), ("ctx_cap", C.c_int32), ("kcache", C.c_void_p),
+                ("vcache", C.c_void_p)]
+
+
+@dataclass(frozen=True)
+class Shape:
+    """ModelCfg fields the path reads (include/g2b.h:51-55) plus F_KV_Q8."""
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    rope_theta: float
+    arch: int
+    kv_q8: bool
+
+    @property
+    def nq(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def nkv(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    def c(self) -> _Shape:
+        return _Shape(self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
+                      self.rope_theta, self.arch, 1 if self.kv_q8 else 0)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load the in-tree libg2b_attn.so; fail loudly when it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBPATH):
+            raise RuntimeError(f"{LIBPATH} is missing: build it with `make -C gguf2bin_amd` "
+                               "(or __graft_entry__.build())")
+        L = C.CDLL(LIBPATH)
+        vp, i32, u64 = C.c_void_p, C.c_int32, C.c_uint64
+        fp = C.c_void_p
+        sig = {
+            "g2b_ctx_create": ([C.POINTER(vp), i32, C.POINTER(_Shape)], C.c_int),
+            "g2b_ctx_destroy": ([vp], C.c_int),
+            "g2b_ctx_set_stream": ([vp, vp], C.c_int),
+            "g2b_ctx_stream": ([vp], vp),
+            "g2b_strerror": ([i32], C.c_char_p),
+            "g2b_ctx_last_error": ([vp], C.c_char_p),
+            "g2b_kv_row_bytes": ([C.POINTER(_Shape)], C.c_size_t),
+            "g2b_kv_bytes": ([C.POINTER(_Shape), i32], u64),
+            "g2b_kv_offset": ([C.POINTER(_Shape), i32, i32, i32], u64),
+            "g2b_kv_alloc": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], C.c_int),
+            "g2b_kv_free": ([vp, vp, vp], C.c_int),
+            "g2b_kv_append_rows": ([vp, vp, vp, i32, i32, i32, i32, fp, fp], C.c_int),
+            "g2b_batch_begin": ([vp, i32, C.POINTER(_Seq)], C.c_int),
+            "g2b_attn_layers": ([vp, i32, i32, fp, fp, fp, fp, i32], C.c_int),
+            "g2b_attn_forward": ([vp, i32, i32, i32, vp, vp, fp, fp, fp, fp], C.c_int),
+            "g2b_attn_forward_host": ([vp, i32, i32, i32, vp, vp, fp, fp, fp, fp], C.c_int),
+            "g2b_rope_table": ([i32, i32, i32, C.c_float, fp], C.c_int),
+            "g2b_sync": ([vp], C.c_int),
+            "g2b_stream_seed": ([u64, i32, i32, i32], u64),
+            "g2b_synth_normal": ([vp, fp, u64, u64], C.c_int),
+            "g2b_synth_fill_kv": ([vp, vp, vp, i32, i32, i32, i32, i32, u64, i32, C.c_float],
+                                  C.c_int),
+            "g2b_synth_copy": ([vp, vp, vp, u64], C.c_int),
+            "g2b_ctx_profile": ([vp, i32], C.c_int),
+            "g2b_ctx_profile_read": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)],
+                                     C.c_int),
+        }
+        for name, (args, res) in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = res
+        _lib = L
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().g2b_strerror(code).decode()
+
+
+def kv_row_bytes(shape: Shape) -> int:
+    return int(lib().g2b_kv_row_bytes(C.byref(shape.c())))
+
+
+def kv_bytes(shape: Shape, ctx_cap: int) -> int:
+    return int(lib().g2b_kv_bytes(C.byref(shape.c()), ctx_cap))
+
+
+def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
+    return int(lib().g2b_kv_offset(C.byref(shape.c()), ctx_cap, layer, pos))
+
+
+def rope_table(pos0: int, n_pos: int, head_dim: int, theta: float) -> np.ndarray:
+    out = np.zeros((max(n_pos, 1), max(head_dim, 2)), np.float32)
+    rc = lib().g2b_rope_table(pos0, n_pos, head_dim, theta, out.ctypes.data)
+    if rc:
+        raise G2BError(rc, f"g2b_rope_table: {strerror(rc)}")
+    return out[:n_pos, :head_dim]
+
+
+def stream_seed(base: int, seq: int, layer: int, tensor: int) -> int:
+    return int(lib().g2b_stream_seed(base & 0xFFFFFFFFFFFFFFFF, seq, layer, tensor))
+
+
+class Context:
+    """One g2b_ctx: a model shape on one device (include/g2b_attn.h)."""
+
+    def __init__(self, shape: Shape, device: int = 0):
+        self.shape = shape
+        h = C.c_void_p()
+        rc = lib().g2b_ctx_create(C.byref(h), device, C.byref(shape.c()))
+        if rc:
+            raise G2BError(rc, f"g2b_ctx_create: {strerror(rc)}")
+        self.h = h.value
+
+    def _check(self, rc: int, what: str):
+        if rc:
+            detail = lib().g2b_ctx_last_error(self.h).decode()
+            raise G2BError(rc, f"{what}: {strerror(rc)}: {detail}")
+
+    def close(self):
+        if self.h:
+            lib().g2b_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return lib().g2b_ctx_stream(self.h) or 0
+
+    def set_stream(self, stream: Optional[int]):
+        self._check(lib().g2b_ctx_set_stream(self.h, stream), "g2b_ctx_set_stream")
+
+    def sync(self):
+        self._check(lib().g2b_sync(self.h), "g2b_sync")
+
+    # ---- KV (alloc_rt / free_rt) ----
+    def kv_alloc(self, ctx_cap: int):
+        k, v = C.c_void_p(), C.c_void_p()
+        self._check(lib().g2b_kv_alloc(self.h, ctx_cap, C.byref(k), C.byref(v)), "g2b_kv_alloc")
+        return k.value, v.value
+
+    def kv_free(self, k: int, v: int):
+        self._check(lib().g2b_kv_free(self.h, k, v), "g2b_kv_free")
+
+    def kv_append_rows(self, kc: int, vc: int, ctx_cap: int, layer: int, pos0: int,
+                       n_rows: int, k_dev: int, v_dev: int):
+        self._check(lib().g2b_kv_append_rows(self.h, kc, vc, ctx_cap, layer, pos0, n_rows,
+                                             k_dev, v_dev), "g2b_kv_append_rows")
+
+    # ---- the path ----
+    def batch_begin(self, seqs: Sequence[tuple]):
+        arr = (_Seq * len(seqs))(*[_Seq(int(p), int(c), k, v) for (p, c, k, v) in seqs])
+        self._check(lib().g2b_batch_begin(self.h, len(seqs), arr), "g2b_batch_begin")
+
+    def attn_layers(self, layer0: int, n_layers: int, q: int, k: int, v: int,
+                    att: Optional[int] = None, att_stride: int = 0):
+        self._check(lib().g2b_attn_layers(self.h, layer0, n_layers, q, k, v, att, att_stride),
+                    "g2b_attn_layers")
+
+    def attn_forward(self, layer: int, pos: int, ctx_cap: int, kc: int, vc: int, q: int,
+                     k: int, v: int, att: Optional[int] = None):
+        self._check(lib().g2b_attn_forward(self.h, layer, pos, ctx_cap, kc, vc, q, k, v, att),
+                    "g2b_attn_forward")
+
+    def attn_forward_host(self, layer: int, pos: int, ctx_cap: int, kc: int, vc: int,
+                          q: np.ndarray, k: np.ndarray, v: np.ndarray, want_att: bool = False):
+        """Host-memory variant; returns (out, att or None).  q is not modified."""
+        qo = np.ascontiguousarray(q, np.float32).copy()
+        kk = np.ascontiguousarray(k, np.float32)
+        vv = np.ascontiguousarray(v, np.float32)
+        att = np.zeros(self.shape.n_heads * ctx_cap, np.float32) if want_att else None
+        self._check(lib().g2b_attn_forward_host(
+            self.h, layer, pos, ctx_cap, kc, vc, qo.ctypes.data, kk.ctypes.data,
+            vv.ctypes.data, att.ctypes.data if att is not None else None),
+            "g2b_attn_forward_host")
+        return qo, (att.reshape(self.shape.n_heads, ctx_cap) if att is not None else None)
+
+    # ---- synthetic inputs (bench / full-size tests) ----
+    def synth_normal(self, out: int, n: int, seed: int):
+        self._check(lib().g2b_synth_normal(self.h, out, n, seed & 0xFFFFFFFFFFFFFFFF),
+                    "g2b_synth_normal")
+
+    def synth_copy(self, dst: int, src: int, nbytes: int):
+        self._check(lib().g2b_synth_copy(self.h, dst, src, nbytes), "g2b_synth_copy")
+
+    def profile(self, enable: bool):
+        self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")
+
+    def profile_read(self):
+        """(summed decode-kernel milliseconds, launches) since the last read."""
+        ms, n = C.c_double(0), C.c_int64(0)
+        self._check(lib().g2b_ctx_profile_read(self.h, C.byref(ms), C.byref(n)),
+                    "g2b_ctx_profile_read")
+        return ms.value, n.value
+
+    def synth_fill_kv(self, kc: int, vc: int, ctx_cap: int, layer0: int, n_layers: int,
+                      pos0: int, n_pos: int, base_seed: int, seq: int,
+                      sel_threshold: float = float("inf")):
+        self._check(lib().g2b_synth_fill_kv(self.h, kc, vc, ctx_cap, layer0, n_layers, pos0,
+                                            n_pos, base_seed & 0xFFFFFFFFFFFFFFFF, seq,
+                                            sel_threshold), "g2b_synth_fill_kv")

@@ -1,0 +1,565 @@
+// g2b_api.hip - the C ABI of include/g2b_attn.h and include/g2b_synth.h.
+//
+// Host-side control of the decode-attention path: shape validation, KV
+// buffers in HBM with the reference layout, the RoPE table (built on the host
+// by g2b_rope_table), staging of batch descriptors, split sizing and the
+// three launches per call (append, decode, combine).  Nothing here computes
+// attention on the CPU: if the device path cannot run, the call fails.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "g2b_attn.h"
+#include "g2b_internal.h"
+#include "g2b_synth.h"
+
+using namespace g2b;
+
+struct g2b_ctx {
+  int32_t device = 0;
+  g2b_shape shape{};
+  ShapeDev sh{};
+  float qscale = 0.f;
+  hipStream_t own = nullptr, stream = nullptr;
+
+  float *rope = nullptr;  // [rope_len][head_dim]
+  int32_t rope_len = 0;
+
+  // current batch
+  int32_t n_seq = 0, max_pos = 0;
+  int64_t total_pos = 0;
+  SeqDev *d_seqs = nullptr, *h_seqs = nullptr;  // h_seqs: pinned staging
+  int32_t seqs_cap = 0;
+  hipEvent_t seqs_ev = nullptr;
+  bool seqs_ev_live = false;
+
+  // scratch
+  float *qrot = nullptr;
+  size_t qrot_cap = 0;  // floats
+  float *part = nullptr;
+  size_t part_cap = 0;
+  float *hstage = nullptr;  // device staging for the *_host entry point
+  size_t hstage_cap = 0;
+
+  // decode-launch timing (g2b_ctx_profile)
+  bool prof = false;
+  std::vector<hipEvent_t> prof_ev;  // pairs: [2i] before, [2i+1] after launch i
+  size_t prof_used = 0;             // events used in the current window
+
+  std::string err;
+};
+
+namespace {
+
+int fail(g2b_ctx *c, int code, const char *fmt, ...) {
+  if (c) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+  }
+  return code;
+}
+
+#define G2B_HIP(c, call)                                                          \
+  do {                                                                            \
+    hipError_t e_ = (call);                                                       \
+    if (e_ != hipSuccess) return fail((c), G2B_EDEVICE, "%s: %s", #call, hipGetErrorString(e_)); \
+  } while (0)
+
+size_t row_bytes_of(const g2b_shape *s) {
+  const size_t nkv = (size_t)s->n_kv_heads * (size_t)s->head_dim;
+  return s->kv_q8 ? (nkv + 31u) / 32u * 34u : nkv * 4u;
+}
+
+// Readable slack after each cache: the specialised loaders fetch whole
+// dwords around 34-byte blocks.
+constexpr size_t kKvSlack = 256;
+
+int set_device(g2b_ctx *c) {
+  G2B_HIP(c, hipSetDevice(c->device));
+  return G2B_OK;
+}
+
+// Grow a device buffer (contents are not kept); waits for queued work first.
+int grow(g2b_ctx *c, float **buf, size_t *cap, size_t need_floats) {
+  if (*cap >= need_floats) return G2B_OK;
+  size_t n = std::max(need_floats, *cap + *cap / 2);
+  if (*buf) {
+    G2B_HIP(c, hipStreamSynchronize(c->stream));
+    G2B_HIP(c, hipFree(*buf));
+    *buf = nullptr;
+    *cap = 0;
+  }
+  if (hipMalloc((void **)buf, n * sizeof(float)) != hipSuccess) {
+    *buf = nullptr;
+    (void)hipGetLastError();
+    return fail(c, G2B_ENOMEM, "hipMalloc of %zu bytes failed", n * sizeof(float));
+  }
+  *cap = n;
+  return G2B_OK;
+}
+
+int ensure_rope(g2b_ctx *c, int32_t len) {
+  if (!c->sh.rope_on || len <= c->rope_len) return G2B_OK;
+  const int32_t n = std::max(len, std::max(c->rope_len * 2, 256));
+  const size_t floats = (size_t)n * (size_t)c->shape.head_dim;
+  float *host = (float *)malloc(floats * sizeof(float));
+  if (!host) return fail(c, G2B_ENOMEM, "host RoPE table of %zu bytes", floats * 4);
+  int rc = g2b_rope_table(0, n, c->shape.head_dim, c->shape.rope_theta, host);
+  if (rc) {
+    free(host);
+    return fail(c, rc, "g2b_rope_table failed");
+  }
+  float *dev = nullptr;
+  if (hipMalloc((void **)&dev, floats * sizeof(float)) != hipSuccess) {
+    free(host);
+    (void)hipGetLastError();
+    return fail(c, G2B_ENOMEM, "hipMalloc RoPE table");
+  }
+  hipError_t e = hipMemcpy(dev, host, floats * sizeof(float), hipMemcpyHostToDevice);
+  free(host);
+  if (e != hipSuccess) {
+    (void)hipFree(dev);
+    return fail(c, G2B_EDEVICE, "RoPE table upload: %s", hipGetErrorString(e));
+  }
+  if (c->rope) {
+    G2B_HIP(c, hipStreamSynchronize(c->stream));
+    G2B_HIP(c, hipFree(c->rope));
+  }
+  c->rope = dev;
+  c->rope_len = n;
+  return G2B_OK;
+}
+
+// Positions per split.  Aim for ~2048 workgroups per call so that the 256
+// CUs (two resident 256-thread workgroups each) see several waves of work;
+// keep at most 512 splits per sequence (the combine stages 4 weights per
+// split in LDS) and obey the generic kernel's LDS limit.
+int32_t choose_split(const g2b_ctx *c, int64_t total_pos, int32_t max_pos, int32_t n_layers,
+                     bool fast) {
+  const int64_t work = total_pos * (int64_t)n_layers;
+  int64_t sl = (work + 2047) / 2048;
+  sl = std::max<int64_t>(sl, 64);
+  sl = (sl + 63) / 64 * 64;
+  const int64_t min_for_cap = ((int64_t)max_pos + 1 + 511) / 512;
+  sl = std::max(sl, (min_for_cap + 63) / 64 * 64);
+  if (!fast) sl = std::min<int64_t>(sl, kGenericMaxSplit);
+  sl = std::min<int64_t>(sl, (int64_t)max_pos + 1 + 63);
+  (void)c;
+  return (int32_t)std::max<int64_t>(sl, 1);
+}
+
+int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_seq,
+               int32_t max_pos, int64_t total_pos, int32_t layer0, int32_t n_layers, float *q,
+               const float *k, const float *v, float *att, int32_t att_stride) {
+  if (layer0 < 0 || n_layers < 1 || layer0 + n_layers > c->shape.n_layers)
+    return fail(c, G2B_EINVAL, "layers [%d,%d) outside [0,%d)", layer0, layer0 + n_layers,
+                c->shape.n_layers);
+  if (!q || !k || !v) return fail(c, G2B_EINVAL, "q/k/v must be device pointers");
+  if (att && att_stride < max_pos + 1)
+    return fail(c, G2B_EINVAL, "att_stride %d < pos+1 = %d", att_stride, max_pos + 1);
+  if (int rc = ensure_rope(c, max_pos + 1)) return rc;
+
+  const int32_t nh = c->shape.n_heads, hd = c->shape.head_dim;
+  const size_t nq = (size_t)nh * hd;
+  const bool fast = decode_fast_available(c->sh);
+  const int32_t split_len = choose_split(c, total_pos, max_pos, n_layers, fast);
+  const int32_t max_splits = (max_pos + 1 + split_len - 1) / split_len;
+  if (max_splits > 512)
+    return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
+
+  if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
+  const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
+                             kWavesPerSplit * (size_t)(kPartHead + hd);
+  if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
+
+  AppendParams ap{};
+  ap.sh = c->sh;
+  ap.seqs = d_seqs;
+  ap.one = one;
+  ap.n_seq = n_seq;
+  ap.layer0 = layer0;
+  ap.q_in = q;
+  ap.q_rot = c->qrot;
+  ap.k_in = k;
+  ap.v_in = v;
+  ap.rope = c->rope;
+  G2B_HIP(c, launch_append_batch(ap, n_layers, c->stream));
+
+  DecodeParams dp{};
+  dp.sh = c->sh;
+  dp.seqs = d_seqs;
+  dp.one = one;
+  dp.n_seq = n_seq;
+  dp.layer0 = layer0;
+  dp.split_len = split_len;
+  dp.max_splits = max_splits;
+  dp.q_rot = c->qrot;
+  dp.q_out = q;
+  dp.part = c->part;
+  dp.att = att;
+  dp.att_stride = att_stride;
+  dp.qscale = c->qscale;
+  int used_fast = 0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  if (c->prof) {
+    if (c->prof_used + 2 > c->prof_ev.size()) {
+      for (int i = 0; i < 2; i++) {
+        hipEvent_t e;
+        G2B_HIP(c, hipEventCreate(&e));
+        c->prof_ev.push_back(e);
+      }
+    }
+    ev0 = c->prof_ev[c->prof_used];
+    ev1 = c->prof_ev[c->prof_used + 1];
+    c->prof_used += 2;
+    G2B_HIP(c, hipEventRecord(ev0, c->stream));
+  }
+  G2B_HIP(c, launch_decode(dp, n_layers, c->stream, &used_fast));
+  if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
+  G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
+  return G2B_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *g2b_strerror(int32_t code) {
+  switch (code) {
+    case G2B_OK: return "ok";
+    case G2B_EINVAL: return "invalid argument";
+    case G2B_EPOS: return "position outside [0, ctx)";
+    case G2B_ENOKV: return "KV cache not allocated";
+    case G2B_ENOMEM: return "device allocation failed";
+    case G2B_EDEVICE: return "HIP runtime error";
+    case G2B_ESWAP: return "file-backed KV cannot live in HBM";
+    case G2B_EUNSUP: return "unsupported shape";
+    default: return "unknown error";
+  }
+}
+
+const char *g2b_ctx_last_error(g2b_ctx *c) { return c ? c->err.c_str() : ""; }
+
+size_t g2b_kv_row_bytes(const g2b_shape *s) { return s ? row_bytes_of(s) : 0; }
+
+uint64_t g2b_kv_bytes(const g2b_shape *s, int32_t ctx_cap) {
+  if (!s || ctx_cap <= 0 || s->n_layers <= 0) return 0;
+  return (uint64_t)s->n_layers * (uint64_t)ctx_cap * (uint64_t)row_bytes_of(s);
+}
+
+uint64_t g2b_kv_offset(const g2b_shape *s, int32_t ctx_cap, int32_t layer, int32_t pos) {
+  if (!s) return 0;
+  return ((uint64_t)layer * (uint64_t)ctx_cap + (uint64_t)pos) * (uint64_t)row_bytes_of(s);
+}
+
+int g2b_ctx_create(g2b_ctx **out, int32_t device, const g2b_shape *s) {
+  if (!out || !s) return G2B_EINVAL;
+  *out = nullptr;
+  if (s->n_layers < 1 || s->n_heads < 1 || s->n_kv_heads < 1 || s->head_dim < 2 ||
+      (s->head_dim & 1) || s->n_heads % s->n_kv_heads)
+    return G2B_EINVAL;
+  if ((int64_t)s->n_kv_heads * s->head_dim > 16384) return G2B_EUNSUP;  // append LDS
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
+    (void)hipGetLastError();
+    return G2B_EDEVICE;
+  }
+  g2b_ctx *c = new (std::nothrow) g2b_ctx();
+  if (!c) return G2B_ENOMEM;
+  c->device = device;
+  c->shape = *s;
+  c->sh.n_layers = s->n_layers;
+  c->sh.n_heads = s->n_heads;
+  c->sh.n_kv_heads = s->n_kv_heads;
+  c->sh.head_dim = s->head_dim;
+  c->sh.arch_llama = s->arch == G2B_ARCH_LLAMA ? 1 : 0;
+  c->sh.kv_q8 = s->kv_q8 ? 1 : 0;
+  c->sh.rope_on = (s->head_dim / 2) <= 512 ? 1 : 0;
+  c->sh.row_bytes = (uint32_t)row_bytes_of(s);
+  // l5_model.c:518 scale, times log2(e) for exp2-based softmax
+  c->qscale = (1.f / sqrtf((float)s->head_dim)) * 1.44269504088896340736f;
+  if (hipSetDevice(device) != hipSuccess ||
+      hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&c->seqs_ev, hipEventDisableTiming) != hipSuccess) {
+    (void)hipGetLastError();
+    if (c->own) (void)hipStreamDestroy(c->own);
+    delete c;
+    return G2B_EDEVICE;
+  }
+  c->stream = c->own;
+  *out = c;
+  return G2B_OK;
+}
+
+int g2b_ctx_destroy(g2b_ctx *c) {
+  if (!c) return G2B_EINVAL;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  if (c->own) (void)hipStreamSynchronize(c->own);
+  if (c->rope) (void)hipFree(c->rope);
+  if (c->d_seqs) (void)hipFree(c->d_seqs);
+  if (c->h_seqs) (void)hipHostFree(c->h_seqs);
+  if (c->qrot) (void)hipFree(c->qrot);
+  if (c->part) (void)hipFree(c->part);
+  if (c->hstage) (void)hipFree(c->hstage);
+  if (c->seqs_ev) (void)hipEventDestroy(c->seqs_ev);
+  for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
+  if (c->own) (void)hipStreamDestroy(c->own);
+  delete c;
+  return G2B_OK;
+}
+
+int g2b_ctx_set_stream(g2b_ctx *c, void *stream) {
+  if (!c) return G2B_EINVAL;
+  c->stream = stream ? (hipStream_t)stream : c->own;
+  return G2B_OK;
+}
+
+void *g2b_ctx_stream(g2b_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int g2b_kv_alloc(g2b_ctx *c, int32_t ctx_cap, void **kc, void **vc) {
+  if (!c || !kc || !vc || ctx_cap < 1) return fail(c, G2B_EINVAL, "bad kv_alloc arguments");
+  *kc = *vc = nullptr;
+  if (int rc = set_device(c)) return rc;
+  const size_t bytes = (size_t)g2b_kv_bytes(&c->shape, ctx_cap) + kKvSlack;
+  void *k = nullptr, *v = nullptr;
+  if (hipMalloc(&k, bytes) != hipSuccess || hipMalloc(&v, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    if (k) (void)hipFree(k);
+    return fail(c, G2B_ENOMEM, "KV allocation of 2 x %zu bytes failed", bytes);
+  }
+  if (hipMemset(k, 0, bytes) != hipSuccess || hipMemset(v, 0, bytes) != hipSuccess) {
+    (void)hipFree(k);
+    (void)hipFree(v);
+    return fail(c, G2B_EDEVICE, "KV memset failed");
+  }
+  if (int rc = ensure_rope(c, ctx_cap)) {
+    (void)hipFree(k);
+    (void)hipFree(v);
+    return rc;
+  }
+  *kc = k;
+  *vc = v;
+  return G2B_OK;
+}
+
+int g2b_kv_free(g2b_ctx *c, void *kc, void *vc) {
+  if (!c) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  if (kc) G2B_HIP(c, hipFree(kc));
+  if (vc) G2B_HIP(c, hipFree(vc));
+  return G2B_OK;
+}
+
+int g2b_kv_append_rows(g2b_ctx *c, void *kc, void *vc, int32_t ctx_cap, int32_t layer,
+                       int32_t pos0, int32_t n_rows, const float *k, const float *v) {
+  if (!c) return G2B_EINVAL;
+  if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (!k || !v || n_rows < 0 || layer < 0 || layer >= c->shape.n_layers)
+    return fail(c, G2B_EINVAL, "bad append_rows arguments");
+  if (pos0 < 0 || (int64_t)pos0 + n_rows > ctx_cap)
+    return fail(c, G2B_EPOS, "rows [%d,%d) outside [0,%d)", pos0, pos0 + n_rows, ctx_cap);
+  if (n_rows == 0) return G2B_OK;
+  if (int rc = set_device(c)) return rc;
+  if (int rc = ensure_rope(c, pos0 + n_rows)) return rc;
+  AppendParams ap{};
+  ap.sh = c->sh;
+  ap.seqs = nullptr;
+  ap.one.pos = pos0;
+  ap.one.ctx_cap = ctx_cap;
+  ap.one.k = (uint8_t *)kc;
+  ap.one.v = (uint8_t *)vc;
+  ap.n_seq = 1;
+  ap.k_in = k;
+  ap.v_in = v;
+  ap.rope = c->rope;
+  ap.pos0 = pos0;
+  G2B_HIP(c, launch_append_rows(ap, layer, n_rows, c->stream));
+  return G2B_OK;
+}
+
+int g2b_batch_begin(g2b_ctx *c, int32_t n_seq, const g2b_seq *seqs) {
+  if (!c) return G2B_EINVAL;
+  if (n_seq < 1 || !seqs) return fail(c, G2B_EINVAL, "empty batch");
+  if (n_seq > 65535) return fail(c, G2B_EUNSUP, "batch of %d sequences", n_seq);
+  int32_t max_pos = 0;
+  int64_t total = 0;
+  for (int32_t i = 0; i < n_seq; i++) {
+    const g2b_seq &s = seqs[i];
+    if (!s.kcache || !s.vcache) return fail(c, G2B_ENOKV, "sequence %d has no KV", i);
+    if (s.ctx_cap < 1 || s.pos < 0 || s.pos >= s.ctx_cap)
+      return fail(c, G2B_EPOS, "sequence %d: pos=%d outside [0,%d)", i, s.pos, s.ctx_cap);
+    max_pos = std::max(max_pos, s.pos);
+    total += (int64_t)s.pos + 1;
+  }
+  if (int rc = set_device(c)) return rc;
+  if (n_seq > c->seqs_cap) {
+    G2B_HIP(c, hipStreamSynchronize(c->stream));
+    if (c->d_seqs) G2B_HIP(c, hipFree(c->d_seqs));
+    if (c->h_seqs) G2B_HIP(c, hipHostFree(c->h_seqs));
+    c->d_seqs = nullptr;
+    c->h_seqs = nullptr;
+    c->seqs_cap = 0;
+    c->seqs_ev_live = false;
+    const int32_t cap = std::max(n_seq, 64);
+    if (hipMalloc((void **)&c->d_seqs, cap * sizeof(SeqDev)) != hipSuccess ||
+        hipHostMalloc((void **)&c->h_seqs, cap * sizeof(SeqDev), hipHostMallocDefault) !=
+            hipSuccess) {
+      (void)hipGetLastError();
+      return fail(c, G2B_ENOMEM, "batch descriptors");
+    }
+    c->seqs_cap = cap;
+  }
+  if (c->seqs_ev_live) G2B_HIP(c, hipEventSynchronize(c->seqs_ev));
+  for (int32_t i = 0; i < n_seq; i++) {
+    SeqDev d{};
+    d.pos = seqs[i].pos;
+    d.ctx_cap = seqs[i].ctx_cap;
+    d.k = (uint8_t *)seqs[i].kcache;
+    d.v = (uint8_t *)seqs[i].vcache;
+    c->h_seqs[i] = d;
+  }
+  G2B_HIP(c, hipMemcpyAsync(c->d_seqs, c->h_seqs, n_seq * sizeof(SeqDev),
+                            hipMemcpyHostToDevice, c->stream));
+  G2B_HIP(c, hipEventRecord(c->seqs_ev, c->stream));
+  c->seqs_ev_live = true;
+  if (int rc = ensure_rope(c, max_pos + 1)) return rc;
+  c->n_seq = n_seq;
+  c->max_pos = max_pos;
+  c->total_pos = total;
+  return G2B_OK;
+}
+
+int g2b_attn_layers(g2b_ctx *c, int32_t layer0, int32_t n_layers, float *q, const float *k,
+                    const float *v, float *att, int32_t att_stride) {
+  if (!c) return G2B_EINVAL;
+  if (c->n_seq < 1) return fail(c, G2B_EINVAL, "no batch: call g2b_batch_begin first");
+  if (int rc = set_device(c)) return rc;
+  SeqDev none{};
+  return run_layers(c, c->d_seqs, none, c->n_seq, c->max_pos, c->total_pos, layer0, n_layers,
+                    q, k, v, att, att_stride);
+}
+
+int g2b_attn_forward(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, void *kc,
+                     void *vc, float *q, const float *k, const float *v, float *att) {
+  if (!c) return G2B_EINVAL;
+  if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (ctx_cap < 1 || pos < 0 || pos >= ctx_cap)
+    return fail(c, G2B_EPOS, "pos=%d outside [0,%d)", pos, ctx_cap);
+  if (int rc = set_device(c)) return rc;
+  SeqDev one{};
+  one.pos = pos;
+  one.ctx_cap = ctx_cap;
+  one.k = (uint8_t *)kc;
+  one.v = (uint8_t *)vc;
+  return run_layers(c, nullptr, one, 1, pos, (int64_t)pos + 1, layer, 1, q, k, v, att, ctx_cap);
+}
+
+int g2b_attn_forward_host(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, void *kc,
+                          void *vc, float *q, const float *k, const float *v, float *att) {
+  if (!c) return G2B_EINVAL;
+  if (!q || !k || !v) return fail(c, G2B_EINVAL, "q/k/v must be host pointers");
+  if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (ctx_cap < 1 || pos < 0 || pos >= ctx_cap)
+    return fail(c, G2B_EPOS, "pos=%d outside [0,%d)", pos, ctx_cap);
+  if (int rc = set_device(c)) return rc;
+  const size_t nq = (size_t)c->shape.n_heads * c->shape.head_dim;
+  const size_t nkv = (size_t)c->shape.n_kv_heads * c->shape.head_dim;
+  const size_t natt = att ? (size_t)c->shape.n_heads * (size_t)ctx_cap : 0;
+  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nq + 2 * nkv + natt)) return rc;
+  float *dq = c->hstage, *dk = dq + nq, *dv = dk + nkv, *da = att ? dv + nkv : nullptr;
+  G2B_HIP(c, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, c->stream));
+  G2B_HIP(c, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, c->stream));
+  G2B_HIP(c, hipMemcpyAsync(dv, v, nkv * 4, hipMemcpyHostToDevice, c->stream));
+  if (int rc = g2b_attn_forward(c, layer, pos, ctx_cap, kc, vc, dq, dk, dv, da)) return rc;
+  G2B_HIP(c, hipMemcpyAsync(q, dq, nq * 4, hipMemcpyDeviceToHost, c->stream));
+  if (att)
+    G2B_HIP(c, hipMemcpyAsync(att, da, natt * 4, hipMemcpyDeviceToHost, c->stream));
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
+int g2b_sync(g2b_ctx *c) {
+  if (!c) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
+int g2b_synth_normal(g2b_ctx *c, float *out, uint64_t n, uint64_t seed) {
+  if (!c || (!out && n)) return fail(c, G2B_EINVAL, "bad synth_normal arguments");
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, launch_synth_normal(out, n, seed, c->stream));
+  return G2B_OK;
+}
+
+int g2b_synth_fill_kv(g2b_ctx *c, void *kc, void *vc, int32_t ctx_cap, int32_t layer0,
+                      int32_t n_layers, int32_t pos0, int32_t n_pos, uint64_t base_seed,
+                      int32_t seq, float sel_threshold) {
+  if (!c) return G2B_EINVAL;
+  if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (layer0 < 0 || n_layers < 1 || layer0 + n_layers > c->shape.n_layers || n_pos < 0)
+    return fail(c, G2B_EINVAL, "bad synth_fill_kv range");
+  if (pos0 < 0 || (int64_t)pos0 + n_pos > ctx_cap)
+    return fail(c, G2B_EPOS, "rows [%d,%d) outside [0,%d)", pos0, pos0 + n_pos, ctx_cap);
+  if (n_pos == 0) return G2B_OK;
+  if (int rc = set_device(c)) return rc;
+  if (int rc = ensure_rope(c, pos0 + n_pos)) return rc;
+  SynthParams sp{};
+  sp.sh = c->sh;
+  sp.k = (uint8_t *)kc;
+  sp.v = (uint8_t *)vc;
+  sp.ctx_cap = ctx_cap;
+  sp.layer0 = layer0;
+  sp.pos0 = pos0;
+  sp.n_pos = n_pos;
+  sp.base_seed = base_seed;
+  sp.seq = seq;
+  sp.sel_threshold = sel_threshold;
+  sp.rope = c->rope;
+  G2B_HIP(c, launch_synth_fill(sp, n_layers, c->stream));
+  return G2B_OK;
+}
+
+int g2b_synth_copy(g2b_ctx *c, void *dst, const void *src, uint64_t nbytes) {
+  if (!c || !dst || !src || (nbytes & 15) || ((uintptr_t)dst & 15) || ((uintptr_t)src & 15))
+    return fail(c, G2B_EINVAL, "copy needs 16-byte multiples and alignment");
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, launch_copy16(dst, src, nbytes / 16, c->stream));
+  return G2B_OK;
+}
+
+int g2b_ctx_profile(g2b_ctx *c, int32_t enable) {
+  if (!c) return G2B_EINVAL;
+  c->prof = enable != 0;
+  c->prof_used = 0;
+  return G2B_OK;
+}
+
+int g2b_ctx_profile_read(g2b_ctx *c, double *decode_ms, int64_t *launches) {
+  if (!c || !decode_ms || !launches) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  double total = 0.0;
+  for (size_t i = 0; i + 1 < c->prof_used; i += 2) {
+    G2B_HIP(c, hipEventSynchronize(c->prof_ev[i + 1]));
+    float ms = 0.f;
+    G2B_HIP(c, hipEventElapsedTime(&ms, c->prof_ev[i], c->prof_ev[i + 1]));
+    total += ms;
+  }
+  *decode_ms = total;
+  *launches = (int64_t)(c->prof_used / 2);
+  c->prof_used = 0;
+  return G2B_OK;
+}
+
+}  // extern "C"

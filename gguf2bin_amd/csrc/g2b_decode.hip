@@ -1,0 +1,521 @@
+// g2b_decode.hip - split-K flash-decoding over the reference KV layout, gfx950.
+//
+// Replaces the score / softmax / V-accumulate loops of
+// /root/reference/src/l5_model.c:518-557 (AVX2) and :558-577 (scalar):
+//   att[h][t] = dot(q_h, k_t[h/group]) / sqrt(hd), softmax over t <= pos,
+//   out_h = sum_t att[h][t] * v_t[h/group].
+// The reference dequantises a whole row per position into a scratch buffer
+// (kv_key_row / kv_val_row, l5_model.c:248-265) and walks every q head.  Here
+// the row is never materialised: each lane owns one chunk of the row (one
+// 32-element Q8_0 block, half a block, or 16 F32 values), keeps the q values
+// of the GQA group for that chunk in registers, dequantises in registers,
+// and keeps its own online-softmax state.  A position's partial dot products
+// are summed over the lanes of a head with DPP.  Nothing goes through LDS in
+// the main loop and there is no barrier: each wave streams rows
+// independently with wide loads.  Scores are kept in the log2 domain
+// (q pre-scaled by log2(e)/sqrt(hd)) so that softmax uses v_exp_f32.
+//
+// Splits: workgroup (split, seq, layer) covers positions
+// [split*split_len, min(pos+1, (split+1)*split_len)); its four waves take
+// interleaved groups of PPW positions and each writes one partial
+// (m, l, acc[hd]) per q head.  k_combine merges the partials of a
+// (seq, layer, head), writes the output over q (as l5_model.c:541-557 does)
+// and, when asked, turns the stored scores into the reference's
+// att[h*ctx+t] weights.
+#include "g2b_internal.h"
+
+namespace g2b {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of N consecutive lanes; every lane of a group ends
+// with the same value (each step adds two equal-order operands).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+  if constexpr (N >= 2) x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (N >= 4) x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (N >= 8) x += dpp_f<0x141>(x);  // row_half_mirror: other quad of 8
+  if constexpr (N >= 16) x += dpp_f<0x140>(x); // row_mirror: other half of 16
+  return x;
+}
+
+__device__ __forceinline__ float i8f(uint32_t w, int byte) {
+  return (float)(int8_t)(uint8_t)(w >> (8 * byte));
+}
+
+// Per-lane addressing of its chunk inside a row.
+struct LaneOff {
+  uint32_t o0, o1, o2;  // byte offsets inside the row
+  uint32_t sel;         // v_perm_b32 selector that realigns quant dwords
+  uint32_t sshift;      // 0 or 16: where the fp16 scale sits in its dword
+};
+
+template <int FMT, int CD>
+struct Codec;
+
+// ---- F32 rows: 16 contiguous floats, four 16-byte loads ----
+template <>
+struct Codec<0, 16> {
+  struct Raw {
+    float4 x[4];
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    LaneOff o;
+    o.o0 = (uint32_t)elem0 * 4u;
+    o.o1 = o.o2 = o.sel = o.sshift = 0;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const float4 *p = reinterpret_cast<const float4 *>(row + o.o0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.x[i] = p[i];
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[16], float &scale,
+                                                const LaneOff &) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      f[4 * i + 0] = r.x[i].x;
+      f[4 * i + 1] = r.x[i].y;
+      f[4 * i + 2] = r.x[i].z;
+      f[4 * i + 3] = r.x[i].w;
+    }
+    scale = 1.f;
+  }
+};
+
+// ---- Q8_0, one full 34-byte block per lane ----
+// Block b starts at byte 34b: for even b the dword window starts at the
+// block (scale = low half of dword 0, quants at window bytes 2..33); for odd
+// b it starts two bytes earlier (scale = high half, quants at bytes 4..35).
+// Nine dwords cover the block either way and, because the last block of a
+// row is odd whenever head_dim is a multiple of 64, never leave the row.
+template <>
+struct Codec<1, 32> {
+  struct Raw {
+    uint4 a, b;
+    uint32_t c;
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u;
+    LaneOff o;
+    o.o0 = (34u * b) & ~3u;
+    o.o1 = o.o2 = 0;
+    o.sel = odd ? 0x07060504u : 0x05040302u;
+    o.sshift = odd ? 16u : 0u;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const uint8_t *p = row + o.o0;
+    r.a = *reinterpret_cast<const uint4 *>(p);
+    r.b = *reinterpret_cast<const uint4 *>(p + 16);
+    r.c = *reinterpret_cast<const uint32_t *>(p + 32);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[32], float &scale,
+                                                const LaneOff &o) {
+    const uint32_t d[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+    scale = half_bits_to_f32((d[0] >> o.sshift) & 0xffffu);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t w = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
+#pragma unroll
+      for (int k = 0; k < 4; k++) f[4 * j + k] = i8f(w, k);
+    }
+  }
+};
+
+// ---- Q8_0, half a block (16 quants) per lane ----
+// Scale dword at (34b)&~3; quant window at (34b+2+16h)&~3 (two bytes early
+// for even b).  For odd b the window is aligned and only four dwords are
+// used; the fifth load is pointed inside the block so it never leaves it.
+template <>
+struct Codec<1, 16> {
+  struct Raw {
+    uint32_t s;
+    uint4 a;
+    uint32_t c;
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u, h = ((uint32_t)elem0 >> 4) & 1u;
+    const uint32_t qstart = 34u * b + 2u + 16u * h;
+    LaneOff o;
+    o.o0 = (34u * b) & ~3u;
+    o.o1 = qstart & ~3u;
+    o.o2 = odd ? o.o1 + 12u : o.o1 + 16u;
+    o.sel = odd ? 0x03020100u : 0x05040302u;
+    o.sshift = odd ? 16u : 0u;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+    r.s = *reinterpret_cast<const uint32_t *>(row + o.o0);
+    r.a = *reinterpret_cast<const uint4 *>(row + o.o1);
+    r.c = *reinterpret_cast<const uint32_t *>(row + o.o2);
+  }
+  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[16], float &scale,
+                                                const LaneOff &o) {
+    const uint32_t d[5] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c};
+    scale = half_bits_to_f32((r.s >> o.sshift) & 0xffffu);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t w = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
+#pragma unroll
+      for (int k = 0; k < 4; k++) f[4 * j + k] = i8f(w, k);
+    }
+  }
+};
+
+// FMT: 0 = F32 KV, 1 = Q8_0 KV.  HD: head_dim.  CD: elements per lane.
+// G: q heads per KV head.  U: wave-steps in flight per loop trip.
+template <int FMT, int HD, int CD, int G, int U>
+__global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
+  constexpr int LPH = HD / CD;  // lanes per head
+  using C = Codec<FMT, CD>;
+  const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  const int t0 = split * P.split_len;
+  if (t0 >= npos) return;
+  const int t1 = min(npos, t0 + P.split_len);
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int LPP = P.sh.n_kv_heads * LPH;  // lanes per position (<= 64, checked on host)
+  const int PPW = 64 / LPP;               // positions per wave-step
+  const int slot = lane / LPP;
+  const bool lane_on = slot < PPW;
+  const int r = lane_on ? lane - slot * LPP : 0;
+  const int g = r / LPH, c = r - g * LPH;
+  const int layer = P.layer0 + li;
+  const int n_heads = P.sh.n_heads;
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+
+  float q[G][CD];
+  {
+    const float *qs =
+        P.q_rot + sidx * (size_t)(n_heads * HD) + (size_t)(g * G) * HD + (size_t)c * CD;
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int j = 0; j < CD; j += 4) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(qs + i * HD + j);
+        q[i][j + 0] = v4.x * P.qscale;
+        q[i][j + 1] = v4.y * P.qscale;
+        q[i][j + 2] = v4.z * P.qscale;
+        q[i][j + 3] = v4.w * P.qscale;
+      }
+  }
+  const LaneOff lo = C::offsets(g * HD + c * CD);
+  const size_t row = P.sh.row_bytes;
+  const uint8_t *kb = sd.k + (size_t)layer * (size_t)sd.ctx_cap * row;
+  const uint8_t *vb = sd.v + (size_t)layer * (size_t)sd.ctx_cap * row;
+
+  float m[G], l[G], acc[G][CD];
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    m[i] = kNegBig;
+    l[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CD; j++) acc[i][j] = 0.f;
+  }
+  float *att_h = nullptr;
+  if (P.att) att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
+
+  const int stride = kWavesPerSplit * PPW;
+  for (int tb = t0 + wave * PPW; tb < t1; tb += stride * U) {
+    typename C::Raw kr[U], vr[U];
+    bool valid[U];
+    int tu[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      tu[u] = tb + u * stride + slot;
+      valid[u] = lane_on && tu[u] < t1;
+      const size_t tt = (size_t)(valid[u] ? tu[u] : t0);
+      C::load(kr[u], kb + tt * row, lo);
+      C::load(vr[u], vb + tt * row, lo);
+    }
+    float sc[U][G];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float kf[CD], ks;
+      C::decode(kr[u], kf, ks, lo);
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < CD; j += 2) {
+          s0 = fmaf(q[i][j], kf[j], s0);
+          s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
+        }
+        const float s = group_sum<LPH>((s0 + s1) * ks);
+        sc[u][i] = valid[u] ? s : -INFINITY;
+      }
+    }
+    bool need = false;
+    float mn[G];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float mx = m[i];
+#pragma unroll
+      for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][i]);
+      mn[i] = mx;
+      need |= mx > m[i];
+    }
+    if (__any(need)) {
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        const float a = exp2f(m[i] - mn[i]);
+        l[i] *= a;
+#pragma unroll
+        for (int j = 0; j < CD; j++) acc[i][j] *= a;
+        m[i] = mn[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float vf[CD], vs;
+      C::decode(vr[u], vf, vs, lo);
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        const float p = exp2f(sc[u][i] - m[i]);
+        l[i] += p;
+        const float pv = p * vs;
+#pragma unroll
+        for (int j = 0; j < CD; j++) acc[i][j] = fmaf(pv, vf[j], acc[i][j]);
+      }
+      if (att_h && c == 0 && valid[u]) {
+#pragma unroll
+        for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tu[u]] = sc[u][i];
+      }
+    }
+  }
+
+  // Fold the PPW position slots of the wave into slot 0.
+  for (int k = 1; k < PPW; k++) {
+    const int src = lane + k * LPP;
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const float m2 = __shfl(m[i], src & 63);
+      const float l2 = __shfl(l[i], src & 63);
+      const float M = fmaxf(m[i], m2);
+      const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
+      l[i] = l[i] * f1 + l2 * f2;
+#pragma unroll
+      for (int j = 0; j < CD; j++) {
+        const float a2 = __shfl(acc[i][j], src & 63);
+        acc[i][j] = acc[i][j] * f1 + a2 * f2;
+      }
+      m[i] = M;
+    }
+  }
+  if (slot == 0) {
+    const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const int h = g * G + i;
+      float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * nparts +
+                            (size_t)split * kWavesPerSplit + (size_t)wave) *
+                               (size_t)(kPartHead + HD);
+      if (c == 0) {
+        pp[0] = m[i];
+        pp[1] = l[i];
+      }
+#pragma unroll
+      for (int j = 0; j < CD; j += 4)
+        *reinterpret_cast<float4 *>(pp + kPartHead + c * CD + j) =
+            make_float4(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- generic
+// Any shape (blocks spanning heads, partial blocks, any head_dim): a
+// three-pass split per q head with scores staged in LDS.  Correctness path
+// for shapes without a specialised kernel.
+
+__device__ __forceinline__ float kv_elem(const uint8_t *rowp, int e, int q8) {
+  if (!q8) return reinterpret_cast<const float *>(rowp)[e];
+  const uint8_t *blk = rowp + 34 * (e >> 5);
+  const float s = half_bits_to_f32(*reinterpret_cast<const uint16_t *>(blk));
+  return s * (float)(int8_t)blk[2 + (e & 31)];
+}
+
+__device__ float block_reduce(float x, bool is_max, float *scratch) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const float y = __shfl_xor(x, o);
+    x = is_max ? fmaxf(x, y) : x + y;
+  }
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[wave] = x;
+  __syncthreads();
+  float r = scratch[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = is_max ? fmaxf(r, scratch[w]) : r + scratch[w];
+  return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
+  __shared__ float sc[kGenericMaxSplit];
+  __shared__ float red[kThreads / 64];
+  const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  const int t0 = split * P.split_len;
+  if (t0 >= npos) return;
+  const int t1 = min(npos, t0 + P.split_len);
+  const int n = t1 - t0;
+  const int HD = P.sh.head_dim, nh = P.sh.n_heads, group = nh / P.sh.n_kv_heads;
+  const int layer = P.layer0 + li;
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const size_t row = P.sh.row_bytes;
+  const uint8_t *kb = sd.k + (size_t)layer * (size_t)sd.ctx_cap * row;
+  const uint8_t *vb = sd.v + (size_t)layer * (size_t)sd.ctx_cap * row;
+  const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
+  for (int h = 0; h < nh; h++) {
+    const int e0 = (h / group) * HD;
+    const float *qh = P.q_rot + sidx * (size_t)(nh * HD) + (size_t)h * HD;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+      const uint8_t *rp = kb + (size_t)(t0 + t) * row;
+      float s = 0.f;
+      for (int d = 0; d < HD; d++) s = fmaf(qh[d], kv_elem(rp, e0 + d, P.sh.kv_q8), s);
+      s *= P.qscale;
+      sc[t] = s;
+      if (P.att) P.att[(sidx * nh + h) * (size_t)P.att_stride + t0 + t] = s;
+    }
+    __syncthreads();
+    float mx = kNegBig;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) mx = fmaxf(mx, sc[t]);
+    const float M = block_reduce(mx, true, red);
+    float sum = 0.f;
+    for (int t = threadIdx.x; t < n; t += blockDim.x) {
+      const float p = exp2f(sc[t] - M);
+      sc[t] = p;
+      sum += p;
+    }
+    const float L = block_reduce(sum, false, red);
+    __syncthreads();
+    float *pp = P.part + ((sidx * nh + h) * nparts + (size_t)split * kWavesPerSplit) *
+                             (size_t)(kPartHead + HD);
+    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+      float a = 0.f;
+      for (int t = 0; t < n; t++) a = fmaf(sc[t], kv_elem(vb + (size_t)(t0 + t) * row, e0 + d, P.sh.kv_q8), a);
+      pp[kPartHead + d] = a;
+      for (int w = 1; w < kWavesPerSplit; w++) pp[(size_t)w * (kPartHead + HD) + kPartHead + d] = 0.f;
+    }
+    if (threadIdx.x == 0) {
+      pp[0] = M;
+      pp[1] = L;
+      for (int w = 1; w < kWavesPerSplit; w++) {
+        pp[(size_t)w * (kPartHead + HD)] = kNegBig;
+        pp[(size_t)w * (kPartHead + HD) + 1] = 0.f;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- combine
+constexpr int kCombineThreads = 128;
+constexpr int kCombineMaxParts = 2048;
+
+__global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, float *q_out) {
+  __shared__ float w[kCombineMaxParts];
+  const int h = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  const int nsplit = (npos + P.split_len - 1) / P.split_len;
+  const int np = nsplit * kWavesPerSplit;
+  const int HD = P.sh.head_dim, nh = P.sh.n_heads;
+  const size_t pstr = (size_t)(kPartHead + HD);
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const float *base =
+      P.part + (sidx * nh + h) * (size_t)P.max_splits * kWavesPerSplit * pstr;
+  float M = kNegBig;
+  for (int p = 0; p < np; p++) M = fmaxf(M, base[p * pstr]);
+  for (int p = threadIdx.x; p < np; p += blockDim.x) w[p] = exp2f(base[p * pstr] - M);
+  __syncthreads();
+  float L = 0.f;
+  for (int p = 0; p < np; p++) L = fmaf(base[p * pstr + 1], w[p], L);
+  float *out = q_out + sidx * (size_t)(nh * HD) + (size_t)h * HD;
+  for (int d = threadIdx.x; d < HD; d += blockDim.x) {
+    float o = 0.f;
+    for (int p = 0; p < np; p++) o = fmaf(base[p * pstr + kPartHead + d], w[p], o);
+    out[d] = o / L;
+  }
+  if (P.att) {
+    float *a = P.att + (sidx * nh + h) * (size_t)P.att_stride;
+    for (int t = threadIdx.x; t < npos; t += blockDim.x) a[t] = exp2f(a[t] - M) / L;
+  }
+}
+
+// ---------------------------------------------------------------- dispatch
+
+template <int FMT, int HD, int CD, int G>
+static hipError_t launch_fast(const DecodeParams &p, int n_layers, hipStream_t s) {
+  constexpr int U = 2;
+  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U>), grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int FMT, int HD>
+static hipError_t launch_fast_hd(const DecodeParams &p, int group, int n_layers, hipStream_t s) {
+  if constexpr (FMT == 1) {
+    switch (group) {
+      case 1: return launch_fast<1, HD, 32, 1>(p, n_layers, s);
+      case 2: return launch_fast<1, HD, 32, 2>(p, n_layers, s);
+      case 3: return launch_fast<1, HD, 16, 3>(p, n_layers, s);
+      case 4: return launch_fast<1, HD, 16, 4>(p, n_layers, s);
+    }
+  } else {
+    switch (group) {
+      case 1: return launch_fast<0, HD, 16, 1>(p, n_layers, s);
+      case 2: return launch_fast<0, HD, 16, 2>(p, n_layers, s);
+      case 3: return launch_fast<0, HD, 16, 3>(p, n_layers, s);
+      case 4: return launch_fast<0, HD, 16, 4>(p, n_layers, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+static int fast_chunk(const ShapeDev &sh) {
+  const int group = sh.n_heads / sh.n_kv_heads;
+  if (sh.kv_q8) return group <= 2 ? 32 : 16;
+  return 16;
+}
+
+bool decode_fast_available(const ShapeDev &sh) {
+  if (sh.head_dim != 64 && sh.head_dim != 128) return false;
+  if (sh.n_kv_heads <= 0 || sh.n_heads % sh.n_kv_heads) return false;
+  const int group = sh.n_heads / sh.n_kv_heads;
+  if (group < 1 || group > 4) return false;
+  const int lanes = sh.n_kv_heads * (sh.head_dim / fast_chunk(sh));
+  return lanes <= 64;
+}
+
+hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int *used_fast) {
+  if (decode_fast_available(p.sh)) {
+    if (used_fast) *used_fast = 1;
+    const int group = p.sh.n_heads / p.sh.n_kv_heads;
+    if (p.sh.kv_q8)
+      return p.sh.head_dim == 128 ? launch_fast_hd<1, 128>(p, group, n_layers, s)
+                                  : launch_fast_hd<1, 64>(p, group, n_layers, s);
+    return p.sh.head_dim == 128 ? launch_fast_hd<0, 128>(p, group, n_layers, s)
+                                : launch_fast_hd<0, 64>(p, group, n_layers, s);
+  }
+  if (used_fast) *used_fast = 0;
+  if (p.split_len > kGenericMaxSplit) return hipErrorInvalidValue;
+  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  hipLaunchKernelGGL(k_decode_generic, grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s) {
+  (void)kCombineMaxParts;
+  dim3 grid(p.sh.n_heads, p.n_seq, n_layers);
+  hipLaunchKernelGGL(k_combine, grid, dim3(kCombineThreads), 0, s, p, p.q_out);
+  return hipGetLastError();
+}
+
+}  // namespace g2b

@@ -1,0 +1,162 @@
+// g2b_device.h - device-side pieces shared by the gfx950 kernels.
+//
+// Everything here that produces KV bytes must be bit-exact with the
+// reference, so this code is compiled with -ffp-contract=off, IEEE division
+// (__fdiv_rn) and fp32 denormals preserved; explicit fmaf() is used only in
+// the attention arithmetic, where a tolerance applies.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g2b {
+
+constexpr float kNegBig = -1.0e30f;  // "no score yet": finite, so m - m == 0
+
+// Per-sequence descriptor as the kernels read it (32 bytes).
+struct SeqDev {
+  int32_t pos;      // new token position; positions 0..pos are attended
+  int32_t ctx_cap;  // layer stride in rows
+  int32_t pad0, pad1;
+  uint8_t *k;       // [n_layers][ctx_cap][row]
+  uint8_t *v;
+};
+
+// Shape as the kernels read it.
+struct ShapeDev {
+  int32_t n_layers, n_heads, n_kv_heads, head_dim;
+  int32_t arch_llama;  // 1: interleaved pairs, 0: NEOX halves
+  int32_t kv_q8;
+  int32_t rope_on;     // 0 when head_dim/2 > 512 (reference leaves x unrotated)
+  uint32_t row_bytes;
+};
+
+// Truncating fp32 -> fp16 of /root/reference/src/l3_math.c:6-16.
+__device__ __forceinline__ uint32_t f32_to_half_trunc(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const int32_t e8 = (int32_t)((u >> 23) & 0xffu);
+  if (e8 == 0xff) return sign | 0x7c00u;
+  const int32_t e5 = e8 - 112;
+  if (e5 <= 0) return sign;
+  if (e5 >= 31) return sign | 0x7c00u;
+  return sign | ((uint32_t)e5 << 10) | ((u & 0x7fffffu) >> 13);
+}
+
+// Exact fp16 -> fp32 of /root/reference/src/l2_codec.c:35-54, built from bits
+// (subnormals: m * 2^-24 is exact in fp32).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t e5 = (h >> 10) & 0x1fu;
+  const uint32_t m10 = h & 0x3ffu;
+  if (e5 == 0) {
+    const float f = (float)m10 * 5.9604644775390625e-8f;  // 2^-24
+    return __uint_as_float(__float_as_uint(f) | sign);
+  }
+  const uint32_t e8 = (e5 == 31) ? 0xffu : (e5 + 112u);
+  return __uint_as_float(sign | (e8 << 23) | (m10 << 13));
+}
+
+// (int32)lroundf(r) as glibc on x86-64 gives it: round half away from zero,
+// out-of-range and NaN produce LONG_MIN, whose low 32 bits are 0.
+__device__ __forceinline__ int32_t lround_i32_like_host(float r) {
+  if (!(fabsf(r) < 9.2233720368547758e18f)) return 0;
+  return (int32_t)(int64_t)roundf(r);
+}
+
+// One Q8_0 block (/root/reference/src/l5_model.c:49-59) of cnt <= 32 floats
+// to 34 bytes at dst (2-byte aligned), little-endian fp16 scale first.
+__device__ __forceinline__ void q8_quant_block(const float *x, int cnt, uint8_t *dst) {
+  float amax = 0.f;
+  for (int j = 0; j < cnt; j++) {
+    const float a = fabsf(x[j]);
+    if (a > amax) amax = a;
+  }
+  float d = __fdiv_rn(amax, 127.f);
+  if (!(d > 0.f)) d = 1e-10f;
+  uint16_t *out16 = reinterpret_cast<uint16_t *>(dst);
+  out16[0] = (uint16_t)f32_to_half_trunc(d);
+#pragma unroll
+  for (int j = 0; j < 32; j += 2) {
+    int32_t qa = 0, qb = 0;
+    if (j < cnt) {
+      qa = lround_i32_like_host(__fdiv_rn(x[j], d));
+      qa = qa > 127 ? 127 : (qa < -127 ? -127 : qa);
+    }
+    if (j + 1 < cnt) {
+      qb = lround_i32_like_host(__fdiv_rn(x[j + 1], d));
+      qb = qb > 127 ? 127 : (qb < -127 ? -127 : qb);
+    }
+    out16[1 + j / 2] = (uint16_t)((uint32_t)(qa & 0xff) | ((uint32_t)(qb & 0xff) << 8));
+  }
+}
+
+// RoPE pair rotation of /root/reference/src/l3_math.c:79 and :98-99:
+// a' = a*c - b*s, b' = a*s + b*c, each product rounded (no contraction).
+__device__ __forceinline__ void rope_pair(float &a, float &b, float c, float s) {
+  const float a0 = a, b0 = b;
+  a = a0 * c - b0 * s;
+  b = a0 * s + b0 * c;
+}
+
+// Indices of RoPE pair j inside a head: LLaMA (2j, 2j+1), NEOX (j, j+hd/2).
+__device__ __forceinline__ void rope_pair_index(int arch_llama, int j, int half, int &ia,
+                                                int &ib) {
+  ia = arch_llama ? 2 * j : j;
+  ib = arch_llama ? 2 * j + 1 : j + half;
+}
+
+// RoPE(k) [and RoPE(q) into qr when q != nullptr] at `pos`, then store the
+// k and v rows at (layer, pos): l5_model.c:513-516 for one sequence.  Called
+// by every thread of the block; kr is LDS scratch of nkv floats.
+__device__ inline void append_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
+                           const float *k, const float *v, const float *q, float *qr,
+                           const float *rope, float *kr) {
+  const int hd = sh.head_dim, half = hd / 2;
+  const int nkv = sh.n_kv_heads * hd;
+  const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
+
+  for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
+  __syncthreads();
+  if (cs) {
+    for (int p = threadIdx.x; p < sh.n_kv_heads * half; p += blockDim.x) {
+      const int h = p / half, j = p - h * half;
+      int ia, ib;
+      rope_pair_index(sh.arch_llama, j, half, ia, ib);
+      rope_pair(kr[h * hd + ia], kr[h * hd + ib], cs[2 * j], cs[2 * j + 1]);
+    }
+  }
+  if (q) {
+    for (int p = threadIdx.x; p < sh.n_heads * half; p += blockDim.x) {
+      const int h = p / half, j = p - h * half;
+      int ia, ib;
+      rope_pair_index(sh.arch_llama, j, half, ia, ib);
+      float a = q[h * hd + ia], b = q[h * hd + ib];
+      if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+      qr[h * hd + ia] = a;
+      qr[h * hd + ib] = b;
+    }
+  }
+  __syncthreads();
+
+  const size_t off = ((size_t)layer * (size_t)sd.ctx_cap + (size_t)pos) * sh.row_bytes;
+  if (!sh.kv_q8) {
+    float *kd = reinterpret_cast<float *>(sd.k + off);
+    float *vd = reinterpret_cast<float *>(sd.v + off);
+    for (int e = threadIdx.x; e < nkv; e += blockDim.x) {
+      kd[e] = kr[e];
+      vd[e] = v[e];
+    }
+    return;
+  }
+  const int nb = (nkv + 31) / 32;
+  for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
+    const bool is_k = b < nb;
+    const int bb = is_k ? b : b - nb;
+    const int cnt = min(32, nkv - 32 * bb);
+    const float *src = is_k ? kr + 32 * bb : v + 32 * bb;
+    uint8_t *dst = (is_k ? sd.k : sd.v) + off + 34 * (size_t)bb;
+    q8_quant_block(src, cnt, dst);
+  }
+}
+
+}  // namespace g2b

@@ -1,0 +1,72 @@
+// g2b_internal.h - parameter blocks and launchers shared between the C ABI
+// (g2b_api.hip) and the kernel translation units.  Not installed.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "g2b_device.h"
+
+namespace g2b {
+
+// Partial state of one wave of one split for one q head:
+// [m, l, 0, 0, acc[head_dim]] in the log2 domain (m = running max of the
+// scaled scores, l = sum of exp2(score - m), acc = sum of exp2(score - m)*v).
+constexpr int kPartHead = 4;
+constexpr int kWavesPerSplit = 4;      // one partial per wave of a 256-thread split
+constexpr int kThreads = 256;
+constexpr int kGenericMaxSplit = 1024; // positions per split in the generic kernel
+
+
+struct AppendParams {
+  ShapeDev sh;
+  const SeqDev *seqs;  // nullptr: use `one`
+  SeqDev one;
+  int32_t n_seq, layer0;
+  const float *q_in;   // [L][n_seq][nq] (nullptr in row-prefill mode)
+  float *q_rot;        // [L][n_seq][nq]
+  const float *k_in;   // [L][n_seq][nkv]  or [n_rows][nkv] in row-prefill mode
+  const float *v_in;
+  const float *rope;   // [rope_len][head_dim] cos/sin pairs, or nullptr
+  int32_t pos0;        // row-prefill mode: first position
+};
+
+struct DecodeParams {
+  ShapeDev sh;
+  const SeqDev *seqs;
+  SeqDev one;
+  int32_t n_seq, layer0;
+  int32_t split_len, max_splits;
+  const float *q_rot;  // [L][n_seq][nq]
+  float *q_out;        // [L][n_seq][nq]: the output overwrites q
+  float *part;         // [L][n_seq][n_heads][max_splits*kWavesPerSplit][kPartHead+hd]
+  float *att;          // nullable: [L][n_seq][n_heads][att_stride]
+  int32_t att_stride;
+  float qscale;        // (1/sqrtf(hd)) * log2(e)
+};
+
+// Launchers: return hipSuccess or the launch error.
+hipError_t launch_append_batch(const AppendParams &p, int n_layers, hipStream_t s);
+hipError_t launch_append_rows(const AppendParams &p, int layer, int n_rows, hipStream_t s);
+// Picks the specialised kernel for the shape when there is one, else the generic one.
+// Returns hipErrorInvalidValue when split_len is too large for the generic kernel.
+hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int *used_fast);
+hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
+// Whether a specialised decode kernel exists for this shape.
+bool decode_fast_available(const ShapeDev &sh);
+
+// Synthetic fill (bench / full-size tests): see g2b_synth.h.
+struct SynthParams {
+  ShapeDev sh;
+  uint8_t *k, *v;
+  int32_t ctx_cap, layer0, pos0, n_pos;
+  uint64_t base_seed;
+  int32_t seq;
+  float sel_threshold;  // scale a K row x8 when its selector draw exceeds this
+  const float *rope;
+};
+hipError_t launch_synth_fill(const SynthParams &p, int n_layers, hipStream_t s);
+hipError_t launch_synth_normal(float *out, uint64_t n, uint64_t seed, hipStream_t s);
+hipError_t launch_copy16(void *dst, const void *src, uint64_t n16, hipStream_t s);
+
+}  // namespace g2b

@@ -1,0 +1,56 @@
+/*
+ * g2b_synth.h - seeded synthetic inputs generated on the device.
+ *
+ * These entry points have NO counterpart in the reference: they exist for
+ * benchmarks and full-size tests, which need tens of gigabytes of KV that
+ * cannot be produced on the host.  They write into caches allocated with
+ * g2b_kv_alloc and go through the same RoPE + append arithmetic as
+ * g2b_kv_append_rows.
+ *
+ * Streams: the stream (seq, layer, tensor) has seed
+ * g2b_stream_seed(base, seq, layer, tensor); element i of a stream is the
+ * i-th float of SplitMix64 -> Box-Muller (double) -> float, pair (2j, 2j+1)
+ * taken from generator outputs 2j+1 and 2j+2 as (r*cos, r*sin).  Tensors:
+ * 0 = K prefill rows, 1 = V prefill rows, 5 = K row-scale selector.
+ * K/V row t uses elements [t*nkv, (t+1)*nkv) of its stream, pre-RoPE.
+ */
+#ifndef G2B_SYNTH_H
+#define G2B_SYNTH_H
+#include <stdint.h>
+
+#include "g2b_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { G2B_STREAM_K = 0, G2B_STREAM_V = 1, G2B_STREAM_SEL = 5 };
+
+uint64_t g2b_stream_seed(uint64_t base, int32_t seq, int32_t layer, int32_t tensor);
+
+/* n floats of stream `seed` into device memory `out`. */
+int g2b_synth_normal(g2b_ctx *ctx, float *out, uint64_t n, uint64_t seed);
+
+/* Fill rows [pos0, pos0+n_pos) of layers [layer0, layer0+n_layers) of one
+ * sequence (`seq` picks its streams): draw k and v, scale a K row by 8 when
+ * its selector draw exceeds sel_threshold (pass +INFINITY for none), RoPE k
+ * at its position, store (F32) or quantise (Q8_0) both rows.  Asynchronous. */
+int g2b_synth_fill_kv(g2b_ctx *ctx, void *kcache, void *vcache, int32_t ctx_cap,
+                      int32_t layer0, int32_t n_layers, int32_t pos0, int32_t n_pos,
+                      uint64_t base_seed, int32_t seq, float sel_threshold);
+
+/* Plain device copy of nbytes (multiple of 16, 16-byte aligned pointers):
+ * the known-size reference kernel used to scale HBM byte counters. */
+int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
+
+/* Kernel timing with HIP events on the context's stream: while enabled,
+ * every decode-kernel launch is bracketed by two events.  _read waits for
+ * them, returns the summed milliseconds and the number of launches since
+ * the last read, and starts a new window. */
+int g2b_ctx_profile(g2b_ctx *ctx, int32_t enable);
+int g2b_ctx_profile_read(g2b_ctx *ctx, double *decode_ms, int64_t *launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

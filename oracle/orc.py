@@ -1,0 +1,314 @@
+"""ctypes wrapper for the CPU oracle (oracle/liborc.so) and, where it was
+built, the compiled reference (oracle/_ref/libg2bref_*.so).
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of bench.py may import this module, and only as the
+checker or the timed CPU baseline; the product path never does.
+
+The C functions restate /root/reference/src/l5_model.c:47-67,232-265,448-452,
+513-578, src/l3_math.c:6-16,52-56,64-102 and src/l2_codec.c:35-54 (see
+oracle/orc.h for the per-function citations and how each one is pinned).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBORC = os.path.join(HERE, "liborc.so")
+REF_DIR = os.path.join(HERE, "_ref")
+
+ARCH_LLAMA, ARCH_QWEN2, ARCH_QWEN3 = 0, 1, 2
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+
+
+class OrcShape(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int32),
+        ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("rope_theta", C.c_float),
+        ("arch", C.c_int32),
+        ("kv_q8", C.c_int32),
+    ]
+
+
+@dataclass(frozen=True)
+class Shape:
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    rope_theta: float
+    arch: int
+    kv_q8: bool
+
+    @property
+    def nq(self) -> int:
+        return self.n_heads * self.head_dim
+
+    @property
+    def nkv(self) -> int:
+        return self.n_kv_heads * self.head_dim
+
+    @property
+    def row_bytes(self) -> int:
+        return q8_rowsize(self.nkv) if self.kv_q8 else self.nkv * 4
+
+    def c(self) -> OrcShape:
+        return OrcShape(self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
+                        self.rope_theta, self.arch, 1 if self.kv_q8 else 0)
+
+
+def q8_rowsize(nkv: int) -> int:
+    return (nkv + 31) // 32 * 34
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load liborc.so (built by ``make -C oracle``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIBORC):
+            raise RuntimeError(f"{LIBORC} missing: run `make -C oracle`")
+        L = C.CDLL(LIBORC)
+        L.orc_splitmix64.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_splitmix64.restype = C.c_uint64
+        L.orc_normal_f32.argtypes = [C.POINTER(C.c_uint64), _f32p, C.c_size_t]
+        L.orc_f32_to_half_n.argtypes = [_f32p, _u16p, C.c_size_t]
+        L.orc_half_to_float_n.argtypes = [_u16p, _f32p, C.c_size_t]
+        L.orc_q8_quant_row.argtypes = [_f32p, _u8p, C.c_int32]
+        L.orc_q8_dequant_row.argtypes = [_u8p, _f32p, C.c_int32]
+        L.orc_rope_table.argtypes = [C.c_int32, C.c_int32, C.c_float, _f32p]
+        L.orc_rope_table.restype = C.c_int
+        L.orc_rope.argtypes = [C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float]
+        L.orc_softmax.argtypes = [_f32p, C.c_int32]
+        L.orc_kv_prefill.argtypes = [C.POINTER(OrcShape), C.c_int32, C.c_int32, C.c_int32,
+                                     C.c_int32, _u8p, _u8p, _f32p, _f32p]
+        L.orc_attn_layer.argtypes = [C.POINTER(OrcShape), C.c_int32, C.c_int32, C.c_int32,
+                                     _u8p, _u8p, _f32p, _f32p, _f32p, _f32p, C.c_int]
+        L.orc_attn_layer.restype = C.c_int
+        L.orc_attn_batch.argtypes = [C.POINTER(OrcShape), C.c_int32, C.c_int32, C.c_int32,
+                                     _i32p, _i32p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                     _f32p, _f32p, _f32p, C.c_int]
+        L.orc_attn_batch.restype = C.c_int
+        L.orc_now_sec.restype = C.c_double
+        L.orc_max_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+# ---------------------------------------------------------------- RNG
+
+def normal(seed: int, n: int) -> np.ndarray:
+    """n float32 N(0,1) values of the SplitMix64/Box-Muller stream ``seed``."""
+    st = C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF)
+    out = np.empty(n, np.float32)
+    if n:
+        lib().orc_normal_f32(C.byref(st), out, n)
+    return out
+
+
+def stream_seed(base: int, seq: int, layer: int, tensor: int) -> int:
+    """Seed of the synthetic stream for (sequence, layer, tensor).
+
+    tensor: 0 = K prefill rows, 1 = V prefill rows, 2 = new q, 3 = new k,
+    4 = new v, 5 = row-scale selector.  Same formula as the device fill.
+    """
+    m = 0xFFFFFFFFFFFFFFFF
+
+    def mix(z):
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+        return z ^ (z >> 31)
+
+    z = mix((base ^ (tensor * 0xD1B54A32D192ED03)) & m)
+    z = mix((z + (seq + 1) * 0x9E3779B97F4A7C15) & m)
+    return mix((z + (layer + 1) * 0xC2B2AE3D27D4EB4F) & m)
+
+
+# ---------------------------------------------------------------- codec
+
+def f32_to_half(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(x.size, np.uint16)
+    lib().orc_f32_to_half_n(x, out, x.size)
+    return out
+
+
+def half_to_float(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, np.uint16).ravel()
+    out = np.empty(h.size, np.float32)
+    lib().orc_half_to_float_n(h, out, h.size)
+    return out
+
+
+def q8_quant_row(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.zeros(q8_rowsize(x.size), np.uint8)
+    lib().orc_q8_quant_row(x, out, x.size)
+    return out
+
+
+def q8_dequant_row(b: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(b, np.uint8).ravel()
+    assert b.size >= q8_rowsize(n)
+    out = np.empty(n, np.float32)
+    lib().orc_q8_dequant_row(b, out, n)
+    return out
+
+
+def rope_table(pos: int, head_dim: int, theta: float) -> np.ndarray:
+    cs = np.zeros(max(head_dim, 2), np.float32)
+    rc = lib().orc_rope_table(pos, head_dim, theta, cs)
+    if rc:
+        raise ValueError("head_dim/2 > 512")
+    return cs[:head_dim]
+
+
+def rope(arch: int, x: np.ndarray, pos: int, head_dim: int, theta: float) -> np.ndarray:
+    y = np.ascontiguousarray(x, np.float32).copy().ravel()
+    lib().orc_rope(arch, y, y.size, pos, head_dim, theta)
+    return y
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(x, np.float32).copy().ravel()
+    lib().orc_softmax(y, y.size)
+    return y
+
+
+# ---------------------------------------------------------------- KV + attention
+
+def alloc_kv(shape: Shape, ctx_cap: int):
+    n = shape.n_layers * ctx_cap * shape.row_bytes
+    return np.zeros(n, np.uint8), np.zeros(n, np.uint8)
+
+
+def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
+    return (layer * ctx_cap + pos) * shape.row_bytes
+
+
+def kv_prefill(shape: Shape, ctx_cap: int, layer: int, pos0: int, kc: np.ndarray,
+               vc: np.ndarray, k_rows: np.ndarray, v_rows: np.ndarray):
+    """RoPE + append rows [pos0, pos0+n) of one layer into kc/vc in place."""
+    k_rows = np.ascontiguousarray(k_rows, np.float32)
+    v_rows = np.ascontiguousarray(v_rows, np.float32)
+    n = int(k_rows.shape[0]) if k_rows.ndim > 1 else 0
+    if n:
+        lib().orc_kv_prefill(C.byref(shape.c()), ctx_cap, layer, pos0, n, kc, vc,
+                             k_rows.reshape(-1), v_rows.reshape(-1))
+
+
+def attn_layer(shape: Shape, ctx_cap: int, layer: int, pos: int, kc: np.ndarray,
+               vc: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray,
+               avx2_order: bool = True):
+    """One layer (RoPE, append into kc/vc in place, attention).
+
+    Returns (out [nq], att [n_heads, pos+1]) or raises on a bad pos."""
+    qo = np.ascontiguousarray(q, np.float32).copy().ravel()
+    att = np.zeros(shape.n_heads * ctx_cap, np.float32)
+    rc = lib().orc_attn_layer(C.byref(shape.c()), ctx_cap, layer, pos, kc, vc, qo,
+                              np.ascontiguousarray(k, np.float32).ravel(),
+                              np.ascontiguousarray(v, np.float32).ravel(), att,
+                              1 if avx2_order else 0)
+    if rc:
+        raise ValueError(f"orc_attn_layer rc={rc} (pos={pos}, ctx_cap={ctx_cap})")
+    return qo, att.reshape(shape.n_heads, ctx_cap)[:, : pos + 1].copy()
+
+
+def attn_batch(shape: Shape, layer0: int, n_layers: int, pos: np.ndarray,
+               ctx_cap: np.ndarray, kcs, vcs, q: np.ndarray, k: np.ndarray,
+               v: np.ndarray, n_threads: int = 1) -> np.ndarray:
+    """The CPU baseline: q/k/v are [n_layers][n_seq][...]; returns outputs."""
+    n_seq = len(kcs)
+    kp = (C.c_void_p * n_seq)(*[a.ctypes.data for a in kcs])
+    vp = (C.c_void_p * n_seq)(*[a.ctypes.data for a in vcs])
+    qo = np.ascontiguousarray(q, np.float32).copy()
+    rc = lib().orc_attn_batch(C.byref(shape.c()), layer0, n_layers, n_seq,
+                              np.ascontiguousarray(pos, np.int32),
+                              np.ascontiguousarray(ctx_cap, np.int32), kp, vp,
+                              qo.reshape(-1), np.ascontiguousarray(k, np.float32).reshape(-1),
+                              np.ascontiguousarray(v, np.float32).reshape(-1), n_threads)
+    if rc:
+        raise RuntimeError(f"orc_attn_batch: {rc} failures")
+    return qo
+
+
+def now() -> float:
+    return lib().orc_now_sec()
+
+
+def max_threads() -> int:
+    return lib().orc_max_threads()
+
+
+# ---------------------------------------------------------------- compiled reference
+
+_ref = {}
+
+
+def ref_lib(variant: str = "avx2"):
+    """The compiled reference driver, or None where it was not built."""
+    if variant in _ref:
+        return _ref[variant]
+    path = os.path.join(REF_DIR, f"libg2bref_{variant}.so")
+    if not os.path.exists(path):
+        _ref[variant] = None
+        return None
+    L = C.CDLL(path)
+    L.ref_q8_quant_row.argtypes = [_f32p, _u8p, C.c_int32]
+    L.ref_q8_dequant_row.argtypes = [_u8p, _f32p, C.c_int32]
+    L.ref_f32_to_half_n.argtypes = [_f32p, _u16p, C.c_size_t]
+    L.ref_half_to_float_n.argtypes = [_u16p, _f32p, C.c_size_t]
+    L.ref_softmax.argtypes = [_f32p, C.c_int32]
+    L.ref_rope.argtypes = [C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float]
+    L.ref_forward_case.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                   C.c_int32, C.c_int32, C.c_int32,
+                                   C.c_int32, _f32p, _f32p, C.c_int32, _f32p,
+                                   _f32p, _f32p, _f32p, _u8p, _u8p]
+    L.ref_forward_case.restype = C.c_int
+    _ref[variant] = L
+    return L
+
+
+def ref_forward_case(shape: Shape, ctx_cap: int, k_pre: np.ndarray, v_pre: np.ndarray,
+                     x_rows: np.ndarray, variant: str = "avx2"):
+    """Run the reference model_forward on a selector model (oracle/ref_driver.c).
+
+    Returns dict(xb [n_fwd, dim], out [n_fwd, nq], att [n_heads, ctx_cap],
+    kc, vc [n_layers*ctx_cap*row])."""
+    L = ref_lib(variant)
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    nq, nkv = shape.nq, shape.nkv
+    dim = nq + 2 * nkv
+    n_pre = 0 if k_pre is None else int(k_pre.shape[0])
+    n_fwd = int(x_rows.shape[0])
+    kp = np.ascontiguousarray(k_pre if n_pre else np.zeros((1, nkv)), np.float32)
+    vp = np.ascontiguousarray(v_pre if n_pre else np.zeros((1, nkv)), np.float32)
+    xr = np.ascontiguousarray(x_rows, np.float32)
+    assert xr.shape[1] == dim
+    xb = np.zeros((n_fwd, dim), np.float32)
+    out = np.zeros((n_fwd, nq), np.float32)
+    att = np.zeros((shape.n_heads, ctx_cap), np.float32)
+    nbytes = shape.n_layers * ctx_cap * shape.row_bytes
+    kc = np.zeros(nbytes, np.uint8)
+    vc = np.zeros(nbytes, np.uint8)
+    rc = L.ref_forward_case(shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
+                            shape.rope_theta, shape.arch, 1 if shape.kv_q8 else 0, ctx_cap,
+                            n_pre, kp.reshape(-1), vp.reshape(-1), n_fwd, xr.reshape(-1),
+                            xb.reshape(-1), out.reshape(-1), att.reshape(-1), kc, vc)
+    if rc:
+        raise RuntimeError(f"ref_forward_case rc={rc}")
+    return dict(xb=xb, out=out, att=att, kc=kc, vc=vc)

@@ -1,0 +1,159 @@
+/*
+ * ref_driver.c - drives the COMPILED REFERENCE for golden vectors.
+ * TEST INFRASTRUCTURE ONLY.  Built by oracle/Makefile (target `ref`) into
+ * oracle/_ref/ from the reference sources where they lie under
+ * /root/reference; nothing of the reference is copied into this repository.
+ * The reference's path lives in static helpers and inline in model_forward,
+ * so this translation unit includes src/l5_model.c to reach them.
+ *
+ * ref_forward_case() builds an in-memory one-or-more-layer model whose
+ * weights make model_forward run exactly the decode-attention path on chosen
+ * inputs:
+ *   - dim = nq + 2*nkv, token embeddings are the caller's rows (F32);
+ *   - attn_norm = 1, so xb = rmsnorm(x) (returned to the caller: it is the
+ *     q|k|v the reference actually uses);
+ *   - Wq/Wk/Wv are F32 0/1 selector matrices, so q, k, v are exact slices of
+ *     xb (the F32 GEMV of l3_math.c:17-20 adds exact zeros);
+ *   - Wo and the FFN are zero, so every layer sees the same xb.
+ * Positions [0, n_pre) are prefilled with the reference's own apply_rope and
+ * kv_store; positions [n_pre, n_pre+n_fwd) go through model_forward.
+ */
+#include "l5_model.c"
+
+void ref_q8_quant_row(const f32 *src, u8 *dst, i32 n) { q8_quant_row(src, dst, n); }
+void ref_q8_dequant_row(const u8 *src, f32 *out, i32 n) { q8_dequant_row(src, out, n); }
+u16 ref_f32_to_half(f32 f) { return f32_to_half(f); }
+f32 ref_half_to_float(u16 h) { return half_to_float(h); }
+void ref_f32_to_half_n(const f32 *x, u16 *out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] = f32_to_half(x[i]);
+}
+void ref_half_to_float_n(const u16 *h, f32 *out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] = half_to_float(h[i]);
+}
+void ref_softmax(f32 *x, i32 n) { softmax(x, n); }
+void ref_rope(i32 arch, f32 *x, i32 len, i32 pos, i32 hd, f32 theta) {
+  Model m;
+  memset(&m, 0, sizeof m);
+  m.arch = (u8)arch;
+  apply_rope(&m, x, len, pos, hd, theta);
+}
+
+static void put_slot(Slot *sl, u32 *ns, u64 *cur, u8 role, u16 layer, u64 nfloats) {
+  Slot *s = &sl[*ns];
+  s->role = role;
+  s->layer = layer;
+  s->type = T_F32;
+  s->nbytes = (u32)(nfloats * 4u);
+  s->off = *cur;
+  *cur = ALIGN64(*cur + nfloats * 4u);
+  (*ns)++;
+}
+
+int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f32 theta,
+                     i32 arch, i32 kv_q8, i32 ctx_cap,
+                     i32 n_pre, const f32 *k_pre, const f32 *v_pre,
+                     i32 n_fwd, const f32 *x_rows,
+                     f32 *xb_out, f32 *out_per_step, f32 *att_out,
+                     u8 *kc_out, u8 *vc_out) {
+  const i32 hd = head_dim, nq = n_heads * hd, nkv = n_kv_heads * hd;
+  const i32 dim = nq + 2 * nkv, hid = 32, vocab = n_fwd > 0 ? n_fwd : 1;
+  Model m;
+  memset(&m, 0, sizeof m);
+  m.fd = -1;
+  m.swap_fd = -1;
+  m.c.dim = dim;
+  m.c.hidden_dim = hid;
+  m.c.n_layers = n_layers;
+  m.c.n_heads = n_heads;
+  m.c.n_kv_heads = n_kv_heads;
+  m.c.vocab = vocab;
+  m.c.seq_len = ctx_cap;
+  m.c.head_dim = hd;
+  m.c.eps = 1e-6f;
+  m.c.rope_theta = theta;
+  m.arch = (u8)arch;
+  m.flags = kv_q8 ? F_KV_Q8 : 0;
+
+  u32 max_slots = 2 + (u32)n_layers * 9u;
+  Slot *sl = calloc(max_slots, sizeof(Slot));
+  u32 ns = 0;
+  u64 cur = 0;
+  put_slot(sl, &ns, &cur, R_TOK_EMBD, 0xFFFF, (u64)vocab * dim);
+  put_slot(sl, &ns, &cur, R_OUT_NORM, 0xFFFF, (u64)dim);
+  for (i32 L = 0; L < n_layers; L++) {
+    put_slot(sl, &ns, &cur, R_ATTN_NORM, (u16)L, (u64)dim);
+    put_slot(sl, &ns, &cur, R_ATTN_Q, (u16)L, (u64)nq * dim);
+    put_slot(sl, &ns, &cur, R_ATTN_K, (u16)L, (u64)nkv * dim);
+    put_slot(sl, &ns, &cur, R_ATTN_V, (u16)L, (u64)nkv * dim);
+    put_slot(sl, &ns, &cur, R_ATTN_O, (u16)L, (u64)dim * nq);
+    put_slot(sl, &ns, &cur, R_FFN_NORM, (u16)L, (u64)dim);
+    put_slot(sl, &ns, &cur, R_FFN_GATE, (u16)L, (u64)hid * dim);
+    put_slot(sl, &ns, &cur, R_FFN_UP, (u16)L, (u64)hid * dim);
+    put_slot(sl, &ns, &cur, R_FFN_DOWN, (u16)L, (u64)dim * hid);
+  }
+  u8 *blob = calloc(1, (size_t)cur + 64);
+  if (!sl || !blob) { free(sl); free(blob); return -1; }
+  m.slots = sl;
+  m.n_slots = ns;
+  m.data = blob;
+  m.data_size = (size_t)cur;
+  m.own_data = 0;
+
+  for (u32 i = 0; i < ns; i++) {
+    f32 *w = (f32 *)(blob + sl[i].off);
+    u64 nf = sl[i].nbytes / 4u;
+    switch (sl[i].role) {
+      case R_TOK_EMBD:
+        if (n_fwd > 0) memcpy(w, x_rows, (size_t)n_fwd * dim * 4u);
+        break;
+      case R_OUT_NORM: case R_ATTN_NORM: case R_FFN_NORM:
+        for (u64 j = 0; j < nf; j++) w[j] = 1.f;
+        break;
+      case R_ATTN_Q:
+        for (i32 r = 0; r < nq; r++) w[(size_t)r * dim + r] = 1.f;
+        break;
+      case R_ATTN_K:
+        for (i32 r = 0; r < nkv; r++) w[(size_t)r * dim + nq + r] = 1.f;
+        break;
+      case R_ATTN_V:
+        for (i32 r = 0; r < nkv; r++) w[(size_t)r * dim + nq + nkv + r] = 1.f;
+        break;
+      default:
+        break; /* Wo and FFN stay zero */
+    }
+  }
+  build_index(&m);
+  if (model_set_ctx(&m, ctx_cap)) { free(blob); model_free(&m); return -2; }
+  size_t half_bytes = kv_q8 ? (size_t)n_layers * ctx_cap * kv_q8_rowsize(nkv)
+                            : (size_t)n_layers * ctx_cap * (size_t)nkv * 4u;
+  if (kv_q8) { memset(m.kcq, 0, half_bytes); memset(m.vcq, 0, half_bytes); }
+  else { memset(m.kcache, 0, half_bytes); memset(m.vcache, 0, half_bytes); }
+
+  f32 *tmp = malloc((size_t)nkv * 4u);
+  for (i32 t = 0; t < n_pre; t++)
+    for (i32 L = 0; L < n_layers; L++) {
+      memcpy(tmp, k_pre + (size_t)t * nkv, (size_t)nkv * 4u);
+      apply_rope(&m, tmp, nkv, t, hd, theta);
+      kv_store(&m, L, t, tmp, v_pre + (size_t)t * nkv);
+    }
+  free(tmp);
+
+  f32 *ones = malloc((size_t)dim * 4u);
+  f32 *logits = malloc((size_t)vocab * 4u);
+  for (i32 j = 0; j < dim; j++) ones[j] = 1.f;
+  f32 *qbuf = m.buf + 3 * dim + 2 * hid; /* q region, see model_forward :485-486 */
+  for (i32 i = 0; i < n_fwd; i++) {
+    rmsnorm(xb_out + (size_t)i * dim, (f32 *)(x_rows + (size_t)i * dim), ones, dim, m.c.eps);
+    model_forward(&m, i, n_pre + i, logits);
+    memcpy(out_per_step + (size_t)i * nq, qbuf, (size_t)nq * 4u);
+  }
+  if (n_fwd > 0 && att_out)
+    memcpy(att_out, qbuf + nq + 2 * nkv, (size_t)n_heads * ctx_cap * 4u);
+  if (kc_out) memcpy(kc_out, kv_q8 ? (void *)m.kcq : (void *)m.kcache, half_bytes);
+  if (vc_out) memcpy(vc_out, kv_q8 ? (void *)m.vcq : (void *)m.vcache, half_bytes);
+  free(ones);
+  free(logits);
+  model_free(&m);
+  free(blob);
+  return 0;
+}

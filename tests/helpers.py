@@ -1,0 +1,116 @@
+"""Shared test helpers: golden fixtures, seeded inputs, oracle runs and
+device runs of the same case."""
+from __future__ import annotations
+
+import hashlib
+import os
+from statistics import NormalDist
+
+import numpy as np
+
+from oracle import orc
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def load_golden(name: str) -> dict:
+    with np.load(os.path.join(GOLDEN, name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def fwd_cases():
+    return sorted(f for f in os.listdir(GOLDEN) if f.startswith("fwd_") and f.endswith(".npz"))
+
+
+def golden_shape(d: dict) -> orc.Shape:
+    L, nh, nkv, hd, arch, q8 = [int(x) for x in d["shape"]]
+    return orc.Shape(L, nh, nkv, hd, float(d["theta"]), arch, bool(q8))
+
+
+def case_inputs(shape: orc.Shape, n_pre: int, n_fwd: int, seed: int, p_scale: float):
+    """Seeded inputs of a forward case: pre-RoPE k/v prefill rows and x rows.
+
+    A prefill K row is scaled x8 when its own N(0,1) selector draw exceeds
+    the (1 - p_scale) quantile."""
+    nkv = shape.nkv
+    dim = shape.nq + 2 * nkv
+    kp = orc.normal(seed * 16 + 0, n_pre * nkv).reshape(n_pre, nkv)
+    vp = orc.normal(seed * 16 + 1, n_pre * nkv).reshape(n_pre, nkv)
+    if p_scale > 0 and n_pre:
+        thr = float(NormalDist().inv_cdf(1.0 - p_scale))
+        sel = orc.normal(seed * 16 + 3, n_pre)
+        kp[sel > thr] *= np.float32(8.0)
+    xr = orc.normal(seed * 16 + 2, n_fwd * dim).reshape(n_fwd, dim)
+    return kp, vp, xr
+
+
+def golden_inputs(d: dict):
+    shape = golden_shape(d)
+    kp, vp, xr = case_inputs(shape, int(d["n_pre"]), int(d["n_fwd"]), int(d["seed"]),
+                             float(d["p_scale"]))
+    assert d["inputs_sha"].item().decode() == sha(kp) + sha(vp) + sha(xr), "RNG drift"
+    return shape, kp, vp
+
+
+def split_xb(shape: orc.Shape, xb: np.ndarray):
+    nq, nkv = shape.nq, shape.nkv
+    return xb[:nq], xb[nq:nq + nkv], xb[nq + nkv:nq + 2 * nkv]
+
+
+def oracle_run_case(d: dict):
+    """The oracle on a golden case: prefill, then every forward step on every
+    layer (all layers see the same q/k/v, as in the reference selector model).
+    Returns (outs [n_fwd, nq], att of the last step [n_heads, pos+1], kc, vc)."""
+    shape, kp, vp = golden_inputs(d)
+    ctx_cap, n_pre = int(d["ctx_cap"]), int(d["n_pre"])
+    avx2 = d["variant"].item().decode() == "avx2"
+    kc, vc = orc.alloc_kv(shape, ctx_cap)
+    for L in range(shape.n_layers):
+        orc.kv_prefill(shape, ctx_cap, L, 0, kc, vc, kp, vp)
+    outs, att = [], None
+    for i, xb in enumerate(d["xb"]):
+        q, k, v = split_xb(shape, xb)
+        for L in range(shape.n_layers):
+            o, att = orc.attn_layer(shape, ctx_cap, L, n_pre + i, kc, vc, q, k, v, avx2)
+        outs.append(o)
+    return np.array(outs), att, kc, vc
+
+
+def kv_rows(shape: orc.Shape, buf: np.ndarray, ctx_cap: int, n_rows: int) -> np.ndarray:
+    return buf.reshape(shape.n_layers, ctx_cap, shape.row_bytes)[:, :n_rows]
+
+
+def bits(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def q8_special_rows() -> np.ndarray:
+    """Rows of 64 floats whose blocks exercise every branch of q8_quant_row."""
+    rows = []
+    z = np.zeros(64, np.float32)
+    rows.append(z.copy())                                  # zero blocks: d -> 1e-10
+    r = z.copy(); r[0] = 127.0; r[1:32] = np.arange(31) - 15 + 0.5   # d = 1: exact .5 ties
+    r[32] = -127.0; r[33:64] = -(np.arange(31) - 15 + 0.5)
+    rows.append(r)
+    r = z.copy(); r[:32] = np.linspace(-0.007, 0.007, 32); r[32:] = 1e-6   # amax < 2^-14*127
+    rows.append(r)
+    r = z.copy(); r[:32] = np.float32(5e-39); r[40] = np.float32(1e-45)    # subnormal inputs
+    rows.append(r)
+    r = np.linspace(-3, 3, 64).astype(np.float32); r[5] = np.nan             # NaN skipped by '>'
+    rows.append(r)
+    r = np.linspace(-3, 3, 64).astype(np.float32); r[7] = np.inf; r[40] = -np.inf
+    rows.append(r)
+    r = np.linspace(-1, 1, 64).astype(np.float32) * np.float32(1e30)        # fp16 scale overflow
+    rows.append(r)
+    r = np.full(64, -0.0, np.float32); r[63] = 1e-3                          # negative zeros
+    rows.append(r)
+    r = np.linspace(-65504 * 127, 65504 * 127, 64).astype(np.float32)      # near fp16 max scale
+    rows.append(r)
+    rng = np.random.default_rng(7)
+    for s in (1e-4, 1e-2, 1.0, 8.0, 300.0):
+        rows.append((rng.standard_normal(64) * s).astype(np.float32))
+    return np.stack(rows).astype(np.float32)
