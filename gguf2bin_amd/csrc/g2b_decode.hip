@@ -291,22 +291,25 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
     }
   }
 
-  // Fold the PPW position slots of the wave into slot 0.
+  // Fold the PPW position slots of the wave into slot 0.  Every lane takes
+  // part in the shuffles, but only slot-0 lanes update their state, so the
+  // state read from slot k is always slot k's own.
+  const bool gather = slot == 0;
   for (int k = 1; k < PPW; k++) {
-    const int src = lane + k * LPP;
+    const int src = (lane + k * LPP) & 63;
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      const float m2 = __shfl(m[i], src & 63);
-      const float l2 = __shfl(l[i], src & 63);
+      const float m2 = __shfl(m[i], src);
+      const float l2 = __shfl(l[i], src);
       const float M = fmaxf(m[i], m2);
       const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
-      l[i] = l[i] * f1 + l2 * f2;
+      l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
 #pragma unroll
       for (int j = 0; j < CD; j++) {
-        const float a2 = __shfl(acc[i][j], src & 63);
-        acc[i][j] = acc[i][j] * f1 + a2 * f2;
+        const float a2 = __shfl(acc[i][j], src);
+        acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
       }
-      m[i] = M;
+      m[i] = gather ? M : m[i];
     }
   }
   if (slot == 0) {
@@ -431,21 +434,27 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
   const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
   const float *base =
       P.part + (sidx * nh + h) * (size_t)P.max_splits * kWavesPerSplit * pstr;
+  // The merge over up to 2048 partials is accumulated in float64: a serial
+  // fp32 sum of that many terms drifts by ~1e-5 relative once one partial
+  // dominates.  This kernel moves a few KB per head, so the cost is nil.
   float M = kNegBig;
   for (int p = 0; p < np; p++) M = fmaxf(M, base[p * pstr]);
   for (int p = threadIdx.x; p < np; p += blockDim.x) w[p] = exp2f(base[p * pstr] - M);
   __syncthreads();
-  float L = 0.f;
-  for (int p = 0; p < np; p++) L = fmaf(base[p * pstr + 1], w[p], L);
+  double L = 0.0;
+  for (int p = 0; p < np; p++) L = fma((double)base[p * pstr + 1], (double)w[p], L);
   float *out = q_out + sidx * (size_t)(nh * HD) + (size_t)h * HD;
   for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-    float o = 0.f;
-    for (int p = 0; p < np; p++) o = fmaf(base[p * pstr + kPartHead + d], w[p], o);
-    out[d] = o / L;
+    double o = 0.0;
+    for (int p = 0; p < np; p++) o = fma((double)base[p * pstr + kPartHead + d], (double)w[p], o);
+    out[d] = (float)(o / L);
   }
   if (P.att) {
+    // weights of the scores this kernel used, normalised without an fp32
+    // rounding of (score - max)
     float *a = P.att + (sidx * nh + h) * (size_t)P.att_stride;
-    for (int t = threadIdx.x; t < npos; t += blockDim.x) a[t] = exp2f(a[t] - M) / L;
+    for (int t = threadIdx.x; t < npos; t += blockDim.x)
+      a[t] = (float)(exp2((double)a[t] - (double)M) / L);
   }
 }
 

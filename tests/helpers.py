@@ -114,3 +114,74 @@ def q8_special_rows() -> np.ndarray:
     for s in (1e-4, 1e-2, 1.0, 8.0, 300.0):
         rows.append((rng.standard_normal(64) * s).astype(np.float32))
     return np.stack(rows).astype(np.float32)
+
+
+def dequant_rows(shape: orc.Shape, buf: np.ndarray, ctx_cap: int, layer: int,
+                 n_rows: int) -> np.ndarray:
+    """Rows [0, n_rows) of one layer as float64, decoded with numpy (float16
+    scale times int8, exact), independent of the C codec."""
+    rb = shape.row_bytes
+    raw = buf[layer * ctx_cap * rb:(layer * ctx_cap + n_rows) * rb].reshape(n_rows, rb)
+    if not shape.kv_q8:
+        return raw.copy().view(np.float32).astype(np.float64)
+    nb = rb // 34
+    blk = raw.reshape(n_rows, nb, 34)
+    scale = blk[:, :, :2].copy().view(np.float16).astype(np.float64)  # [n, nb, 1]
+    q = blk[:, :, 2:].copy().view(np.int8).astype(np.float64)
+    return (scale * q).reshape(n_rows, nb * 32)[:, :shape.nkv]
+
+
+def exact_attention(shape: orc.Shape, ctx_cap: int, layer: int, pos: int, kc: np.ndarray,
+                    vc: np.ndarray, q: np.ndarray):
+    """float64 attention over the given cache bytes.  q is rotated in float32
+    by the oracle (bit-exact with the reference and the device), so only the
+    score/softmax/V arithmetic is evaluated exactly.
+    Returns (out [nq], weights [n_heads, pos+1])."""
+    hd, nh = shape.head_dim, shape.n_heads
+    group = nh // shape.n_kv_heads
+    qr = orc.rope(shape.arch, q, pos, hd, shape.rope_theta).astype(np.float64).reshape(nh, hd)
+    K = dequant_rows(shape, kc, ctx_cap, layer, pos + 1)
+    V = dequant_rows(shape, vc, ctx_cap, layer, pos + 1)
+    out = np.zeros((nh, hd))
+    W = np.zeros((nh, pos + 1))
+    for h in range(nh):
+        g = h // group
+        sc = K[:, g * hd:(g + 1) * hd] @ qr[h] / np.sqrt(np.float64(hd))
+        w = np.exp(sc - sc.max())
+        w /= w.sum()
+        W[h] = w
+        out[h] = w @ V[:, g * hd:(g + 1) * hd]
+    return out.ravel(), W
+
+
+OUT_ATOL = 1e-4
+W_RTOL = 1e-5
+
+
+def check_out(got, ref, exact, atol: float = OUT_ATOL):
+    """Attention outputs.  got must be within atol of the float64 evaluation
+    and within atol + (the reference's own float32 error) of the reference.
+    Where the reference is accurate (almost always: ~1e-7) this is plain
+    max |got - ref| <= atol; where its serial float32 sums drift (32k
+    contexts with dominant rows), the reference's measured error is added."""
+    got, ref, exact = (np.asarray(a, np.float64) for a in (got, ref, exact))
+    own = float(np.max(np.abs(ref - exact)))
+    e_ex = float(np.max(np.abs(got - exact)))
+    e_ref = float(np.max(np.abs(got - ref)))
+    assert e_ex <= atol, f"max |out - float64| = {e_ex:.3g} > {atol}"
+    assert e_ref <= atol + own, f"max |out - ref| = {e_ref:.3g} > {atol} + ref's own {own:.3g}"
+    return e_ref, e_ex, own
+
+
+def check_weights(got, ref, exact, rtol: float = W_RTOL):
+    """Softmax weights, relative, with the same rule as check_out; weights
+    below 1e-30 are compared absolutely (1e-35)."""
+    got, ref, exact = (np.asarray(a, np.float64) for a in (got, ref, exact))
+    big = exact > 1e-30
+    if big.any():
+        own = float(np.max(np.abs(ref[big] - exact[big]) / exact[big]))
+        r_ex = float(np.max(np.abs(got[big] - exact[big]) / exact[big]))
+        r_ref = float(np.max(np.abs(got[big] - ref[big]) / ref[big]))
+        assert r_ex <= rtol, f"max rel |w - float64| = {r_ex:.3g} > {rtol}"
+        assert r_ref <= rtol + own, f"max rel |w - ref| = {r_ref:.3g} > {rtol} + own {own:.3g}"
+    assert np.all(np.abs(got[~big] - exact[~big]) <= 1e-35)
