@@ -1,0 +1,386 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X, through the C ABI.
+
+Workload (default): BASELINE config 4, the headline roofline case -
+Qwen3-0.6B-shape decode attention, 256 independent sequences each with 8192
+cached positions plus the new token, 28 layers, 16 q / 8 KV heads,
+head_dim 128, NEOX RoPE theta 1e6, Q8_0 KV (~128 GB resident in HBM).
+
+One step = for every sequence and layer: RoPE(q, k), append k/v at pos,
+attention over pos+1 positions, output over q.  The timed step is
+layer-serial (28 g2b_attn_layers calls, three launches each), as a real
+model's layer loop would run it; a one-call-for-all-layers variant is
+reported beside it.  Inputs are synthetic, seeded, generated on the device
+(KV prefill through the same RoPE + append arithmetic) and resident in HBM
+before timing starts.  The q buffer is restored from a pristine copy at the
+start of each step (that 0.1% of traffic is inside the timed region).
+
+Bytes per step are algorithmic, as BASELINE states them:
+  sum over seq, layer of (pos+1)*2*row + 2*row + 4*(2*nq + 2*nkv).
+
+CPU baseline: the C99 oracle (a restatement of the reference path, built
+with the reference flags) on a bounded sample of the same units and the
+same KV bytes the GPU used, timed on the host cores; its outputs double as
+a full-size parity check.  rank 0 prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from gguf2bin_amd import attn, hip  # noqa: E402
+
+METRIC = "decode-attention KV-read GB/s (% of HBM peak) + us/step, Qwen3-0.6B shape"
+HBM_PEAK_GBPS = 8000.0
+Q3, LL = attn.ARCH_QWEN3, attn.ARCH_LLAMA
+
+# name: (shape, n_seq, (ctx_lo, ctx_hi) cached positions, K-row x8 probability, description)
+CONFIGS = {
+    "c1": (attn.Shape(28, 16, 8, 128, 1e6, Q3, False), 1, (2048, 2048), 0.0,
+           "Qwen3-0.6B shape, 1 seq, F32 KV, ctx 2048+1"),
+    "c2": (attn.Shape(28, 16, 8, 128, 1e6, Q3, True), 1, (8192, 8192), 0.0,
+           "Qwen3-0.6B shape, 1 seq, Q8_0 KV, ctx 8192+1"),
+    "c3": (attn.Shape(30, 9, 3, 64, 1e5, LL, False), 64, (256, 2048), 0.0,
+           "SmolLM2-135M shape, 64 seq, F32 KV, ctx U[256,2048]"),
+    "c4": (attn.Shape(28, 16, 8, 128, 1e6, Q3, True), 256, (8192, 8192), 0.0,
+           "Qwen3-0.6B shape, 256 seq, Q8_0 KV, ctx 8192+1 (~128 GB KV)"),
+    "c5": (attn.Shape(32, 32, 8, 128, 5e5, LL, True), 32, (16384, 32767), 0.01,
+           "Llama-3-8B shape, 32 seq, Q8_0 KV, ctx U[16384,32767], 1% K rows x8"),
+}
+
+
+def log(msg: str):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def splitmix_uniform(seed: int, n: int) -> np.ndarray:
+    """n uniforms in (0,1] from SplitMix64 (same generator as the fills)."""
+    m = (1 << 64) - 1
+    out = np.empty(n)
+    s = seed & m
+    for i in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & m
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+        z ^= z >> 31
+        out[i] = ((z >> 11) + 1) * (1.0 / 9007199254740992.0)
+    return out
+
+
+def norm_ppf(p: float) -> float:
+    from statistics import NormalDist
+    return float(NormalDist().inv_cdf(p))
+
+
+def row_bytes(s: attn.Shape) -> int:
+    return attn.kv_row_bytes(s)
+
+
+def step_bytes(s: attn.Shape, poss) -> int:
+    rb = row_bytes(s)
+    per = sum((p + 1) * 2 * rb + 2 * rb + 4 * (2 * s.nq + 2 * s.nkv) for p in poss)
+    return per * s.n_layers
+
+
+def decode_bytes_per_launch(s: attn.Shape, poss, layers_per_launch: int) -> int:
+    """Algorithmic bytes of one decode-kernel launch: the K and V rows of
+    positions 0..pos of every sequence and layer it covers, plus the rotated q."""
+    rb = row_bytes(s)
+    return layers_per_launch * sum((p + 1) * 2 * rb + 4 * s.nq for p in poss)
+
+
+def load_traffic(workload: str):
+    """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE,
+    WRITE_SIZE) and scaled by a copy kernel of known size, when that summary
+    has been committed under profiles/."""
+    p = os.path.join(ROOT, "profiles", f"traffic_k_decode_{workload}.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--n-seq", type=int, default=0, help="override the sequence count")
+    ap.add_argument("--seed", type=int, default=20241201)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-fused", action="store_true", help="skip the all-layers-in-one-call run")
+    ap.add_argument("--cpu-seq-a", type=int, default=4, help="sequences in the 1-thread sample")
+    ap.add_argument("--cpu-seq-b", type=int, default=32, help="sequences in the all-threads sample")
+    ap.add_argument("--cpu-min-s", type=float, default=8.0,
+                    help="repeat each CPU sample until it has run this long")
+    ap.add_argument("--split", type=int, default=0, help="decode split length (0 = automatic)")
+    ap.add_argument("--unroll", type=int, default=0, help="decode wave-steps per trip (0 = auto)")
+    ap.add_argument("--chunk", type=int, default=0, help="Q8 elements per lane (0 = auto)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="before timing, run one plain copy kernel of this many MiB (a "
+                         "known-size reference for rocprofv3 byte counters)")
+    ap.add_argument("--sweep-splits", default="", help="comma list: time layer-serial per split")
+    ap.add_argument("--sweep-variants", default="",
+                    help="semicolon list of split,unroll,chunk: time layer-serial and fused")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+        sys.exit(2)
+    if hip.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    hip.set_device(0)
+
+    shape, n_seq, (lo, hi), p_scale, desc = CONFIGS[args.config]
+    if args.n_seq:
+        n_seq = args.n_seq
+    L, nq, nkv, rb = shape.n_layers, shape.nq, shape.nkv, row_bytes(shape)
+    if lo == hi:
+        poss = [lo] * n_seq
+    else:
+        u = splitmix_uniform(args.seed ^ 0xC7C7, n_seq)
+        poss = [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]
+    caps = [p + 1 for p in poss]
+    thr = norm_ppf(1.0 - p_scale) if p_scale > 0 else float("inf")
+    kv_total = sum(2 * attn.kv_bytes(shape, c) for c in caps)
+    log(f"{args.config}: {desc}; n_seq={n_seq}, KV {kv_total / 1e9:.2f} GB")
+
+    ctx = attn.Context(shape)
+    ctx.tune(args.split, args.unroll, args.chunk)
+    stream = ctx.stream
+    t0 = time.perf_counter()
+    kvs = [ctx.kv_alloc(c) for c in caps]
+    for i, (p, c) in enumerate(zip(poss, caps)):
+        k, v = kvs[i]
+        ctx.synth_fill_kv(k, v, c, 0, L, 0, p, args.seed, i, thr)
+        if i % 32 == 31:
+            ctx.sync()
+            log(f"filled {i + 1}/{n_seq} sequences ({time.perf_counter() - t0:.1f}s)")
+    ctx.sync()
+    t_fill = time.perf_counter() - t0
+    log(f"KV fill done in {t_fill:.1f}s")
+
+    nQ, nK = L * n_seq * nq, L * n_seq * nkv
+    q0 = hip.DeviceBuffer(nQ * 4)
+    qw = hip.DeviceBuffer(nQ * 4)
+    kb = hip.DeviceBuffer(nK * 4)
+    vb = hip.DeviceBuffer(nK * 4)
+    ctx.synth_normal(q0.ptr, nQ, attn.stream_seed(args.seed, 0, 0, 2))
+    ctx.synth_normal(kb.ptr, nK, attn.stream_seed(args.seed, 0, 0, 3))
+    ctx.synth_normal(vb.ptr, nK, attn.stream_seed(args.seed, 0, 0, 4))
+    ctx.batch_begin([(p, c, k, v) for p, c, (k, v) in zip(poss, caps, kvs)])
+    ctx.sync()
+    if args.calibrate_copy:
+        nb = args.calibrate_copy << 20
+        src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+        ctx.synth_copy(dst.ptr, src.ptr, nb)
+        ctx.sync()
+        src.free()
+        dst.free()
+        log(f"calibration copy of {args.calibrate_copy} MiB done")
+
+    def step_layer_serial():
+        ctx.synth_copy(qw.ptr, q0.ptr, nQ * 4)
+        for layer in range(L):
+            ctx.attn_layers(layer, 1, qw.ptr + layer * n_seq * nq * 4,
+                            kb.ptr + layer * n_seq * nkv * 4, vb.ptr + layer * n_seq * nkv * 4)
+
+    def step_fused():
+        ctx.synth_copy(qw.ptr, q0.ptr, nQ * 4)
+        ctx.attn_layers(0, L, qw.ptr, kb.ptr, vb.ptr)
+
+    def timed(step, steps, warmup):
+        for _ in range(warmup):
+            step()
+        ctx.sync()
+        ctx.profile(True)
+        ctx.profile_read()
+        e0, e1 = hip.Event(), hip.Event()
+        h0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        e1.synchronize()
+        wall = time.perf_counter() - h0
+        dms, nlaunch = ctx.profile_read()
+        ctx.profile(False)
+        return e0.elapsed_ms(e1) / steps, wall / steps * 1e3, dms, nlaunch
+
+    if args.sweep_splits:
+        for sl in [int(x) for x in args.sweep_splits.split(",")]:
+            ctx.tune(sl, args.unroll, args.chunk)
+            sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
+            log(f"split {sl}: {sms * 1e3:.1f} us/step, {step_bytes(shape, poss) / sms / 1e6:.1f} "
+                f"GB/s, k_decode avg {sd / max(sn, 1) * 1e3:.1f} us")
+        ctx.tune(args.split, args.unroll, args.chunk)
+    if args.sweep_variants:
+        for v in args.sweep_variants.split(";"):
+            sl, un, ch = [int(x) for x in v.split(",")]
+            ctx.tune(sl, un, ch)
+            sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
+            fms, _, fd, fn = timed(step_fused, max(3, args.steps // 2), 1)
+            log(f"variant split={sl} unroll={un} chunk={ch}: layer-serial {sms * 1e3:.1f} us/step "
+                f"({step_bytes(shape, poss) / sms / 1e6:.1f} GB/s, k_decode {sd / max(sn, 1) * 1e3:.1f}"
+                f" us), fused {fms * 1e3:.1f} us/step ({step_bytes(shape, poss) / fms / 1e6:.1f} GB/s)")
+        ctx.tune(args.split, args.unroll, args.chunk)
+
+    ms, wall_ms, dec_ms, dec_n = timed(step_layer_serial, args.steps, args.warmup)
+    sb = step_bytes(shape, poss)
+    gbps = sb / (ms * 1e-3) / 1e9
+    log(f"layer-serial: {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), {gbps:.1f} GB/s, "
+        f"{100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak")
+    dec_avg_ms = dec_ms / max(dec_n, 1)
+    dec_bytes = decode_bytes_per_launch(shape, poss, 1)
+    dec_gbps = dec_bytes / (dec_avg_ms * 1e-3) / 1e9
+    log(f"k_decode: {dec_n} launches, avg {dec_avg_ms * 1e3:.1f} us, {dec_gbps:.1f} GB/s")
+
+    fused = None
+    if not args.no_fused:
+        fms, fwall, fdec, fn = timed(step_fused, args.steps, 1)
+        fused = {"us_per_step": round(fms * 1e3, 2),
+                 "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
+                 "k_decode_avg_us": round(fdec / max(fn, 1) * 1e3, 2),
+                 "k_decode_GBps": round(decode_bytes_per_launch(shape, poss, L) /
+                                        (fdec / max(fn, 1) * 1e-3) / 1e9, 2),
+                 "launches_per_step": 4}
+        log(f"all layers in one call: {fms * 1e3:.1f} us/step, {fused['GBps']} GB/s")
+
+    # Leave the layer-serial outputs in qw for the parity sample.
+    step_layer_serial()
+    ctx.sync()
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        cpu, parity = cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb)
+
+    traffic = load_traffic(args.config)
+    roof = {"bound": "hbm", "kernel": "k_decode", "achieved": round(dec_gbps, 2),
+            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
+            "bytes_per_launch": dec_bytes, "avg_launch_us": round(dec_avg_ms * 1e3, 2),
+            "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None}
+    if traffic:
+        roof["traffic_source"] = traffic.get("source")
+
+    line = {
+        "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"{args.config}: {desc}", "n_seq": n_seq,
+                   "ctx_min": min(poss), "ctx_max": max(poss), "layers": L,
+                   "n_heads": shape.n_heads, "n_kv_heads": shape.n_kv_heads,
+                   "head_dim": shape.head_dim, "kv": "q8_0" if shape.kv_q8 else "f32",
+                   "step": "layer-serial: per layer one append, one decode, one combine launch",
+                   "parallelism": "single GPU"},
+        "us_per_step": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "bytes_per_step": sb,
+        "kv_fill_s": round(t_fill, 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "all_layers_one_call": fused,
+        "parity_full_size": parity,
+    }
+    for k, v in kvs:
+        ctx.kv_free(k, v)
+    ctx.close()
+    print(json.dumps(line), flush=True)
+
+
+def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):
+    """Time the oracle on a bounded sample of the same units (same KV bytes,
+    same inputs) and compare its outputs and appended rows with the GPU's."""
+    from oracle import orc  # CPU baseline and checker only
+
+    o = orc.Shape(shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
+                  shape.rope_theta, shape.arch, shape.kv_q8)
+    L, nq, nkv, rb = shape.n_layers, shape.nq, shape.nkv, row_bytes(shape)
+    n_seq = len(poss)
+    nb = max(1, min(args.cpu_seq_b, n_seq))
+    na = max(1, min(args.cpu_seq_a, nb))
+    idx = list(range(nb))
+    nQ, nK = L * n_seq * nq, L * n_seq * nkv
+    q_all = q0.download(np.float32, nQ).reshape(L, n_seq, nq)
+    k_all = kb.download(np.float32, nK).reshape(L, n_seq, nkv)
+    v_all = vb.download(np.float32, nK).reshape(L, n_seq, nkv)
+    out_gpu = qw.download(np.float32, nQ).reshape(L, n_seq, nq)
+    t0 = time.perf_counter()
+    host = []
+    for i in idx:
+        nbytes = attn.kv_bytes(shape, caps[i])
+        host.append((hip.copy_d2h(kvs[i][0], np.uint8, nbytes),
+                     hip.copy_d2h(kvs[i][1], np.uint8, nbytes)))
+    log(f"cpu sample: {nb} sequences copied to host in {time.perf_counter() - t0:.1f}s")
+    gpu_rows = [(kc.reshape(L, caps[i], rb)[:, poss[i]].copy(),
+                 vc.reshape(L, caps[i], rb)[:, poss[i]].copy()) for i, (kc, vc) in zip(idx, host)]
+
+    def sample(ids, threads):
+        """Run the sample repeatedly for at least --cpu-min-s; seconds per pass."""
+        pos = np.array([poss[i] for i in ids], np.int32)
+        cap = np.array([caps[i] for i in ids], np.int32)
+        sel = np.array(ids)
+        q = np.ascontiguousarray(q_all[:, sel])
+        k = np.ascontiguousarray(k_all[:, sel])
+        v = np.ascontiguousarray(v_all[:, sel])
+        reps, t = 0, orc.now()
+        while True:
+            out = orc.attn_batch(o, 0, L, pos, cap, [host[j][0] for j in range(len(ids))],
+                                 [host[j][1] for j in range(len(ids))], q, k, v, threads)
+            reps += 1
+            if orc.now() - t >= args.cpu_min_s:
+                break
+        return (orc.now() - t) / reps, out, reps
+
+    threads = orc.max_threads()
+    ta, out_a, reps_a = sample(idx[:na], 1)
+    tb, out_b, reps_b = sample(idx, threads)
+    bytes_a = step_bytes(shape, [poss[i] for i in idx[:na]])
+    bytes_b = step_bytes(shape, [poss[i] for i in idx])
+    gbps_a, gbps_b = bytes_a / ta / 1e9, bytes_b / tb / 1e9
+    log(f"cpu: 1 thread {gbps_a:.2f} GB/s ({reps_a} x {ta:.2f}s), {threads} threads "
+        f"{gbps_b:.2f} GB/s ({reps_b} x {tb:.2f}s)")
+
+    err = float(np.max(np.abs(out_b - out_gpu[:, idx])))
+    rows_exact = all(
+        np.array_equal(host[j][0].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][0]) and
+        np.array_equal(host[j][1].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][1])
+        for j, i in enumerate(idx))
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    cpu = {"value": round(gbps_b, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{nb} of {len(poss)} sequences x {L} layers (all host threads, OpenMP "
+                     f"over sequences), same KV bytes and inputs as the GPU, {reps_b} passes",
+           "seconds": round(tb * reps_b, 2), "cpu": cpu_model,
+           "one_thread": {"value": round(gbps_a, 3), "unit": "GB/s", "cores": 1,
+                          "sample": f"{na} sequences x {L} layers, sequences in turn "
+                                    f"(the reference attention is single-threaded), "
+                                    f"{reps_a} passes",
+                          "seconds": round(ta * reps_a, 2)}}
+    parity = {"units_checked": nb * L, "max_abs_out_err_vs_oracle": err,
+              "appended_rows_bit_exact": bool(rows_exact)}
+    return cpu, parity
+
+
+if __name__ == "__main__":
+    main()

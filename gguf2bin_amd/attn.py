@@ -32,7 +32,7 @@ EXPORTS = [
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
-    "g2b_ctx_profile", "g2b_ctx_profile_read",
+    "g2b_ctx_profile", "g2b_ctx_profile_read", "g2b_ctx_tune",
 ]
 
 
@@ -115,6 +115,7 @@ def lib() -> C.CDLL:
                                   C.c_int),
             "g2b_synth_copy": ([vp, vp, vp, u64], C.c_int),
             "g2b_ctx_profile": ([vp, i32], C.c_int),
+            "g2b_ctx_tune": ([vp, i32, i32, i32], C.c_int),
             "g2b_ctx_profile_read": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)],
                                      C.c_int),
         }
@@ -246,6 +247,10 @@ class Context:
 
     def synth_copy(self, dst: int, src: int, nbytes: int):
         self._check(lib().g2b_synth_copy(self.h, dst, src, nbytes), "g2b_synth_copy")
+
+    def tune(self, split_len: int = 0, unroll: int = 0, chunk: int = 0):
+        """Decode-kernel tuning (0 = automatic): split length, unroll, Q8 chunk."""
+        self._check(lib().g2b_ctx_tune(self.h, split_len, unroll, chunk), "g2b_ctx_tune")
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

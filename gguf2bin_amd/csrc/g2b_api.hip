@@ -46,6 +46,10 @@ struct g2b_ctx {
   float *hstage = nullptr;  // device staging for the *_host entry point
   size_t hstage_cap = 0;
 
+  int32_t slots = 0;           // resident decode workgroups on the device
+  int32_t split_override = 0;  // g2b_ctx_tune
+  int32_t tune_unroll = 0, tune_chunk = 0;
+
   // decode-launch timing (g2b_ctx_profile)
   bool prof = false;
   std::vector<hipEvent_t> prof_ev;  // pairs: [2i] before, [2i+1] after launch i
@@ -139,21 +143,23 @@ int ensure_rope(g2b_ctx *c, int32_t len) {
   return G2B_OK;
 }
 
-// Positions per split.  Aim for ~2048 workgroups per call so that the 256
-// CUs (two resident 256-thread workgroups each) see several waves of work;
-// keep at most 512 splits per sequence (the combine stages 4 weights per
-// split in LDS) and obey the generic kernel's LDS limit.
+// Positions per split.  The decode workgroups of one call should form whole
+// rounds of the device's resident slots (CUs x workgroups per CU): with equal
+// work per workgroup they start and finish together, and the launch has no
+// partly idle tail.  One round when the work allows it; otherwise as many
+// rounds as the minimum split length forces.  At most 512 splits per
+// sequence (the combine stages 4 weights per split in LDS) and the generic
+// kernel's LDS limit apply.
 int32_t choose_split(const g2b_ctx *c, int64_t total_pos, int32_t max_pos, int32_t n_layers,
                      bool fast) {
   const int64_t work = total_pos * (int64_t)n_layers;
-  int64_t sl = (work + 2047) / 2048;
-  sl = std::max<int64_t>(sl, 64);
-  sl = (sl + 63) / 64 * 64;
+  const int64_t slots = std::max<int64_t>(c->slots, 1);
+  int64_t sl = c->split_override > 0 ? c->split_override : (work + slots - 1) / slots;
+  if (c->split_override <= 0) sl = std::max<int64_t>(sl, 64);
   const int64_t min_for_cap = ((int64_t)max_pos + 1 + 511) / 512;
-  sl = std::max(sl, (min_for_cap + 63) / 64 * 64);
+  sl = std::max(sl, min_for_cap);
   if (!fast) sl = std::min<int64_t>(sl, kGenericMaxSplit);
-  sl = std::min<int64_t>(sl, (int64_t)max_pos + 1 + 63);
-  (void)c;
+  sl = std::min<int64_t>(sl, (int64_t)max_pos + 1);
   return (int32_t)std::max<int64_t>(sl, 1);
 }
 
@@ -208,6 +214,10 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.att = att;
   dp.att_stride = att_stride;
   dp.qscale = c->qscale;
+  dp.tune_unroll = c->tune_unroll;
+  // half-block lanes need twice the lanes per position; keep them only where they fit
+  dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
+                   c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
   int used_fast = 0;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   if (c->prof) {
@@ -296,6 +306,11 @@ int g2b_ctx_create(g2b_ctx **out, int32_t device, const g2b_shape *s) {
     return G2B_EDEVICE;
   }
   c->stream = c->own;
+  int n_cu = 0;
+  if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+    n_cu = 0;
+  (void)hipGetLastError();
+  c->slots = std::max(1, n_cu) * decode_blocks_per_cu(c->sh);
   *out = c;
   return G2B_OK;
 }
@@ -536,6 +551,16 @@ int g2b_synth_copy(g2b_ctx *c, void *dst, const void *src, uint64_t nbytes) {
     return fail(c, G2B_EINVAL, "copy needs 16-byte multiples and alignment");
   if (int rc = set_device(c)) return rc;
   G2B_HIP(c, launch_copy16(dst, src, nbytes / 16, c->stream));
+  return G2B_OK;
+}
+
+int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t unroll, int32_t chunk) {
+  if (!c || split_len < 0 || (unroll != 0 && unroll != 2 && unroll != 4) ||
+      (chunk != 0 && chunk != 16 && chunk != 32))
+    return G2B_EINVAL;
+  c->split_override = split_len;
+  c->tune_unroll = unroll;
+  c->tune_chunk = chunk;
   return G2B_OK;
 }
 

@@ -22,6 +22,8 @@
 // (seq, layer, head), writes the output over q (as l5_model.c:541-557 does)
 // and, when asked, turns the stored scores into the reference's
 // att[h*ctx+t] weights.
+#include <type_traits>
+
 #include "g2b_internal.h"
 
 namespace g2b {
@@ -47,6 +49,16 @@ __device__ __forceinline__ float i8f(uint32_t w, int byte) {
   return (float)(int8_t)(uint8_t)(w >> (8 * byte));
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Loads through the global address space (the cache pointers arrive through a
+// descriptor table, so the compiler would otherwise emit flat loads).
+template <typename T>
+__device__ __forceinline__ T gload(const uint8_t *p) {
+  return *(const __attribute__((address_space(1))) T *)(p);
+}
+
 // Per-lane addressing of its chunk inside a row.
 struct LaneOff {
   uint32_t o0, o1, o2;  // byte offsets inside the row
@@ -61,7 +73,7 @@ struct Codec;
 template <>
 struct Codec<0, 16> {
   struct Raw {
-    float4 x[4];
+    f32x4 x[4];
   };
   static __device__ __forceinline__ LaneOff offsets(int elem0) {
     LaneOff o;
@@ -70,12 +82,10 @@ struct Codec<0, 16> {
     return o;
   }
   static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
-    const float4 *p = reinterpret_cast<const float4 *>(row + o.o0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) r.x[i] = p[i];
+    for (int i = 0; i < 4; i++) r.x[i] = gload<f32x4>(row + o.o0 + 16 * i);
   }
-  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[16], float &scale,
-                                                const LaneOff &) {
+  static __device__ __forceinline__ void values(const Raw &r, float (&f)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       f[4 * i + 0] = r.x[i].x;
@@ -83,7 +93,6 @@ struct Codec<0, 16> {
       f[4 * i + 2] = r.x[i].z;
       f[4 * i + 3] = r.x[i].w;
     }
-    scale = 1.f;
   }
 };
 
@@ -96,7 +105,7 @@ struct Codec<0, 16> {
 template <>
 struct Codec<1, 32> {
   struct Raw {
-    uint4 a, b;
+    u32x4 a, b;
     uint32_t c;
   };
   static __device__ __forceinline__ LaneOff offsets(int elem0) {
@@ -110,20 +119,17 @@ struct Codec<1, 32> {
   }
   static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
     const uint8_t *p = row + o.o0;
-    r.a = *reinterpret_cast<const uint4 *>(p);
-    r.b = *reinterpret_cast<const uint4 *>(p + 16);
-    r.c = *reinterpret_cast<const uint32_t *>(p + 32);
+    r.a = gload<u32x4>(p);
+    r.b = gload<u32x4>(p + 16);
+    r.c = gload<uint32_t>(p + 32);
   }
-  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[32], float &scale,
+  // the 32 int8 quants as 8 aligned dwords, and the block scale
+  static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[8], float &scale,
                                                 const LaneOff &o) {
     const uint32_t d[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
     scale = half_bits_to_f32((d[0] >> o.sshift) & 0xffffu);
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const uint32_t w = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
-#pragma unroll
-      for (int k = 0; k < 4; k++) f[4 * j + k] = i8f(w, k);
-    }
+    for (int j = 0; j < 8; j++) w[j] = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
   }
 };
 
@@ -135,7 +141,7 @@ template <>
 struct Codec<1, 16> {
   struct Raw {
     uint32_t s;
-    uint4 a;
+    u32x4 a;
     uint32_t c;
   };
   static __device__ __forceinline__ LaneOff offsets(int elem0) {
@@ -150,26 +156,86 @@ struct Codec<1, 16> {
     return o;
   }
   static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
-    r.s = *reinterpret_cast<const uint32_t *>(row + o.o0);
-    r.a = *reinterpret_cast<const uint4 *>(row + o.o1);
-    r.c = *reinterpret_cast<const uint32_t *>(row + o.o2);
+    r.s = gload<uint32_t>(row + o.o0);
+    r.a = gload<u32x4>(row + o.o1);
+    r.c = gload<uint32_t>(row + o.o2);
   }
-  static __device__ __forceinline__ void decode(const Raw &r, float (&f)[16], float &scale,
+  static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[4], float &scale,
                                                 const LaneOff &o) {
     const uint32_t d[5] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c};
     scale = half_bits_to_f32((r.s >> o.sshift) & 0xffffu);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint32_t w = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
-#pragma unroll
-      for (int k = 0; k < 4; k++) f[4 * j + k] = i8f(w, k);
-    }
+    for (int j = 0; j < 4; j++) w[j] = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
   }
 };
 
+// q for the integer K dot products: each q value of a (head, chunk) becomes
+// m = rint(q * 2^(22-e)) with 2^e > max|q| (so |m| <= 2^22, 23 bits of the
+// chunk maximum), split into three signed base-256 digits packed four per
+// dword.  sum_j m_j k_j is then three chains of v_dot4_i32_i8 (exact in
+// int32) and one fp32 rounding; the quantisation of q costs at most
+// 2^-23 * max|q| per element, less than an fp32 FMA chain over the same
+// int8 values loses.
+template <int CD>
+struct QDigits {
+  uint32_t d[3][CD / 4];
+  float unit;  // 2^(e-22): value of one m step
+};
+
+template <int CD>
+__device__ __forceinline__ QDigits<CD> make_digits(const float (&q)[CD]) {
+  QDigits<CD> r;
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < CD; j++) mx = fmaxf(mx, fabsf(q[j]));
+  int e = 0;
+  (void)frexpf(mx, &e);
+  const float up = ldexpf(1.f, 22 - e);
+  r.unit = ldexpf(1.f, e - 22);
+#pragma unroll
+  for (int k = 0; k < 3; k++)
+#pragma unroll
+    for (int j = 0; j < CD / 4; j++) r.d[k][j] = 0u;
+#pragma unroll
+  for (int j = 0; j < CD; j++) {
+    const int m = (int)rintf(q[j] * up);
+    const int d0 = ((m + 128) & 255) - 128;
+    const int m1 = (m - d0) >> 8;
+    const int d1 = ((m1 + 128) & 255) - 128;
+    const int d2 = (m1 - d1) >> 8;
+    const int sh = 8 * (j & 3);
+    r.d[0][j >> 2] |= ((uint32_t)d0 & 0xffu) << sh;
+    r.d[1][j >> 2] |= ((uint32_t)d1 & 0xffu) << sh;
+    r.d[2][j >> 2] |= ((uint32_t)d2 & 0xffu) << sh;
+  }
+  return r;
+}
+
+// sum_j m_j * k_j for the chunk, as a float in units of m.
+template <int NW>
+__device__ __forceinline__ float qk_int(const uint32_t (&w)[NW], const uint32_t (&d)[3][NW]) {
+  int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+  for (int j = 0; j < NW; j++) {
+    s0 = __builtin_amdgcn_sdot4((int)w[j], (int)d[0][j], s0, false);
+    s1 = __builtin_amdgcn_sdot4((int)w[j], (int)d[1][j], s1, false);
+    s2 = __builtin_amdgcn_sdot4((int)w[j], (int)d[2][j], s2, false);
+  }
+  // |s2| <= 32*65*127, so s2*256 + s1 fits in int32
+  const int hi = s2 * 256 + s1;
+  return (float)hi * 256.f + (float)s0;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  // v_exp_f32; results below 2^-126 (weights under 1e-38 of the maximum)
+  // may flush to zero, which no output can see.
+  return __builtin_amdgcn_exp2f(x);
+}
+
 // FMT: 0 = F32 KV, 1 = Q8_0 KV.  HD: head_dim.  CD: elements per lane.
 // G: q heads per KV head.  U: wave-steps in flight per loop trip.
-template <int FMT, int HD, int CD, int G, int U>
+// ATT: also store each score for the reference-layout weight output.
+template <int FMT, int HD, int CD, int G, int U, bool ATT>
 __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
   constexpr int LPH = HD / CD;  // lanes per head
   using C = Codec<FMT, CD>;
@@ -180,11 +246,13 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
   if (t0 >= npos) return;
   const int t1 = min(npos, t0 + P.split_len);
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int LPP = P.sh.n_kv_heads * LPH;  // lanes per position (<= 64, checked on host)
   const int PPW = 64 / LPP;               // positions per wave-step
   const int slot = lane / LPP;
   const bool lane_on = slot < PPW;
+  const int slot_ld = lane_on ? slot : 0;  // idle lanes shadow slot 0's rows
   const int r = lane_on ? lane - slot * LPP : 0;
   const int g = r / LPH, c = r - g * LPH;
   const int layer = P.layer0 + li;
@@ -206,10 +274,17 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
         q[i][j + 3] = v4.w * P.qscale;
       }
   }
+  [[maybe_unused]] QDigits<CD> qd[G];
+  if constexpr (FMT == 1) {
+#pragma unroll
+    for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
+  }
   const LaneOff lo = C::offsets(g * HD + c * CD);
   const size_t row = P.sh.row_bytes;
-  const uint8_t *kb = sd.k + (size_t)layer * (size_t)sd.ctx_cap * row;
-  const uint8_t *vb = sd.v + (size_t)layer * (size_t)sd.ctx_cap * row;
+  const int stride = kWavesPerSplit * PPW;           // positions between a wave's steps
+  const size_t ustep = (size_t)stride * row;         // bytes between them
+  const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+  const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
 
   float m[G], l[G], acc[G][CD];
 #pragma unroll
@@ -219,37 +294,55 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
 #pragma unroll
     for (int j = 0; j < CD; j++) acc[i][j] = 0.f;
   }
-  float *att_h = nullptr;
-  if (P.att) att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
+  [[maybe_unused]] float *att_h = nullptr;
+  if constexpr (ATT)
+    att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
 
-  const int stride = kWavesPerSplit * PPW;
-  for (int tb = t0 + wave * PPW; tb < t1; tb += stride * U) {
+  // One loop trip: U wave-steps of this wave.  CHECK masks positions >= t1
+  // (only the last trip of a split needs it).
+  auto trip = [&](int tb, auto check) {
+    constexpr bool CHECK = decltype(check)::value;
     typename C::Raw kr[U], vr[U];
     bool valid[U];
-    int tu[U];
+    const size_t base = (size_t)(tb + slot_ld) * row;
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      tu[u] = tb + u * stride + slot;
-      valid[u] = lane_on && tu[u] < t1;
-      const size_t tt = (size_t)(valid[u] ? tu[u] : t0);
-      C::load(kr[u], kb + tt * row, lo);
-      C::load(vr[u], vb + tt * row, lo);
+      size_t off = base + (size_t)u * ustep;
+      if constexpr (CHECK) {
+        valid[u] = lane_on && tb + u * stride + slot < t1;
+        if (!valid[u]) off = (size_t)t0 * row;
+      } else {
+        valid[u] = true;
+      }
+      C::load(kr[u], kb + off, lo);
+      C::load(vr[u], vb + off, lo);
     }
     float sc[U][G];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      float kf[CD], ks;
-      C::decode(kr[u], kf, ks, lo);
+      if constexpr (FMT == 1) {
+        uint32_t w[CD / 4];
+        float ks;
+        C::quants(kr[u], w, ks, lo);
 #pragma unroll
-      for (int i = 0; i < G; i++) {
-        float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < CD; j += 2) {
-          s0 = fmaf(q[i][j], kf[j], s0);
-          s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
+        for (int i = 0; i < G; i++) {
+          const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
+          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
         }
-        const float s = group_sum<LPH>((s0 + s1) * ks);
-        sc[u][i] = valid[u] ? s : -INFINITY;
+      } else {
+        float kf[CD];
+        C::values(kr[u], kf);
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+          for (int j = 0; j < CD; j += 2) {
+            s0 = fmaf(q[i][j], kf[j], s0);
+            s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
+          }
+          const float s = group_sum<LPH>(s0 + s1);
+          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
+        }
       }
     }
     bool need = false;
@@ -265,7 +358,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
     if (__any(need)) {
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        const float a = exp2f(m[i] - mn[i]);
+        const float a = fast_exp2(m[i] - mn[i]);
         l[i] *= a;
 #pragma unroll
         for (int j = 0; j < CD; j++) acc[i][j] *= a;
@@ -274,22 +367,49 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      float vf[CD], vs;
-      C::decode(vr[u], vf, vs, lo);
+      float p[G];
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        const float p = exp2f(sc[u][i] - m[i]);
-        l[i] += p;
-        const float pv = p * vs;
-#pragma unroll
-        for (int j = 0; j < CD; j++) acc[i][j] = fmaf(pv, vf[j], acc[i][j]);
+        p[i] = fast_exp2(sc[u][i] - m[i]);
+        l[i] += p[i];
       }
-      if (att_h && c == 0 && valid[u]) {
+      if constexpr (FMT == 1) {
+        uint32_t w[CD / 4];
+        float vs;
+        C::quants(vr[u], w, vs, lo);
+        float pv[G];
 #pragma unroll
-        for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tu[u]] = sc[u][i];
+        for (int i = 0; i < G; i++) pv[i] = p[i] * vs;
+#pragma unroll
+        for (int j = 0; j < CD / 4; j++)
+#pragma unroll
+          for (int b = 0; b < 4; b++) {
+            const float x = i8f(w[j], b);
+#pragma unroll
+            for (int i = 0; i < G; i++) acc[i][4 * j + b] = fmaf(pv[i], x, acc[i][4 * j + b]);
+          }
+      } else {
+        float vf[CD];
+        C::values(vr[u], vf);
+#pragma unroll
+        for (int j = 0; j < CD; j++)
+#pragma unroll
+          for (int i = 0; i < G; i++) acc[i][j] = fmaf(p[i], vf[j], acc[i][j]);
+      }
+      if constexpr (ATT) {
+        const int t = tb + u * stride + slot;
+        if (c == 0 && valid[u] && lane_on && t < t1) {
+#pragma unroll
+          for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + t] = sc[u][i];
+        }
       }
     }
-  }
+  };
+
+  const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
+  int tb = t0 + wave * PPW;
+  for (; tb + trip_span <= t1; tb += stride * U) trip(tb, std::false_type{});
+  for (; tb < t1; tb += stride * U) trip(tb, std::true_type{});
 
   // Fold the PPW position slots of the wave into slot 0.  Every lane takes
   // part in the shuffles, but only slot-0 lanes update their state, so the
@@ -460,20 +580,31 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
 
 // ---------------------------------------------------------------- dispatch
 
+template <int FMT, int HD, int CD, int G, int U>
+static hipError_t launch_fast_u(const DecodeParams &p, int n_layers, hipStream_t s) {
+  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  if (p.att)
+    hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U, true>), grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U, false>), grid, dim3(kThreads), 0, s, p);
+  return hipGetLastError();
+}
+
 template <int FMT, int HD, int CD, int G>
 static hipError_t launch_fast(const DecodeParams &p, int n_layers, hipStream_t s) {
-  constexpr int U = 2;
-  dim3 grid(p.max_splits, p.n_seq, n_layers);
-  hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U>), grid, dim3(kThreads), 0, s, p);
-  return hipGetLastError();
+  if (p.tune_unroll == 4) return launch_fast_u<FMT, HD, CD, G, 4>(p, n_layers, s);
+  return launch_fast_u<FMT, HD, CD, G, 2>(p, n_layers, s);
 }
 
 template <int FMT, int HD>
 static hipError_t launch_fast_hd(const DecodeParams &p, int group, int n_layers, hipStream_t s) {
   if constexpr (FMT == 1) {
+    const bool half = p.tune_chunk == 16;
     switch (group) {
-      case 1: return launch_fast<1, HD, 32, 1>(p, n_layers, s);
-      case 2: return launch_fast<1, HD, 32, 2>(p, n_layers, s);
+      case 1: return half ? launch_fast<1, HD, 16, 1>(p, n_layers, s)
+                          : launch_fast<1, HD, 32, 1>(p, n_layers, s);
+      case 2: return half ? launch_fast<1, HD, 16, 2>(p, n_layers, s)
+                          : launch_fast<1, HD, 32, 2>(p, n_layers, s);
       case 3: return launch_fast<1, HD, 16, 3>(p, n_layers, s);
       case 4: return launch_fast<1, HD, 16, 4>(p, n_layers, s);
     }
@@ -492,6 +623,45 @@ static int fast_chunk(const ShapeDev &sh) {
   const int group = sh.n_heads / sh.n_kv_heads;
   if (sh.kv_q8) return group <= 2 ? 32 : 16;
   return 16;
+}
+
+template <int FMT, int HD, int CD, int G>
+static int occ_of() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<FMT, HD, CD, G, 2, false>,
+                                                   kThreads, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  return n > 0 ? n : 1;
+}
+
+int decode_blocks_per_cu(const ShapeDev &sh) {
+  if (!decode_fast_available(sh)) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode_generic, kThreads, 0) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      return 1;
+    }
+    return n > 0 ? n : 1;
+  }
+  const int group = sh.n_heads / sh.n_kv_heads;
+  const bool hd128 = sh.head_dim == 128;
+  if (sh.kv_q8) {
+    switch (group) {
+      case 1: return hd128 ? occ_of<1, 128, 32, 1>() : occ_of<1, 64, 32, 1>();
+      case 2: return hd128 ? occ_of<1, 128, 32, 2>() : occ_of<1, 64, 32, 2>();
+      case 3: return hd128 ? occ_of<1, 128, 16, 3>() : occ_of<1, 64, 16, 3>();
+      default: return hd128 ? occ_of<1, 128, 16, 4>() : occ_of<1, 64, 16, 4>();
+    }
+  }
+  switch (group) {
+    case 1: return hd128 ? occ_of<0, 128, 16, 1>() : occ_of<0, 64, 16, 1>();
+    case 2: return hd128 ? occ_of<0, 128, 16, 2>() : occ_of<0, 64, 16, 2>();
+    case 3: return hd128 ? occ_of<0, 128, 16, 3>() : occ_of<0, 64, 16, 3>();
+    default: return hd128 ? occ_of<0, 128, 16, 4>() : occ_of<0, 64, 16, 4>();
+  }
 }
 
 bool decode_fast_available(const ShapeDev &sh) {

@@ -43,6 +43,8 @@ struct DecodeParams {
   float *att;          // nullable: [L][n_seq][n_heads][att_stride]
   int32_t att_stride;
   float qscale;        // (1/sqrtf(hd)) * log2(e)
+  int32_t tune_unroll; // 0 = default, else wave-steps per loop trip (2 or 4)
+  int32_t tune_chunk;  // 0 = default, else elements per lane for Q8 (16 or 32)
 };
 
 // Launchers: return hipSuccess or the launch error.
@@ -54,6 +56,8 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 // Whether a specialised decode kernel exists for this shape.
 bool decode_fast_available(const ShapeDev &sh);
+// Resident 256-thread decode workgroups per CU for this shape (occupancy).
+int decode_blocks_per_cu(const ShapeDev &sh);
 
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {

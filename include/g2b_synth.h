@@ -43,6 +43,12 @@ int g2b_synth_fill_kv(g2b_ctx *ctx, void *kcache, void *vcache, int32_t ctx_cap,
  * the known-size reference kernel used to scale HBM byte counters. */
 int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
 
+/* Tuning of the decode kernel; 0 keeps the automatic choice for each:
+ * split_len = positions per split (automatic: a few workgroups per CU per
+ * launch), unroll = wave-steps per loop trip (2 or 4), chunk = Q8_0
+ * elements per lane (32 = a block, 16 = half a block). */
+int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t unroll, int32_t chunk);
+
 /* Kernel timing with HIP events on the context's stream: while enabled,
  * every decode-kernel launch is bracketed by two events.  _read waits for
  * them, returns the summed milliseconds and the number of launches since
