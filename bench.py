@@ -8,9 +8,10 @@ head_dim 128, NEOX RoPE theta 1e6, Q8_0 KV (~128 GB resident in HBM).
 
 One step = for every sequence and layer: RoPE(q, k), append k/v at pos,
 attention over pos+1 positions, output over q.  The timed step is
-layer-serial (28 g2b_attn_layers calls, three launches each), as a real
-model's layer loop would run it; a one-call-for-all-layers variant is
-reported beside it.  Inputs are synthetic, seeded, generated on the device
+layer-serial (28 g2b_attn_layers calls, each one k_layer launch - RoPE,
+append, attention over the splits - and one k_combine launch that merges
+the split partials), as a real model's layer loop would run it; a
+one-call-for-all-layers variant is reported beside it.  Inputs are synthetic, seeded, generated on the device
 (KV prefill through the same RoPE + append arithmetic) and resident in HBM
 before timing starts.  The q buffer is restored from a pristine copy at the
 start of each step (that 0.1% of traffic is inside the timed region).
@@ -91,18 +92,18 @@ def step_bytes(s: attn.Shape, poss) -> int:
     return per * s.n_layers
 
 
-def decode_bytes_per_launch(s: attn.Shape, poss, layers_per_launch: int) -> int:
-    """Algorithmic bytes of one decode-kernel launch: the K and V rows of
-    positions 0..pos of every sequence and layer it covers, plus the rotated q."""
-    rb = row_bytes(s)
-    return layers_per_launch * sum((p + 1) * 2 * rb + 4 * s.nq for p in poss)
+def launch_bytes(s: attn.Shape, poss, layers_per_launch: int) -> int:
+    """Algorithmic bytes of one k_layer launch: the step's per-layer bytes
+    (KV read of positions 0..pos, the appended rows, q/out/k/v) for every
+    layer the launch covers."""
+    return step_bytes(s, poss) // s.n_layers * layers_per_launch
 
 
 def load_traffic(workload: str):
     """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE) and scaled by a copy kernel of known size, when that summary
     has been committed under profiles/."""
-    p = os.path.join(ROOT, "profiles", f"traffic_k_decode_{workload}.json")
+    p = os.path.join(ROOT, "profiles", f"traffic_k_layer_{workload}.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -224,7 +225,7 @@ def main():
             ctx.tune(sl, args.unroll, args.chunk)
             sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
             log(f"split {sl}: {sms * 1e3:.1f} us/step, {step_bytes(shape, poss) / sms / 1e6:.1f} "
-                f"GB/s, k_decode avg {sd / max(sn, 1) * 1e3:.1f} us")
+                f"GB/s, k_layer avg {sd / max(sn, 1) * 1e3:.1f} us")
         ctx.tune(args.split, args.unroll, args.chunk)
     if args.sweep_variants:
         for v in args.sweep_variants.split(";"):
@@ -233,7 +234,7 @@ def main():
             sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
             fms, _, fd, fn = timed(step_fused, max(3, args.steps // 2), 1)
             log(f"variant split={sl} unroll={un} chunk={ch}: layer-serial {sms * 1e3:.1f} us/step "
-                f"({step_bytes(shape, poss) / sms / 1e6:.1f} GB/s, k_decode {sd / max(sn, 1) * 1e3:.1f}"
+                f"({step_bytes(shape, poss) / sms / 1e6:.1f} GB/s, k_layer {sd / max(sn, 1) * 1e3:.1f}"
                 f" us), fused {fms * 1e3:.1f} us/step ({step_bytes(shape, poss) / fms / 1e6:.1f} GB/s)")
         ctx.tune(args.split, args.unroll, args.chunk)
 
@@ -243,19 +244,18 @@ def main():
     log(f"layer-serial: {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), {gbps:.1f} GB/s, "
         f"{100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak")
     dec_avg_ms = dec_ms / max(dec_n, 1)
-    dec_bytes = decode_bytes_per_launch(shape, poss, 1)
+    dec_bytes = launch_bytes(shape, poss, 1)
     dec_gbps = dec_bytes / (dec_avg_ms * 1e-3) / 1e9
-    log(f"k_decode: {dec_n} launches, avg {dec_avg_ms * 1e3:.1f} us, {dec_gbps:.1f} GB/s")
+    log(f"k_layer: {dec_n} launches, avg {dec_avg_ms * 1e3:.1f} us, {dec_gbps:.1f} GB/s")
 
     fused = None
     if not args.no_fused:
         fms, fwall, fdec, fn = timed(step_fused, args.steps, 1)
         fused = {"us_per_step": round(fms * 1e3, 2),
                  "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
-                 "k_decode_avg_us": round(fdec / max(fn, 1) * 1e3, 2),
-                 "k_decode_GBps": round(decode_bytes_per_launch(shape, poss, L) /
-                                        (fdec / max(fn, 1) * 1e-3) / 1e9, 2),
-                 "launches_per_step": 4}
+                 "k_layer_avg_us": round(fdec / max(fn, 1) * 1e3, 2),
+                 "k_layer_GBps": round(launch_bytes(shape, poss, L) /
+                                       (fdec / max(fn, 1) * 1e-3) / 1e9, 2)}
         log(f"all layers in one call: {fms * 1e3:.1f} us/step, {fused['GBps']} GB/s")
 
     # Leave the layer-serial outputs in qw for the parity sample.
@@ -268,7 +268,7 @@ def main():
         cpu, parity = cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb)
 
     traffic = load_traffic(args.config)
-    roof = {"bound": "hbm", "kernel": "k_decode", "achieved": round(dec_gbps, 2),
+    roof = {"bound": "hbm", "kernel": "k_layer", "achieved": round(dec_gbps, 2),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
             "bytes_per_launch": dec_bytes, "avg_launch_us": round(dec_avg_ms * 1e3, 2),
             "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None}
@@ -284,7 +284,7 @@ def main():
                    "ctx_min": min(poss), "ctx_max": max(poss), "layers": L,
                    "n_heads": shape.n_heads, "n_kv_heads": shape.n_kv_heads,
                    "head_dim": shape.head_dim, "kv": "q8_0" if shape.kv_q8 else "f32",
-                   "step": "layer-serial: per layer one append, one decode, one combine launch",
+                   "step": "layer-serial: per layer one g2b_attn_layers call = k_layer + k_combine",
                    "parallelism": "single GPU"},
         "us_per_step": round(ms * 1e3, 2),
         "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),

@@ -182,23 +182,12 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   if (max_splits > 512)
     return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
 
-  if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              kWavesPerSplit * (size_t)(kPartHead + hd);
   if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
-
-  AppendParams ap{};
-  ap.sh = c->sh;
-  ap.seqs = d_seqs;
-  ap.one = one;
-  ap.n_seq = n_seq;
-  ap.layer0 = layer0;
-  ap.q_in = q;
-  ap.q_rot = c->qrot;
-  ap.k_in = k;
-  ap.v_in = v;
-  ap.rope = c->rope;
-  G2B_HIP(c, launch_append_batch(ap, n_layers, c->stream));
+  if (!fast) {
+    if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
+  }
 
   DecodeParams dp{};
   dp.sh = c->sh;
@@ -210,6 +199,10 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.max_splits = max_splits;
   dp.q_rot = c->qrot;
   dp.q_out = q;
+  dp.q_in = q;
+  dp.k_in = k;
+  dp.v_in = v;
+  dp.rope = c->rope;
   dp.part = c->part;
   dp.att = att;
   dp.att_stride = att_stride;
@@ -218,6 +211,21 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
+
+  if (!fast) {  // generic shapes: append, decode, combine
+    AppendParams ap{};
+    ap.sh = c->sh;
+    ap.seqs = d_seqs;
+    ap.one = one;
+    ap.n_seq = n_seq;
+    ap.layer0 = layer0;
+    ap.q_in = q;
+    ap.q_rot = c->qrot;
+    ap.k_in = k;
+    ap.v_in = v;
+    ap.rope = c->rope;
+    G2B_HIP(c, launch_append_batch(ap, n_layers, c->stream));
+  }
   int used_fast = 0;
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
   if (c->prof) {

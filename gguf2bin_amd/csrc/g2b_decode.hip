@@ -22,6 +22,7 @@
 // (seq, layer, head), writes the output over q (as l5_model.c:541-557 does)
 // and, when asked, turns the stored scores into the reference's
 // att[h*ctx+t] weights.
+#include <algorithm>
 #include <type_traits>
 
 #include "g2b_internal.h"
@@ -85,6 +86,11 @@ struct Codec<0, 16> {
 #pragma unroll
     for (int i = 0; i < 4; i++) r.x[i] = gload<f32x4>(row + o.o0 + 16 * i);
   }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const float *p = reinterpret_cast<const float *>(row + o.o0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.x[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
+  }
   static __device__ __forceinline__ void values(const Raw &r, float (&f)[16]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -123,6 +129,12 @@ struct Codec<1, 32> {
     r.b = gload<u32x4>(p + 16);
     r.c = gload<uint32_t>(p + 32);
   }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + o.o0);
+    r.a = u32x4{p[0], p[1], p[2], p[3]};
+    r.b = u32x4{p[4], p[5], p[6], p[7]};
+    r.c = p[8];
+  }
   // the 32 int8 quants as 8 aligned dwords, and the block scale
   static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[8], float &scale,
                                                 const LaneOff &o) {
@@ -159,6 +171,12 @@ struct Codec<1, 16> {
     r.s = gload<uint32_t>(row + o.o0);
     r.a = gload<u32x4>(row + o.o1);
     r.c = gload<uint32_t>(row + o.o2);
+  }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    r.s = *reinterpret_cast<const uint32_t *>(row + o.o0);
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + o.o1);
+    r.a = u32x4{p[0], p[1], p[2], p[3]};
+    r.c = *reinterpret_cast<const uint32_t *>(row + o.o2);
   }
   static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[4], float &scale,
                                                 const LaneOff &o) {
@@ -232,19 +250,76 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
+// The new row of the workgroup that owns position pos: RoPE(k), then F32 copy
+// or Q8_0 quantisation of k and v into LDS (rowk, rowv), then a copy of both
+// rows to the caches.  The workgroup later reads pos from LDS, so no other
+// workgroup and no cache level is involved.  Every thread calls it.
+__device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
+                                      const float *k, const float *v, const float *rope,
+                                      float *kr, uint8_t *rowk, uint8_t *rowv) {
+  const int hd = sh.head_dim, half = hd / 2;
+  const int nkv = sh.n_kv_heads * hd;
+  const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
+  for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
+  __syncthreads();
+  if (cs) {
+    for (int p = threadIdx.x; p < sh.n_kv_heads * half; p += blockDim.x) {
+      const int h = p / half, j = p - h * half;
+      int ia, ib;
+      rope_pair_index(sh.arch_llama, j, half, ia, ib);
+      rope_pair(kr[h * hd + ia], kr[h * hd + ib], cs[2 * j], cs[2 * j + 1]);
+    }
+  }
+  __syncthreads();
+  if (sh.kv_q8) {
+    const int nb = (nkv + 31) / 32;
+    for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
+      const bool is_k = b < nb;
+      const int bb = is_k ? b : b - nb;
+      const int cnt = min(32, nkv - 32 * bb);
+      q8_quant_block(is_k ? kr + 32 * bb : v + 32 * bb, cnt, (is_k ? rowk : rowv) + 34 * bb);
+    }
+  } else {
+    float *fk = reinterpret_cast<float *>(rowk), *fv = reinterpret_cast<float *>(rowv);
+    for (int e = threadIdx.x; e < nkv; e += blockDim.x) {
+      fk[e] = kr[e];
+      fv[e] = v[e];
+    }
+  }
+  __syncthreads();
+  const size_t off = ((size_t)layer * (size_t)sd.ctx_cap + (size_t)pos) * sh.row_bytes;
+  uint32_t *gk = reinterpret_cast<uint32_t *>(sd.k + off);
+  uint32_t *gv = reinterpret_cast<uint32_t *>(sd.v + off);
+  const uint32_t *lk = reinterpret_cast<const uint32_t *>(rowk);
+  const uint32_t *lv = reinterpret_cast<const uint32_t *>(rowv);
+  for (uint32_t i = threadIdx.x; i < sh.row_bytes / 4; i += blockDim.x) {
+    gk[i] = lk[i];
+    gv[i] = lv[i];
+  }
+}
+
+// Specialised shapes: workgroup (split, seq, layer) rotates its q into LDS,
+// appends the new row if its split holds pos (and reads that row back from
+// LDS, not HBM), streams its positions and writes one partial per wave and
+// head; k_combine merges the partials and writes the output over q
+// (l5_model.c:513-578).  A merge inside this kernel (last workgroup of a
+// (seq, layer) by an atomic counter) measured slower: its agent-scope fences
+// and the merge at the tail of every launch cost more than one more launch.
 // FMT: 0 = F32 KV, 1 = Q8_0 KV.  HD: head_dim.  CD: elements per lane.
 // G: q heads per KV head.  U: wave-steps in flight per loop trip.
-// ATT: also store each score for the reference-layout weight output.
+// ATT: also write the raw scores for the reference-layout softmax weights.
 template <int FMT, int HD, int CD, int G, int U, bool ATT>
-__global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
+__global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
+  extern __shared__ __align__(16) uint8_t lds[];
   constexpr int LPH = HD / CD;  // lanes per head
   using C = Codec<FMT, CD>;
   const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
   const int npos = sd.pos + 1;
   const int t0 = split * P.split_len;
-  if (t0 >= npos) return;
+  if (t0 >= npos) return;  // a shorter sequence of a ragged batch: no split here
   const int t1 = min(npos, t0 + P.split_len);
+  const bool owns_new = t1 == npos;  // this split holds position pos
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -257,32 +332,57 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
   const int g = r / LPH, c = r - g * LPH;
   const int layer = P.layer0 + li;
   const int n_heads = P.sh.n_heads;
+  const int nkv = P.sh.n_kv_heads * HD;
+  const size_t nq = (size_t)n_heads * HD;
   const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const size_t row = P.sh.row_bytes;
+  const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+
+  // LDS: rotated q (nq floats), rotated new k (nkv floats), new K and V rows
+  float *qrot = reinterpret_cast<float *>(lds);
+  float *kr = reinterpret_cast<float *>(lds + nq * 4);
+  uint8_t *rowk = lds + nq * 4 + (((size_t)nkv * 4 + 15) & ~(size_t)15);
+  uint8_t *rowv = rowk + ((row + 15) & ~(size_t)15);
+  {
+    // RoPE(q) for every head, pair by pair as the append does (l3_math.c:74-101)
+    const float *qi = P.q_in + sidx * nq;
+    constexpr int half = HD / 2;
+    for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
+      const int h = pr / half, j = pr - h * half;
+      int ia, ib;
+      rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
+      float a = qi[h * HD + ia], b = qi[h * HD + ib];
+      if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+      qrot[h * HD + ia] = a;
+      qrot[h * HD + ib] = b;
+    }
+  }
+  if (owns_new)  // (its barriers also publish qrot)
+    append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope, kr,
+                   rowk, rowv);
+  else
+    __syncthreads();
 
   float q[G][CD];
-  {
-    const float *qs =
-        P.q_rot + sidx * (size_t)(n_heads * HD) + (size_t)(g * G) * HD + (size_t)c * CD;
 #pragma unroll
-    for (int i = 0; i < G; i++)
+  for (int i = 0; i < G; i++)
 #pragma unroll
-      for (int j = 0; j < CD; j += 4) {
-        const float4 v4 = *reinterpret_cast<const float4 *>(qs + i * HD + j);
-        q[i][j + 0] = v4.x * P.qscale;
-        q[i][j + 1] = v4.y * P.qscale;
-        q[i][j + 2] = v4.z * P.qscale;
-        q[i][j + 3] = v4.w * P.qscale;
-      }
-  }
+    for (int j = 0; j < CD; j += 4) {
+      const float4 v4 =
+          *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
+      q[i][j + 0] = v4.x * P.qscale;
+      q[i][j + 1] = v4.y * P.qscale;
+      q[i][j + 2] = v4.z * P.qscale;
+      q[i][j + 3] = v4.w * P.qscale;
+    }
   [[maybe_unused]] QDigits<CD> qd[G];
   if constexpr (FMT == 1) {
 #pragma unroll
     for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
   }
   const LaneOff lo = C::offsets(g * HD + c * CD);
-  const size_t row = P.sh.row_bytes;
-  const int stride = kWavesPerSplit * PPW;           // positions between a wave's steps
-  const size_t ustep = (size_t)stride * row;         // bytes between them
+  const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
+  const size_t ustep = (size_t)stride * row;  // bytes between them
   const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
   const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
 
@@ -298,32 +398,18 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
   if constexpr (ATT)
     att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
 
-  // One loop trip: U wave-steps of this wave.  CHECK masks positions >= t1
-  // (only the last trip of a split needs it).
-  auto trip = [&](int tb, auto check) {
+  // Scores, online softmax and V for UU positions already loaded.
+  auto consume = [&](const typename C::Raw *kr_, const typename C::Raw *vr_, const bool *valid,
+                     const int *tpos, auto nu, auto check) {
+    constexpr int UU = decltype(nu)::value;
     constexpr bool CHECK = decltype(check)::value;
-    typename C::Raw kr[U], vr[U];
-    bool valid[U];
-    const size_t base = (size_t)(tb + slot_ld) * row;
+    float sc[UU][G];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      size_t off = base + (size_t)u * ustep;
-      if constexpr (CHECK) {
-        valid[u] = lane_on && tb + u * stride + slot < t1;
-        if (!valid[u]) off = (size_t)t0 * row;
-      } else {
-        valid[u] = true;
-      }
-      C::load(kr[u], kb + off, lo);
-      C::load(vr[u], vb + off, lo);
-    }
-    float sc[U][G];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
+    for (int u = 0; u < UU; u++) {
       if constexpr (FMT == 1) {
         uint32_t w[CD / 4];
         float ks;
-        C::quants(kr[u], w, ks, lo);
+        C::quants(kr_[u], w, ks, lo);
 #pragma unroll
         for (int i = 0; i < G; i++) {
           const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
@@ -331,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
         }
       } else {
         float kf[CD];
-        C::values(kr[u], kf);
+        C::values(kr_[u], kf);
 #pragma unroll
         for (int i = 0; i < G; i++) {
           float s0 = 0.f, s1 = 0.f;
@@ -351,7 +437,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
     for (int i = 0; i < G; i++) {
       float mx = m[i];
 #pragma unroll
-      for (int u = 0; u < U; u++) mx = fmaxf(mx, sc[u][i]);
+      for (int u = 0; u < UU; u++) mx = fmaxf(mx, sc[u][i]);
       mn[i] = mx;
       need |= mx > m[i];
     }
@@ -366,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; u++) {
+    for (int u = 0; u < UU; u++) {
       float p[G];
 #pragma unroll
       for (int i = 0; i < G; i++) {
@@ -376,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
       if constexpr (FMT == 1) {
         uint32_t w[CD / 4];
         float vs;
-        C::quants(vr[u], w, vs, lo);
+        C::quants(vr_[u], w, vs, lo);
         float pv[G];
 #pragma unroll
         for (int i = 0; i < G; i++) pv[i] = p[i] * vs;
@@ -390,26 +476,58 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
           }
       } else {
         float vf[CD];
-        C::values(vr[u], vf);
+        C::values(vr_[u], vf);
 #pragma unroll
         for (int j = 0; j < CD; j++)
 #pragma unroll
           for (int i = 0; i < G; i++) acc[i][j] = fmaf(p[i], vf[j], acc[i][j]);
       }
       if constexpr (ATT) {
-        const int t = tb + u * stride + slot;
-        if (c == 0 && valid[u] && lane_on && t < t1) {
+        if (c == 0 && valid[u]) {
 #pragma unroll
-          for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + t] = sc[u][i];
+          for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tpos[u]] = sc[u][i];
         }
       }
     }
   };
 
+  // Positions [t0, tend) stream from HBM; pos itself, when owned, from LDS.
+  const int tend = owns_new ? t1 - 1 : t1;
+  auto trip = [&](int tb, auto check) {
+    constexpr bool CHECK = decltype(check)::value;
+    typename C::Raw krr[U], vrr[U];
+    bool valid[U];
+    int tpos[U];
+    const size_t base = (size_t)(tb + slot_ld) * row;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      size_t off = base + (size_t)u * ustep;
+      tpos[u] = tb + u * stride + slot;
+      if constexpr (CHECK) {
+        valid[u] = lane_on && tpos[u] < tend;
+        if (!valid[u]) off = (size_t)t0 * row;
+      } else {
+        valid[u] = lane_on;
+      }
+      C::load(krr[u], kb + off, lo);
+      C::load(vrr[u], vb + off, lo);
+    }
+    consume(krr, vrr, valid, tpos, std::integral_constant<int, U>{}, check);
+  };
   const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
   int tb = t0 + wave * PPW;
-  for (; tb + trip_span <= t1; tb += stride * U) trip(tb, std::false_type{});
-  for (; tb < t1; tb += stride * U) trip(tb, std::true_type{});
+  if (tend > t0) {  // (a split of one position may hold only pos)
+    for (; tb + trip_span <= tend; tb += stride * U) trip(tb, std::false_type{});
+    for (; tb < tend; tb += stride * U) trip(tb, std::true_type{});
+  }
+  if (owns_new) {
+    typename C::Raw krr[1], vrr[1];
+    C::load_lds(krr[0], rowk, lo);
+    C::load_lds(vrr[0], rowv, lo);
+    const bool valid[1] = {wave == 0 && slot == 0};
+    const int tpos[1] = {sd.pos};
+    consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
+  }
 
   // Fold the PPW position slots of the wave into slot 0.  Every lane takes
   // part in the shuffles, but only slot-0 lanes update their state, so the
@@ -432,14 +550,14 @@ __global__ __launch_bounds__(kThreads) void k_decode(DecodeParams P) {
       m[i] = gather ? M : m[i];
     }
   }
+  const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
+  const size_t pstr = (size_t)(kPartHead + HD);
   if (slot == 0) {
-    const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
 #pragma unroll
     for (int i = 0; i < G; i++) {
       const int h = g * G + i;
       float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * nparts +
-                            (size_t)split * kWavesPerSplit + (size_t)wave) *
-                               (size_t)(kPartHead + HD);
+                            (size_t)split * kWavesPerSplit + (size_t)wave) * pstr;
       if (c == 0) {
         pp[0] = m[i];
         pp[1] = l[i];
@@ -580,13 +698,21 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
 
 // ---------------------------------------------------------------- dispatch
 
+size_t layer_lds_bytes(const ShapeDev &sh) {
+  const size_t nq = (size_t)sh.n_heads * sh.head_dim;
+  const size_t nkv = (size_t)sh.n_kv_heads * sh.head_dim;
+  const size_t a = (nkv * 4 + 15) & ~(size_t)15, rb = ((size_t)sh.row_bytes + 15) & ~(size_t)15;
+  return nq * 4 + a + 2 * rb;
+}
+
 template <int FMT, int HD, int CD, int G, int U>
 static hipError_t launch_fast_u(const DecodeParams &p, int n_layers, hipStream_t s) {
   dim3 grid(p.max_splits, p.n_seq, n_layers);
+  const size_t lds = layer_lds_bytes(p.sh);
   if (p.att)
-    hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U, true>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true>), grid, dim3(kThreads), lds, s, p);
   else
-    hipLaunchKernelGGL((k_decode<FMT, HD, CD, G, U, false>), grid, dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, false>), grid, dim3(kThreads), lds, s, p);
   return hipGetLastError();
 }
 
@@ -626,10 +752,10 @@ static int fast_chunk(const ShapeDev &sh) {
 }
 
 template <int FMT, int HD, int CD, int G>
-static int occ_of() {
+static int occ_of(const ShapeDev &sh) {
   int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode<FMT, HD, CD, G, 2, false>,
-                                                   kThreads, 0) != hipSuccess) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_layer<FMT, HD, CD, G, 2, false>,
+                                                   kThreads, layer_lds_bytes(sh)) != hipSuccess) {
     (void)hipGetLastError();
     return 1;
   }
@@ -650,17 +776,17 @@ int decode_blocks_per_cu(const ShapeDev &sh) {
   const bool hd128 = sh.head_dim == 128;
   if (sh.kv_q8) {
     switch (group) {
-      case 1: return hd128 ? occ_of<1, 128, 32, 1>() : occ_of<1, 64, 32, 1>();
-      case 2: return hd128 ? occ_of<1, 128, 32, 2>() : occ_of<1, 64, 32, 2>();
-      case 3: return hd128 ? occ_of<1, 128, 16, 3>() : occ_of<1, 64, 16, 3>();
-      default: return hd128 ? occ_of<1, 128, 16, 4>() : occ_of<1, 64, 16, 4>();
+      case 1: return hd128 ? occ_of<1, 128, 32, 1>(sh) : occ_of<1, 64, 32, 1>(sh);
+      case 2: return hd128 ? occ_of<1, 128, 32, 2>(sh) : occ_of<1, 64, 32, 2>(sh);
+      case 3: return hd128 ? occ_of<1, 128, 16, 3>(sh) : occ_of<1, 64, 16, 3>(sh);
+      default: return hd128 ? occ_of<1, 128, 16, 4>(sh) : occ_of<1, 64, 16, 4>(sh);
     }
   }
   switch (group) {
-    case 1: return hd128 ? occ_of<0, 128, 16, 1>() : occ_of<0, 64, 16, 1>();
-    case 2: return hd128 ? occ_of<0, 128, 16, 2>() : occ_of<0, 64, 16, 2>();
-    case 3: return hd128 ? occ_of<0, 128, 16, 3>() : occ_of<0, 64, 16, 3>();
-    default: return hd128 ? occ_of<0, 128, 16, 4>() : occ_of<0, 64, 16, 4>();
+    case 1: return hd128 ? occ_of<0, 128, 16, 1>(sh) : occ_of<0, 64, 16, 1>(sh);
+    case 2: return hd128 ? occ_of<0, 128, 16, 2>(sh) : occ_of<0, 64, 16, 2>(sh);
+    case 3: return hd128 ? occ_of<0, 128, 16, 3>(sh) : occ_of<0, 64, 16, 3>(sh);
+    default: return hd128 ? occ_of<0, 128, 16, 4>(sh) : occ_of<0, 64, 16, 4>(sh);
   }
 }
 

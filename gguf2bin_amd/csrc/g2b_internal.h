@@ -15,7 +15,7 @@ namespace g2b {
 constexpr int kPartHead = 4;
 constexpr int kWavesPerSplit = 4;      // one partial per wave of a 256-thread split
 constexpr int kThreads = 256;
-constexpr int kGenericMaxSplit = 1024; // positions per split in the generic kernel
+constexpr int kGenericMaxSplit = 1024;  // positions per split in the generic kernel
 
 
 struct AppendParams {
@@ -37,8 +37,12 @@ struct DecodeParams {
   SeqDev one;
   int32_t n_seq, layer0;
   int32_t split_len, max_splits;
-  const float *q_rot;  // [L][n_seq][nq]
+  const float *q_rot;  // [L][n_seq][nq] rotated q (generic path)
   float *q_out;        // [L][n_seq][nq]: the output overwrites q
+  const float *q_in;   // [L][n_seq][nq] pre-RoPE q (single-launch path; == q_out)
+  const float *k_in;   // [L][n_seq][nkv] pre-RoPE new k (single-launch path)
+  const float *v_in;   // [L][n_seq][nkv] new v (single-launch path)
+  const float *rope;   // [rope_len][head_dim] cos/sin pairs, or nullptr
   float *part;         // [L][n_seq][n_heads][max_splits*kWavesPerSplit][kPartHead+hd]
   float *att;          // nullable: [L][n_seq][n_heads][att_stride]
   int32_t att_stride;
@@ -50,7 +54,9 @@ struct DecodeParams {
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_append_batch(const AppendParams &p, int n_layers, hipStream_t s);
 hipError_t launch_append_rows(const AppendParams &p, int layer, int n_rows, hipStream_t s);
-// Picks the specialised kernel for the shape when there is one, else the generic one.
+// Specialised shapes: one launch does RoPE, append and attention (k_layer).
+// Generic shapes: launch_append_batch, then this (k_decode_generic).  Both
+// are followed by launch_combine.  *used_fast tells which ran.
 // Returns hipErrorInvalidValue when split_len is too large for the generic kernel.
 hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int *used_fast);
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
