@@ -28,7 +28,7 @@ ARCH_LLAMA, ARCH_QWEN2, ARCH_QWEN3 = 0, 1, 2
 EXPORTS = [
     "g2b_ctx_create", "g2b_ctx_destroy", "g2b_ctx_set_stream", "g2b_ctx_stream",
     "g2b_strerror", "g2b_ctx_last_error", "g2b_kv_row_bytes", "g2b_kv_bytes",
-    "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows",
+    "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows", "g2b_set_qk_norm",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
             "g2b_kv_alloc": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], C.c_int),
             "g2b_kv_free": ([vp, vp, vp], C.c_int),
             "g2b_kv_append_rows": ([vp, vp, vp, i32, i32, i32, i32, fp, fp], C.c_int),
+            "g2b_set_qk_norm": ([vp, i32, vp, vp, C.c_float], C.c_int),
             "g2b_batch_begin": ([vp, i32, C.POINTER(_Seq)], C.c_int),
             "g2b_attn_layers": ([vp, i32, i32, fp, fp, fp, fp, i32], C.c_int),
             "g2b_attn_forward": ([vp, i32, i32, i32, vp, vp, fp, fp, fp, fp], C.c_int),
@@ -211,6 +212,23 @@ class Context:
                        n_rows: int, k_dev: int, v_dev: int):
         self._check(lib().g2b_kv_append_rows(self.h, kc, vc, ctx_cap, layer, pos0, n_rows,
                                              k_dev, v_dev), "g2b_kv_append_rows")
+
+    def set_qk_norm(self, layer: int, q_norm=None, k_norm=None, eps: float = 1e-6):
+        """QK-RMSNorm weights of one layer (host arrays of head_dim floats, or
+        None), as model_forward applies them under F_QK_NORM."""
+        keep = []
+        ptrs = []
+        for w in (q_norm, k_norm):
+            if w is None:
+                ptrs.append(None)
+                continue
+            a = np.ascontiguousarray(w, np.float32).reshape(-1)
+            if a.size != self.shape.head_dim:
+                raise ValueError(f"norm weights: {a.size} floats, head_dim {self.shape.head_dim}")
+            keep.append(a)
+            ptrs.append(a.ctypes.data)
+        self._check(lib().g2b_set_qk_norm(self.h, layer, ptrs[0], ptrs[1], eps),
+                    "g2b_set_qk_norm")
 
     # ---- the path ----
     def batch_begin(self, seqs: Sequence[tuple]):

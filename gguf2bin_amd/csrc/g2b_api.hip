@@ -2,8 +2,9 @@
 //
 // Host-side control of the decode-attention path: shape validation, KV
 // buffers in HBM with the reference layout, the RoPE table (built on the host
-// by g2b_rope_table), staging of batch descriptors, split sizing and the
-// three launches per call (append, decode, combine).  Nothing here computes
+// by g2b_rope_table), QK-RMSNorm weights, staging of batch descriptors,
+// split sizing and the launches per call (k_layer + k_combine, or append,
+// generic decode and combine for shapes without a specialised kernel).  Nothing here computes
 // attention on the CPU: if the device path cannot run, the call fails.
 #include <math.h>
 #include <stdarg.h>
@@ -45,6 +46,12 @@ struct g2b_ctx {
   size_t part_cap = 0;
   float *hstage = nullptr;  // device staging for the *_host entry point
   size_t hstage_cap = 0;
+
+  // QK-RMSNorm weights (g2b_set_qk_norm)
+  float *qkn_w = nullptr;       // device [n_layers][2][head_dim]
+  int32_t *qkn_on = nullptr;    // device [n_layers]: bit 0 q, bit 1 k
+  std::vector<int32_t> qkn_on_h;
+  float qkn_eps = 0.f;
 
   int32_t slots = 0;           // resident decode workgroups on the device
   int32_t split_override = 0;  // g2b_ctx_tune
@@ -109,6 +116,16 @@ int grow(g2b_ctx *c, float **buf, size_t *cap, size_t need_floats) {
   }
   *cap = n;
   return G2B_OK;
+}
+
+NormDev norm_of(const g2b_ctx *c) {
+  NormDev n{};
+  bool any = false;
+  for (int32_t f : c->qkn_on_h) any |= f != 0;
+  n.w = any ? c->qkn_w : nullptr;
+  n.on = c->qkn_on;
+  n.eps = c->qkn_eps;
+  return n;
 }
 
 int ensure_rope(g2b_ctx *c, int32_t len) {
@@ -203,6 +220,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.k_in = k;
   dp.v_in = v;
   dp.rope = c->rope;
+  dp.norm = norm_of(c);
   dp.part = c->part;
   dp.att = att;
   dp.att_stride = att_stride;
@@ -224,6 +242,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     ap.k_in = k;
     ap.v_in = v;
     ap.rope = c->rope;
+    ap.norm = norm_of(c);
     G2B_HIP(c, launch_append_batch(ap, n_layers, c->stream));
   }
   int used_fast = 0;
@@ -285,7 +304,7 @@ int g2b_ctx_create(g2b_ctx **out, int32_t device, const g2b_shape *s) {
   if (s->n_layers < 1 || s->n_heads < 1 || s->n_kv_heads < 1 || s->head_dim < 2 ||
       (s->head_dim & 1) || s->n_heads % s->n_kv_heads)
     return G2B_EINVAL;
-  if ((int64_t)s->n_kv_heads * s->head_dim > 16384) return G2B_EUNSUP;  // append LDS
+  if ((int64_t)s->n_kv_heads * s->head_dim + s->n_heads > 16384) return G2B_EUNSUP;  // append LDS
   int ndev = 0;
   if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev) {
     (void)hipGetLastError();
@@ -334,6 +353,8 @@ int g2b_ctx_destroy(g2b_ctx *c) {
   if (c->qrot) (void)hipFree(c->qrot);
   if (c->part) (void)hipFree(c->part);
   if (c->hstage) (void)hipFree(c->hstage);
+  if (c->qkn_w) (void)hipFree(c->qkn_w);
+  if (c->qkn_on) (void)hipFree(c->qkn_on);
   if (c->seqs_ev) (void)hipEventDestroy(c->seqs_ev);
   for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -406,8 +427,45 @@ int g2b_kv_append_rows(g2b_ctx *c, void *kc, void *vc, int32_t ctx_cap, int32_t 
   ap.k_in = k;
   ap.v_in = v;
   ap.rope = c->rope;
+  ap.norm = norm_of(c);
   ap.pos0 = pos0;
   G2B_HIP(c, launch_append_rows(ap, layer, n_rows, c->stream));
+  return G2B_OK;
+}
+
+int g2b_set_qk_norm(g2b_ctx *c, int32_t layer, const float *q_norm, const float *k_norm,
+                    float eps) {
+  if (!c) return G2B_EINVAL;
+  if (layer < 0 || layer >= c->shape.n_layers)
+    return fail(c, G2B_EINVAL, "layer %d outside [0,%d)", layer, c->shape.n_layers);
+  const int32_t L = c->shape.n_layers, hd = c->shape.head_dim;
+  bool others = false;
+  for (int32_t i = 0; i < (int32_t)c->qkn_on_h.size(); i++) others |= i != layer && c->qkn_on_h[i];
+  if (others && memcmp(&eps, &c->qkn_eps, sizeof eps) != 0)
+    return fail(c, G2B_EINVAL, "eps %g differs from %g set for other layers (one per model)",
+                (double)eps, (double)c->qkn_eps);
+  if (int rc = set_device(c)) return rc;
+  if (!c->qkn_w) {
+    if (hipMalloc((void **)&c->qkn_w, (size_t)L * 2 * hd * sizeof(float)) != hipSuccess ||
+        hipMalloc((void **)&c->qkn_on, (size_t)L * sizeof(int32_t)) != hipSuccess) {
+      (void)hipGetLastError();
+      if (c->qkn_w) (void)hipFree(c->qkn_w);
+      c->qkn_w = nullptr;
+      return fail(c, G2B_ENOMEM, "QK-norm weights");
+    }
+    c->qkn_on_h.assign((size_t)L, 0);
+    G2B_HIP(c, hipMemset(c->qkn_on, 0, (size_t)L * sizeof(int32_t)));
+  }
+  // Calls already queued may read the weights: let them finish first.
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  float *wl = c->qkn_w + (size_t)layer * 2 * hd;
+  if (q_norm) G2B_HIP(c, hipMemcpy(wl, q_norm, (size_t)hd * sizeof(float), hipMemcpyHostToDevice));
+  if (k_norm)
+    G2B_HIP(c, hipMemcpy(wl + hd, k_norm, (size_t)hd * sizeof(float), hipMemcpyHostToDevice));
+  const int32_t on = (q_norm ? 1 : 0) | (k_norm ? 2 : 0);
+  G2B_HIP(c, hipMemcpy(c->qkn_on + layer, &on, sizeof on, hipMemcpyHostToDevice));
+  c->qkn_on_h[(size_t)layer] = on;
+  c->qkn_eps = eps;
   return G2B_OK;
 }
 

@@ -250,18 +250,21 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
-// The new row of the workgroup that owns position pos: RoPE(k), then F32 copy
+// The new row of the workgroup that owns position pos: [QK-RMSNorm,] RoPE(k), then F32 copy
 // or Q8_0 quantisation of k and v into LDS (rowk, rowv), then a copy of both
 // rows to the caches.  The workgroup later reads pos from LDS, so no other
 // workgroup and no cache level is involved.  Every thread calls it.
 __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
                                       const float *k, const float *v, const float *rope,
-                                      float *kr, uint8_t *rowk, uint8_t *rowv) {
+                                      const NormDev &norm, float *kr, uint8_t *rowk,
+                                      uint8_t *rowv, float *inv) {
   const int hd = sh.head_dim, half = hd / 2;
   const int nkv = sh.n_kv_heads * hd;
   const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
   for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
   __syncthreads();
+  if (const float *wk = norm_weights(norm, layer, 1, hd))
+    qk_rmsnorm_block(kr, sh.n_kv_heads, hd, wk, norm.eps, inv);
   if (cs) {
     for (int p = threadIdx.x; p < sh.n_kv_heads * half; p += blockDim.x) {
       const int h = p / half, j = p - h * half;
@@ -338,14 +341,23 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   const size_t row = P.sh.row_bytes;
   const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
 
-  // LDS: rotated q (nq floats), rotated new k (nkv floats), new K and V rows
+  // LDS: rotated q (nq floats), rotated new k (nkv floats), new K and V rows,
+  // QK-RMSNorm scratch (n_heads floats)
   float *qrot = reinterpret_cast<float *>(lds);
   float *kr = reinterpret_cast<float *>(lds + nq * 4);
   uint8_t *rowk = lds + nq * 4 + (((size_t)nkv * 4 + 15) & ~(size_t)15);
   uint8_t *rowv = rowk + ((row + 15) & ~(size_t)15);
+  float *inv = reinterpret_cast<float *>(rowv + ((row + 15) & ~(size_t)15));
   {
-    // RoPE(q) for every head, pair by pair as the append does (l3_math.c:74-101)
+    // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by pair
+    // as the append does (l3_math.c:74-101)
     const float *qi = P.q_in + sidx * nq;
+    if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
+      for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
+      __syncthreads();
+      qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, inv);
+      qi = qrot;  // rotate in place: each pair is read and written by one thread
+    }
     constexpr int half = HD / 2;
     for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
       const int h = pr / half, j = pr - h * half;
@@ -358,8 +370,8 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     }
   }
   if (owns_new)  // (its barriers also publish qrot)
-    append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope, kr,
-                   rowk, rowv);
+    append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
+                   P.norm, kr, rowk, rowv, inv);
   else
     __syncthreads();
 
@@ -702,7 +714,7 @@ size_t layer_lds_bytes(const ShapeDev &sh) {
   const size_t nq = (size_t)sh.n_heads * sh.head_dim;
   const size_t nkv = (size_t)sh.n_kv_heads * sh.head_dim;
   const size_t a = (nkv * 4 + 15) & ~(size_t)15, rb = ((size_t)sh.row_bytes + 15) & ~(size_t)15;
-  return nq * 4 + a + 2 * rb;
+  return nq * 4 + a + 2 * rb + (size_t)sh.n_heads * 4;
 }
 
 template <int FMT, int HD, int CD, int G, int U>

@@ -30,6 +30,49 @@ struct ShapeDev {
   uint32_t row_bytes;
 };
 
+// Per-layer QK-RMSNorm weights as the kernels read them (w == nullptr: no
+// layer has any).
+struct NormDev {
+  const float *w;      // [n_layers][2][head_dim]: q weights, then k weights
+  const int32_t *on;   // [n_layers]: bit 0 q, bit 1 k
+  float eps;
+};
+
+__device__ __forceinline__ const float *norm_weights(const NormDev &n, int layer, int which,
+                                                     int hd) {
+  if (!n.w || !((n.on[layer] >> which) & 1)) return nullptr;
+  return n.w + ((size_t)layer * 2 + (size_t)which) * (size_t)hd;
+}
+
+// QK-RMSNorm of /root/reference/src/l3_math.c:107-114 on n_heads heads of x,
+// in place.  One thread per head sums the squares left to right with each
+// product rounded (no contraction, as the reference's -std=c99 build), then
+// inv = 1/sqrtf(ss/hd + eps) with IEEE division and square root, then
+// x = (w*x)*inv elementwise.  The square root is sqrtf(), which
+// -fhip-fp32-correctly-rounded-divide-sqrt makes correctly rounded on gfx950
+// (v_sqrt_f32 plus a residual check of both neighbours); __fsqrt_rn compiles
+// to the bare 1-ulp v_sqrt_f32 and would differ from the host's sqrtss.  x is LDS, or global memory that only this block
+// touches; inv is LDS scratch of n_heads floats.  Every thread calls it.
+__device__ inline void qk_rmsnorm_block(float *x, int n_heads, int hd, const float *w,
+                                        float eps, float *inv) {
+  for (int h = threadIdx.x; h < n_heads; h += blockDim.x) {
+    const float *xh = x + (size_t)h * hd;
+    float ss = 0.f;
+    for (int j = 0; j < hd; j++) {
+      const float sq = xh[j] * xh[j];
+      ss = ss + sq;
+    }
+    inv[h] = __fdiv_rn(1.f, sqrtf(__fdiv_rn(ss, (float)hd) + eps));
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < n_heads * hd; e += blockDim.x) {
+    const int h = e / hd, j = e - h * hd;
+    const float wx = w[j] * x[e];
+    x[e] = wx * inv[h];
+  }
+  __syncthreads();
+}
+
 // Truncating fp32 -> fp16 of /root/reference/src/l3_math.c:6-16.
 __device__ __forceinline__ uint32_t f32_to_half_trunc(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -105,18 +148,29 @@ __device__ __forceinline__ void rope_pair_index(int arch_llama, int j, int half,
   ib = arch_llama ? 2 * j + 1 : j + half;
 }
 
-// RoPE(k) [and RoPE(q) into qr when q != nullptr] at `pos`, then store the
-// k and v rows at (layer, pos): l5_model.c:513-516 for one sequence.  Called
-// by every thread of the block; kr is LDS scratch of nkv floats.
+// [QK-RMSNorm, then] RoPE(k) [and the same for q into qr when q != nullptr]
+// at `pos`, then store the k and v rows at (layer, pos): l5_model.c:505-516
+// for one sequence.  Called by every thread of the block; kr is LDS scratch
+// of nkv floats, inv of n_heads floats.
 __device__ inline void append_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
-                           const float *k, const float *v, const float *q, float *qr,
-                           const float *rope, float *kr) {
+                                  const float *k, const float *v, const float *q, float *qr,
+                                  const float *rope, const NormDev &norm, float *kr,
+                                  float *inv) {
   const int hd = sh.head_dim, half = hd / 2;
   const int nkv = sh.n_kv_heads * hd;
   const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
+  const float *wq = q ? norm_weights(norm, layer, 0, hd) : nullptr;
+  const float *wk = norm_weights(norm, layer, 1, hd);
 
   for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
+  if (wq)
+    for (int e = threadIdx.x; e < sh.n_heads * hd; e += blockDim.x) qr[e] = q[e];
   __syncthreads();
+  if (wk) qk_rmsnorm_block(kr, sh.n_kv_heads, hd, wk, norm.eps, inv);
+  if (wq) {
+    qk_rmsnorm_block(qr, sh.n_heads, hd, wq, norm.eps, inv);
+    q = qr;  // rotate the normalised copy in place
+  }
   if (cs) {
     for (int p = threadIdx.x; p < sh.n_kv_heads * half; p += blockDim.x) {
       const int h = p / half, j = p - h * half;

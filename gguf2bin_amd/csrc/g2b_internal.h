@@ -28,6 +28,7 @@ struct AppendParams {
   const float *k_in;   // [L][n_seq][nkv]  or [n_rows][nkv] in row-prefill mode
   const float *v_in;
   const float *rope;   // [rope_len][head_dim] cos/sin pairs, or nullptr
+  NormDev norm;        // QK-RMSNorm weights (norm.w == nullptr: none)
   int32_t pos0;        // row-prefill mode: first position
 };
 
@@ -43,6 +44,7 @@ struct DecodeParams {
   const float *k_in;   // [L][n_seq][nkv] pre-RoPE new k (single-launch path)
   const float *v_in;   // [L][n_seq][nkv] new v (single-launch path)
   const float *rope;   // [rope_len][head_dim] cos/sin pairs, or nullptr
+  NormDev norm;        // QK-RMSNorm weights (norm.w == nullptr: none)
   float *part;         // [L][n_seq][n_heads][max_splits*kWavesPerSplit][kPartHead+hd]
   float *att;          // nullable: [L][n_seq][n_heads][att_stride]
   int32_t att_stride;

@@ -89,7 +89,8 @@ __global__ __launch_bounds__(kThreads) void k_synth_fill(SynthParams p) {
       vraw[2 * e2 + 1] = b;
     }
     __syncthreads();
-    append_row(p.sh, sd, layer, pos, kraw, vraw, nullptr, nullptr, p.rope, kr);
+    append_row(p.sh, sd, layer, pos, kraw, vraw, nullptr, nullptr, p.rope, NormDev{}, kr,
+               nullptr);  // synthetic rows stand for post-norm k: no QK-RMSNorm
     __syncthreads();
   }
 }

@@ -100,9 +100,22 @@ int g2b_kv_alloc(g2b_ctx *ctx, int32_t ctx_cap, void **kcache, void **vcache);
 /* free_rt's KV part (l5_model.c:117-118). */
 int g2b_kv_free(g2b_ctx *ctx, void *kcache, void *vcache);
 
-/* Prefill append: for t in [pos0, pos0+n_rows), RoPE k_t at position t and
- * store k_t, v_t at (layer, t) - the kv_store of l5_model.c:514-516 applied
- * row by row.  k, v: device, [n_rows][nkv] fp32, pre-RoPE. */
+/* QK-RMSNorm of one layer: with F_QK_NORM set, model_forward runs
+ * qk_rmsnorm (l3_math.c:107-114) on q with attn_q_norm and on the new k with
+ * attn_k_norm before RoPE, each when the layer has that slot
+ * (l5_model.c:505-511).  q_norm, k_norm: host arrays of head_dim floats
+ * (copied), or NULL for none; NULL for both turns the layer's norm off.
+ * eps is ModelCfg.eps, one value per model: a different eps while another
+ * layer has weights set is G2B_EINVAL.  Applies to every later call that
+ * touches the layer, the prefill append included.  Waits for the context's
+ * stream. */
+int g2b_set_qk_norm(g2b_ctx *ctx, int32_t layer, const float *q_norm, const float *k_norm,
+                    float eps);
+
+/* Prefill append: for t in [pos0, pos0+n_rows), [QK-RMSNorm and] RoPE k_t at
+ * position t and store k_t, v_t at (layer, t) - the kv_store of
+ * l5_model.c:505-516 applied row by row.  k, v: device, [n_rows][nkv] fp32,
+ * pre-norm and pre-RoPE. */
 int g2b_kv_append_rows(g2b_ctx *ctx, void *kcache, void *vcache, int32_t ctx_cap,
                        int32_t layer, int32_t pos0, int32_t n_rows,
                        const float *k, const float *v);
@@ -112,13 +125,15 @@ int g2b_kv_append_rows(g2b_ctx *ctx, void *kcache, void *vcache, int32_t ctx_cap
  * The batch stays current until the next g2b_batch_begin. */
 int g2b_batch_begin(g2b_ctx *ctx, int32_t n_seq, const g2b_seq *seqs);
 
-/* The decode-attention path (l5_model.c:513-578) for every sequence of the
+/* The decode-attention path (l5_model.c:505-578) for every sequence of the
  * current batch and layers [layer0, layer0+n_layers):
+ *   [QK-RMSNorm of q and k where g2b_set_qk_norm gave the layer weights]
  *   RoPE(q), RoPE(k) -> store k, v at (layer, pos) -> scores over t <= pos
  *   scaled by 1/sqrt(head_dim) -> softmax -> q := sum_t w_t v_t.
  * q: device [n_layers][n_seq][n_heads*head_dim], overwritten by the output
  * exactly as the reference overwrites q (l5_model.c:541-557).
- * k, v: device [n_layers][n_seq][n_kv_heads*head_dim], pre-RoPE; not written.
+ * k, v: device [n_layers][n_seq][n_kv_heads*head_dim], pre-norm and pre-RoPE;
+ * not written.
  * att: NULL, or device [n_layers][n_seq][n_heads][att_stride] receiving the
  * softmax weights of t <= pos in the reference att[h*ctx+t] layout
  * (l5_model.c:486,537,540); att_stride >= max pos+1 of the batch.

@@ -12,6 +12,7 @@
  *   /root/reference/src/l5_model.c:448-452 (RoPE dispatch by arch)
  *   /root/reference/src/l5_model.c:513-578 (scores, softmax, V-accumulate)
  *   /root/reference/src/l3_math.c:6-16,52-56,64-102 (fp16, softmax, RoPE)
+ *   /root/reference/src/l3_math.c:107-114  (QK-RMSNorm, l5_model.c:505-511)
  *   /root/reference/src/l2_codec.c:35-54   (fp16 -> fp32)
  * Built with the reference's own flags (-O3 -mavx2 -mfma -std=c99, no
  * -ffast-math) so that the AVX2 branch is reproduced bit for bit.
@@ -24,6 +25,9 @@
  *       exact .5 ties, +-127 clamp, NaN/Inf, partial block).
  *   orc_rope_table / orc_rope : goldens; pos 0 identity; per-pair norm;
  *       NEOX vs LLaMA pairing with one-hot inputs.
+ *   orc_qk_rmsnorm : goldens from the compiled reference (random heads and
+ *       special inputs); numpy float32 left-to-right accumulation; float64
+ *       closed form; forward goldens of model_forward with F_QK_NORM.
  *   orc_softmax / orc_attn_layer : goldens from the reference model_forward;
  *       float64 brute force on small cases; invariants (weights sum to 1,
  *       q = 0 gives uniform weights, constant V gives V).
@@ -70,6 +74,11 @@ void orc_q8_dequant_row(const uint8_t *src, float *out, int32_t n);
 int orc_rope_table(int32_t pos, int32_t head_dim, float theta, float *cs);
 void orc_rope(int32_t arch, float *x, int32_t len, int32_t pos, int32_t head_dim,
               float theta);
+
+/* ---- QK-RMSNorm (l3_math.c:107-114), applied before RoPE (l5_model.c:505-511) ---- */
+/* Per head h: ss = sum_j x_j*x_j (serial, each product rounded), inv =
+ * 1/sqrtf(ss/hd + eps), x_j := (w_j*x_j)*inv.  In place. */
+void orc_qk_rmsnorm(float *x, const float *w, int32_t n_heads, int32_t head_dim, float eps);
 
 /* ---- softmax (l3_math.c:52-56) ---- */
 void orc_softmax(float *x, int32_t n);

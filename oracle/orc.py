@@ -93,6 +93,7 @@ def lib() -> C.CDLL:
         L.orc_rope_table.restype = C.c_int
         L.orc_rope.argtypes = [C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float]
         L.orc_softmax.argtypes = [_f32p, C.c_int32]
+        L.orc_qk_rmsnorm.argtypes = [_f32p, _f32p, C.c_int32, C.c_int32, C.c_float]
         L.orc_kv_prefill.argtypes = [C.POINTER(OrcShape), C.c_int32, C.c_int32, C.c_int32,
                                      C.c_int32, _u8p, _u8p, _f32p, _f32p]
         L.orc_attn_layer.argtypes = [C.POINTER(OrcShape), C.c_int32, C.c_int32, C.c_int32,
@@ -179,6 +180,16 @@ def rope_table(pos: int, head_dim: int, theta: float) -> np.ndarray:
 def rope(arch: int, x: np.ndarray, pos: int, head_dim: int, theta: float) -> np.ndarray:
     y = np.ascontiguousarray(x, np.float32).copy().ravel()
     lib().orc_rope(arch, y, y.size, pos, head_dim, theta)
+    return y
+
+
+def qk_rmsnorm(x: np.ndarray, w: np.ndarray, n_heads: int, head_dim: int,
+               eps: float) -> np.ndarray:
+    """QK-RMSNorm of n_heads heads (l3_math.c:107-114); returns a new array."""
+    y = np.ascontiguousarray(x, np.float32).copy().reshape(-1)
+    ww = np.ascontiguousarray(w, np.float32).reshape(-1)
+    assert y.size >= n_heads * head_dim and ww.size >= head_dim
+    lib().orc_qk_rmsnorm(y, ww, n_heads, head_dim, eps)
     return y
 
 
@@ -272,20 +283,43 @@ def ref_lib(variant: str = "avx2"):
     L.ref_f32_to_half_n.argtypes = [_f32p, _u16p, C.c_size_t]
     L.ref_half_to_float_n.argtypes = [_u16p, _f32p, C.c_size_t]
     L.ref_softmax.argtypes = [_f32p, C.c_int32]
+    L.ref_qk_rmsnorm.argtypes = [_f32p, _f32p, C.c_int32, C.c_int32, C.c_float]
     L.ref_rope.argtypes = [C.c_int32, _f32p, C.c_int32, C.c_int32, C.c_int32, C.c_float]
     L.ref_forward_case.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                                    C.c_int32, C.c_int32, C.c_int32,
                                    C.c_int32, _f32p, _f32p, C.c_int32, _f32p,
                                    _f32p, _f32p, _f32p, _u8p, _u8p]
     L.ref_forward_case.restype = C.c_int
+    _vp = C.c_void_p  # nullable float arrays
+    L.ref_forward_case_qkn.argtypes = [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                       C.c_int32, C.c_int32, C.c_int32,
+                                       C.c_int32, _f32p, _f32p, C.c_int32, _f32p,
+                                       _vp, _vp, C.c_float,
+                                       _f32p, _f32p, _f32p, _u8p, _u8p]
+    L.ref_forward_case_qkn.restype = C.c_int
     _ref[variant] = L
     return L
 
 
+def ref_qk_rmsnorm(x: np.ndarray, w: np.ndarray, n_heads: int, head_dim: int,
+                   eps: float) -> np.ndarray:
+    """The compiled reference's qk_rmsnorm (l3_math.c:107-114)."""
+    L = ref_lib("avx2")
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    y = np.ascontiguousarray(x, np.float32).copy().reshape(-1)
+    ww = np.ascontiguousarray(w, np.float32).reshape(-1)
+    L.ref_qk_rmsnorm(y, ww, n_heads, head_dim, eps)
+    return y
+
+
 def ref_forward_case(shape: Shape, ctx_cap: int, k_pre: np.ndarray, v_pre: np.ndarray,
-                     x_rows: np.ndarray, variant: str = "avx2"):
+                     x_rows: np.ndarray, variant: str = "avx2", q_norm: np.ndarray = None,
+                     k_norm: np.ndarray = None, eps: float = 1e-6):
     """Run the reference model_forward on a selector model (oracle/ref_driver.c).
 
+    q_norm / k_norm ([n_layers, head_dim] or None) add attn_q_norm /
+    attn_k_norm slots and F_QK_NORM.
     Returns dict(xb [n_fwd, dim], out [n_fwd, nq], att [n_heads, ctx_cap],
     kc, vc [n_layers*ctx_cap*row])."""
     L = ref_lib(variant)
@@ -305,10 +339,20 @@ def ref_forward_case(shape: Shape, ctx_cap: int, k_pre: np.ndarray, v_pre: np.nd
     nbytes = shape.n_layers * ctx_cap * shape.row_bytes
     kc = np.zeros(nbytes, np.uint8)
     vc = np.zeros(nbytes, np.uint8)
-    rc = L.ref_forward_case(shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
-                            shape.rope_theta, shape.arch, 1 if shape.kv_q8 else 0, ctx_cap,
-                            n_pre, kp.reshape(-1), vp.reshape(-1), n_fwd, xr.reshape(-1),
-                            xb.reshape(-1), out.reshape(-1), att.reshape(-1), kc, vc)
+    norms = []
+    for w in (q_norm, k_norm):
+        if w is None:
+            norms.append(None)
+        else:
+            a = np.ascontiguousarray(w, np.float32).reshape(-1)
+            assert a.size == shape.n_layers * shape.head_dim
+            norms.append(a)
+    ptr = [None if a is None else a.ctypes.data for a in norms]
+    rc = L.ref_forward_case_qkn(shape.n_layers, shape.n_heads, shape.n_kv_heads,
+                                shape.head_dim, shape.rope_theta, shape.arch,
+                                1 if shape.kv_q8 else 0, ctx_cap, n_pre, kp.reshape(-1),
+                                vp.reshape(-1), n_fwd, xr.reshape(-1), ptr[0], ptr[1], eps,
+                                xb.reshape(-1), out.reshape(-1), att.reshape(-1), kc, vc)
     if rc:
         raise RuntimeError(f"ref_forward_case rc={rc}")
     return dict(xb=xb, out=out, att=att, kc=kc, vc=vc)

@@ -126,6 +126,26 @@ int orc_rope_table(int32_t pos, int32_t head_dim, float theta, float *cs) {
  * adjacent pairs (2i, 2i+1) (l3_math.c:74-81); every other arch rotates the
  * half-split pairs (j, j+hd/2) (l3_math.c:93-101).  a' = a*c - b*s,
  * b' = a*s + b*c, in place, head by head. */
+/* l3_math.c:107-114.  ss accumulates left to right with each square rounded
+ * (-std=c99 keeps contraction off, and without -ffast-math GCC does not
+ * reassociate the sum); ss/head_dim divides by the int converted to float;
+ * the output is (w*x)*inv, rounded after each product. */
+void orc_qk_rmsnorm(float *x, const float *w, int32_t n_heads, int32_t head_dim, float eps) {
+  for (int32_t h = 0; h < n_heads; h++) {
+    float *xh = x + (size_t)h * (size_t)head_dim;
+    float ss = 0.f;
+    for (int32_t j = 0; j < head_dim; j++) {
+      const float sq = xh[j] * xh[j];
+      ss = ss + sq;
+    }
+    const float inv = 1.f / sqrtf(ss / (float)head_dim + eps);
+    for (int32_t j = 0; j < head_dim; j++) {
+      const float wx = w[j] * xh[j];
+      xh[j] = wx * inv;
+    }
+  }
+}
+
 void orc_rope(int32_t arch, float *x, int32_t len, int32_t pos, int32_t head_dim,
               float theta) {
   float cs[1024];

@@ -17,6 +17,9 @@
  *   - Wo and the FFN are zero, so every layer sees the same xb.
  * Positions [0, n_pre) are prefilled with the reference's own apply_rope and
  * kv_store; positions [n_pre, n_pre+n_fwd) go through model_forward.
+ * ref_forward_case_qkn() adds attn_q_norm / attn_k_norm slots and F_QK_NORM
+ * (l5_model.c:505-511); its prefill applies the reference's qk_rmsnorm to
+ * each k row before apply_rope, as model_forward would.
  */
 #include "l5_model.c"
 
@@ -31,6 +34,9 @@ void ref_half_to_float_n(const u16 *h, f32 *out, size_t n) {
   for (size_t i = 0; i < n; i++) out[i] = half_to_float(h[i]);
 }
 void ref_softmax(f32 *x, i32 n) { softmax(x, n); }
+void ref_qk_rmsnorm(f32 *x, const f32 *w, i32 n_heads, i32 hd, f32 eps) {
+  qk_rmsnorm(x, w, n_heads, hd, eps);
+}
 void ref_rope(i32 arch, f32 *x, i32 len, i32 pos, i32 hd, f32 theta) {
   Model m;
   memset(&m, 0, sizeof m);
@@ -49,12 +55,13 @@ static void put_slot(Slot *sl, u32 *ns, u64 *cur, u8 role, u16 layer, u64 nfloat
   (*ns)++;
 }
 
-int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f32 theta,
-                     i32 arch, i32 kv_q8, i32 ctx_cap,
-                     i32 n_pre, const f32 *k_pre, const f32 *v_pre,
-                     i32 n_fwd, const f32 *x_rows,
-                     f32 *xb_out, f32 *out_per_step, f32 *att_out,
-                     u8 *kc_out, u8 *vc_out) {
+int ref_forward_case_qkn(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f32 theta,
+                         i32 arch, i32 kv_q8, i32 ctx_cap,
+                         i32 n_pre, const f32 *k_pre, const f32 *v_pre,
+                         i32 n_fwd, const f32 *x_rows,
+                         const f32 *q_norm, const f32 *k_norm, f32 eps,
+                         f32 *xb_out, f32 *out_per_step, f32 *att_out,
+                         u8 *kc_out, u8 *vc_out) {
   const i32 hd = head_dim, nq = n_heads * hd, nkv = n_kv_heads * hd;
   const i32 dim = nq + 2 * nkv, hid = 32, vocab = n_fwd > 0 ? n_fwd : 1;
   Model m;
@@ -69,12 +76,12 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
   m.c.vocab = vocab;
   m.c.seq_len = ctx_cap;
   m.c.head_dim = hd;
-  m.c.eps = 1e-6f;
+  m.c.eps = eps;
   m.c.rope_theta = theta;
   m.arch = (u8)arch;
-  m.flags = kv_q8 ? F_KV_Q8 : 0;
+  m.flags = (kv_q8 ? F_KV_Q8 : 0) | ((q_norm || k_norm) ? F_QK_NORM : 0);
 
-  u32 max_slots = 2 + (u32)n_layers * 9u;
+  u32 max_slots = 2 + (u32)n_layers * 11u;
   Slot *sl = calloc(max_slots, sizeof(Slot));
   u32 ns = 0;
   u64 cur = 0;
@@ -90,6 +97,8 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
     put_slot(sl, &ns, &cur, R_FFN_GATE, (u16)L, (u64)hid * dim);
     put_slot(sl, &ns, &cur, R_FFN_UP, (u16)L, (u64)hid * dim);
     put_slot(sl, &ns, &cur, R_FFN_DOWN, (u16)L, (u64)dim * hid);
+    if (q_norm) put_slot(sl, &ns, &cur, R_ATTN_Q_NORM, (u16)L, (u64)hd);
+    if (k_norm) put_slot(sl, &ns, &cur, R_ATTN_K_NORM, (u16)L, (u64)hd);
   }
   u8 *blob = calloc(1, (size_t)cur + 64);
   if (!sl || !blob) { free(sl); free(blob); return -1; }
@@ -118,6 +127,12 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
       case R_ATTN_V:
         for (i32 r = 0; r < nkv; r++) w[(size_t)r * dim + nq + nkv + r] = 1.f;
         break;
+      case R_ATTN_Q_NORM:
+        memcpy(w, q_norm + (size_t)sl[i].layer * hd, (size_t)hd * 4u);
+        break;
+      case R_ATTN_K_NORM:
+        memcpy(w, k_norm + (size_t)sl[i].layer * hd, (size_t)hd * 4u);
+        break;
       default:
         break; /* Wo and FFN stay zero */
     }
@@ -133,6 +148,7 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
   for (i32 t = 0; t < n_pre; t++)
     for (i32 L = 0; L < n_layers; L++) {
       memcpy(tmp, k_pre + (size_t)t * nkv, (size_t)nkv * 4u);
+      if (k_norm) qk_rmsnorm(tmp, k_norm + (size_t)L * hd, n_kv_heads, hd, eps);
       apply_rope(&m, tmp, nkv, t, hd, theta);
       kv_store(&m, L, t, tmp, v_pre + (size_t)t * nkv);
     }
@@ -156,4 +172,15 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
   model_free(&m);
   free(blob);
   return 0;
+}
+
+int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f32 theta,
+                     i32 arch, i32 kv_q8, i32 ctx_cap,
+                     i32 n_pre, const f32 *k_pre, const f32 *v_pre,
+                     i32 n_fwd, const f32 *x_rows,
+                     f32 *xb_out, f32 *out_per_step, f32 *att_out,
+                     u8 *kc_out, u8 *vc_out) {
+  return ref_forward_case_qkn(n_layers, n_heads, n_kv_heads, head_dim, theta, arch, kv_q8,
+                              ctx_cap, n_pre, k_pre, v_pre, n_fwd, x_rows, NULL, NULL, 1e-6f,
+                              xb_out, out_per_step, att_out, kc_out, vc_out);
 }

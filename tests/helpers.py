@@ -56,6 +56,22 @@ def golden_inputs(d: dict):
     return shape, kp, vp
 
 
+def golden_norms(d: dict):
+    """(q_norm [L, hd] or None, k_norm [L, hd] or None, eps) of a golden case."""
+    eps = float(d["qkn_eps"]) if "qkn_eps" in d else 1e-6
+    return d.get("q_norm"), d.get("k_norm"), eps
+
+
+def normed(x: np.ndarray, w, n_heads: int, head_dim: int, eps: float) -> np.ndarray:
+    """x (any number of rows of n_heads heads) through the oracle's QK-RMSNorm
+    with weights w; x itself when w is None."""
+    if w is None:
+        return np.asarray(x, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.size // head_dim
+    return orc.qk_rmsnorm(x.reshape(-1), w, n, head_dim, eps).reshape(x.shape)
+
+
 def split_xb(shape: orc.Shape, xb: np.ndarray):
     nq, nkv = shape.nq, shape.nkv
     return xb[:nq], xb[nq:nq + nkv], xb[nq + nkv:nq + 2 * nkv]
@@ -63,19 +79,25 @@ def split_xb(shape: orc.Shape, xb: np.ndarray):
 
 def oracle_run_case(d: dict):
     """The oracle on a golden case: prefill, then every forward step on every
-    layer (all layers see the same q/k/v, as in the reference selector model).
+    layer (all layers see the same q/k/v, as in the reference selector model;
+    with QK-RMSNorm weights, each layer normalises them with its own).
     Returns (outs [n_fwd, nq], att of the last step [n_heads, pos+1], kc, vc)."""
     shape, kp, vp = golden_inputs(d)
+    qn, kn, eps = golden_norms(d)
+    hd = shape.head_dim
     ctx_cap, n_pre = int(d["ctx_cap"]), int(d["n_pre"])
     avx2 = d["variant"].item().decode() == "avx2"
     kc, vc = orc.alloc_kv(shape, ctx_cap)
     for L in range(shape.n_layers):
-        orc.kv_prefill(shape, ctx_cap, L, 0, kc, vc, kp, vp)
+        kpl = normed(kp, None if kn is None else kn[L], shape.n_kv_heads, hd, eps)
+        orc.kv_prefill(shape, ctx_cap, L, 0, kc, vc, kpl, vp)
     outs, att = [], None
     for i, xb in enumerate(d["xb"]):
         q, k, v = split_xb(shape, xb)
         for L in range(shape.n_layers):
-            o, att = orc.attn_layer(shape, ctx_cap, L, n_pre + i, kc, vc, q, k, v, avx2)
+            ql = normed(q, None if qn is None else qn[L], shape.n_heads, hd, eps)
+            kl = normed(k, None if kn is None else kn[L], shape.n_kv_heads, hd, eps)
+            o, att = orc.attn_layer(shape, ctx_cap, L, n_pre + i, kc, vc, ql, kl, v, avx2)
         outs.append(o)
     return np.array(outs), att, kc, vc
 

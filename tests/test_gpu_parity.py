@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 from helpers import (bits, check_out, check_weights, exact_attention, fwd_cases, golden_inputs,
-                     kv_rows, load_golden, q8_special_rows, sha, split_xb)
+                     golden_norms, kv_rows, load_golden, normed, q8_special_rows, sha, split_xb)
 from oracle import orc
 
 from gguf2bin_amd import attn, hip
@@ -58,8 +58,13 @@ def test_golden_forward_case(gpu_device, name):
     o, kp, vp = golden_inputs(d)
     ctx_cap, n_pre = int(d["ctx_cap"]), int(d["n_pre"])
     pos = n_pre + int(d["n_fwd"]) - 1
+    qn, kn, eps = golden_norms(d)
     print(f"[golden] {name} shape={o} ctx_cap={ctx_cap} pos={pos}", flush=True)
     with attn.Context(ashape(o)) as ctx:
+        if qn is not None or kn is not None:
+            for L in range(o.n_layers):
+                ctx.set_qk_norm(L, None if qn is None else qn[L], None if kn is None else kn[L],
+                                eps)
         seq = DevSeq(ctx, o, ctx_cap)
         try:
             for L in range(o.n_layers):
@@ -85,7 +90,9 @@ def test_golden_forward_case(gpu_device, name):
     assert sha(vr) == d["vc_sha"].item().decode(), "V bytes differ from the reference"
     last = o.n_layers - 1
     for i, xb in enumerate(d["xb"]):
-        ex, wex = exact_attention(o, ctx_cap, last, n_pre + i, kc, vc, split_xb(o, xb)[0])
+        ql = normed(split_xb(o, xb)[0], None if qn is None else qn[last], o.n_heads,
+                    o.head_dim, eps)
+        ex, wex = exact_attention(o, ctx_cap, last, n_pre + i, kc, vc, ql)
         e_ref, e_ex, own = check_out(outs[i], d["out"][i], ex)
     print(f"[golden] {name}: |out-ref|={e_ref:.2e} |out-f64|={e_ex:.2e} ref own={own:.2e}")
     if "att_heads" in d:
@@ -139,12 +146,32 @@ SHAPES = {
 }
 
 
-def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True):
+def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, norms=None,
+                   setup=None):
     """n_seq ragged sequences, all layers: device (one fused call or layer by
-    layer) against the oracle, sequence by sequence."""
+    layer) against the oracle, sequence by sequence.  norms: None, or
+    (q_norm, k_norm, eps) with q_norm/k_norm None or indexable by layer (an
+    entry None: that layer has no such weights); the oracle side normalises
+    its inputs with them, and they are set on the context unless setup(ctx)
+    is given to do that itself."""
     n_seq, nL = len(caps), o.n_layers
     rng_seed = seed * 1000
+    qn, kn, eps = norms if norms else (None, None, 1e-6)
+    hd = o.head_dim
+
+    def nq_(x, L):
+        return normed(x, None if qn is None else qn[L], o.n_heads, hd, eps)
+
+    def nk_(x, L):
+        return normed(x, None if kn is None else kn[L], o.n_kv_heads, hd, eps)
+
     with attn.Context(ashape(o)) as ctx:
+        if setup:
+            setup(ctx)
+        elif norms:
+            for L in range(nL):
+                ctx.set_qk_norm(L, None if qn is None else qn[L], None if kn is None else kn[L],
+                                eps)
         seqs = [DevSeq(ctx, o, c) for c in caps]
         hosts = [orc.alloc_kv(o, c) for c in caps]
         try:
@@ -153,7 +180,7 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True):
                     kp = orc.normal(rng_seed + 10 * i + L, p * o.nkv).reshape(p, o.nkv)
                     vp = orc.normal(rng_seed + 500 + 10 * i + L, p * o.nkv).reshape(p, o.nkv)
                     seqs[i].prefill(L, kp, vp)
-                    orc.kv_prefill(o, c, L, 0, hosts[i][0], hosts[i][1], kp, vp)
+                    orc.kv_prefill(o, c, L, 0, hosts[i][0], hosts[i][1], nk_(kp, L), vp)
             q = orc.normal(seed + 1, nL * n_seq * o.nq).reshape(nL, n_seq, o.nq)
             k = orc.normal(seed + 2, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
             v = orc.normal(seed + 3, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
@@ -181,8 +208,9 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True):
     for i, (c, p) in enumerate(zip(caps, poss)):
         kc, vc = hosts[i]
         for L in range(nL):
-            ref, ratt = orc.attn_layer(o, c, L, p, kc, vc, q[L, i], k[L, i], v[L, i])
-            ex, wex = exact_attention(o, c, L, p, kc, vc, q[L, i])
+            ql, kl = nq_(q[L, i], L), nk_(k[L, i], L)
+            ref, ratt = orc.attn_layer(o, c, L, p, kc, vc, ql, kl, v[L, i])
+            ex, wex = exact_attention(o, c, L, p, kc, vc, ql)
             check_out(out[L, i], ref, ex)
             if w is not None:
                 check_weights(w[L, i, :, :p + 1], ratt, wex)
@@ -199,6 +227,57 @@ def test_batched_ragged_vs_oracle(gpu_device, name, fused):
     poss = [0, 36, 211, 650, 64]  # pos 0 (attends to itself only), full, ragged
     print(f"[batch] {name} fused={fused}", flush=True)
     run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused)
+
+
+QKN_SHAPES = {
+    # name: (SHAPES entry, which norms, eps)
+    "qwen3_q8_g2": ("qwen3_q8_g2", "qk", 1e-6),
+    "qwen3_f32_g2": ("qwen3_f32_g2", "qk", 1e-6),
+    "llama3_q8_g4_konly": ("llama3_q8_g4", "k", 1e-5),
+    "smollm2_f32_g3_qonly": ("smollm2_f32_g3", "q", 1e-5),
+    "hd24_q8_generic": ("hd24_q8_generic", "qk", 1e-6),
+    "hd64_q8_g3": ("hd64_q8_g3", "qk", 1e-6),
+}
+
+
+@pytest.mark.parametrize("name", sorted(QKN_SHAPES))
+@pytest.mark.parametrize("fused", [True, False])
+def test_batched_qk_norm_vs_oracle(gpu_device, name, fused):
+    """QK-RMSNorm (l5_model.c:505-511) before RoPE on the device, in the
+    prefill append, the single-launch kernel and the generic path: K bytes
+    bit-exact with the oracle, outputs and weights within the bars.  Layer 1
+    gets different weights from layer 0."""
+    base, which, eps = QKN_SHAPES[name]
+    nh, nkv, hd, arch, q8 = SHAPES[base]
+    o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    seed = zlib.crc32(name.encode()) % 1000
+    qn = (1 + 0.25 * orc.normal(seed + 40, 2 * hd)).reshape(2, hd) if "q" in which else None
+    kn = (1 + 0.25 * orc.normal(seed + 41, 2 * hd)).reshape(2, hd) if "k" in which else None
+    print(f"[qknorm] {name} fused={fused}", flush=True)
+    run_batch_case(o, [1, 37, 300, 129], [0, 36, 211, 64], seed=seed, fused=fused,
+                   norms=(qn, kn, eps))
+
+
+def test_qk_norm_off_and_eps_rules(gpu_device):
+    """Weights can be cleared per layer (the layer runs without the norm);
+    eps is one value per model."""
+    o = orc.Shape(2, 16, 8, 128, 1e6, orc.ARCH_QWEN3, True)
+    w = 1 + 0.25 * orc.normal(3, o.head_dim)
+
+    def setup(ctx):
+        ctx.set_qk_norm(0, w, w, 1e-6)
+        with pytest.raises(attn.G2BError) as e:
+            ctx.set_qk_norm(1, w, w, 1e-5)
+        assert e.value.code == attn.G2B_EINVAL
+        with pytest.raises(attn.G2BError):
+            ctx.set_qk_norm(2, w, w, 1e-6)  # no layer 2
+        ctx.set_qk_norm(1, None, w, 1e-6)
+        ctx.set_qk_norm(0, None, None, 1e-6)  # layer 0 off again
+
+    # afterwards: layer 0 without norm, layer 1 with the k norm only
+    print("[qknorm] off/eps rules", flush=True)
+    run_batch_case(o, [50, 90], [49, 80], seed=11, fused=True,
+                   norms=(None, [None, w], 1e-6), setup=setup)
 
 
 @pytest.mark.parametrize("q8", [True, False])

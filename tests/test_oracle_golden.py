@@ -49,6 +49,16 @@ def test_rope_tables_bit_exact():
     assert np.array_equal(bits(got), bits(d["llama_out"]))
 
 
+def test_qk_rmsnorm_bit_exact():
+    """qk_rmsnorm (l3_math.c:107-114) on random heads at three sizes and on
+    special heads (zero, subnormal, overflowing squares, Inf, NaN, -0)."""
+    d = load_golden("qknorm.npz")
+    for i in range(int(d["n_sets"])):
+        nh, hd = [int(x) for x in d[f"meta{i}"]]
+        got = orc.qk_rmsnorm(d[f"x{i}"], d[f"w{i}"], nh, hd, float(d[f"eps{i}"]))
+        assert np.array_equal(bits(got), bits(d[f"y{i}"])), f"set {i}"
+
+
 @pytest.mark.parametrize("name", fwd_cases())
 def test_forward_case_bit_exact(name):
     """Prefill + model_forward steps: KV bytes, outputs and att weights."""

@@ -239,3 +239,60 @@ def test_pos_outside_ctx_is_rejected():
         orc.attn_layer(shape, 8, 0, 8, kc, vc, np.zeros(32, np.float32),
                        np.zeros(16, np.float32), np.zeros(16, np.float32))
     assert not kc.any() and not vc.any()
+
+
+# ---------------------------------------------------------------- QK-RMSNorm
+
+def _rms_f64(x, w, nh, hd, eps):
+    x = x.astype(np.float64).reshape(nh, hd)
+    ms = (x * x).mean(axis=1, keepdims=True)
+    return (w.astype(np.float64) * x / np.sqrt(ms + eps)).ravel()
+
+
+@pytest.mark.parametrize("hd,nh,scale,eps", [(128, 16, 1.0, 1e-6), (64, 9, 1e-3, 1e-6),
+                                             (24, 3, 30.0, 1e-5), (128, 2, 1e-3, 0.0)])
+def test_qk_rmsnorm_matches_float64(hd, nh, scale, eps):
+    """Within a few fp32 ulps of w*x/sqrt(mean(x^2)+eps) in float64.  At
+    x ~ 1e-3, mean(x^2) ~ 1e-6 is the size of eps, so a dropped or misplaced
+    eps, a sum instead of a mean, or a missing weight fails by far more."""
+    x = (orc.normal(hd * 7 + nh, nh * hd) * scale).astype(np.float32)
+    w = (1 + 0.25 * orc.normal(hd * 11 + nh, hd)).astype(np.float32)
+    got = orc.qk_rmsnorm(x, w, nh, hd, eps).astype(np.float64)
+    ref = _rms_f64(x, np.tile(w, 1), nh, hd, eps)
+    assert np.max(np.abs(got - ref) / np.maximum(np.abs(ref), 1e-30)) < 2e-6
+
+
+def test_qk_rmsnorm_unit_weights_give_unit_rms():
+    """w = 1, eps = 0: every head comes out with mean square 1."""
+    nh, hd = 5, 64
+    x = orc.normal(99, nh * hd) * np.float32(7.0)
+    y = orc.qk_rmsnorm(x, np.ones(hd, np.float32), nh, hd, 0.0).astype(np.float64)
+    ms = (y.reshape(nh, hd) ** 2).mean(axis=1)
+    assert np.allclose(ms, 1.0, rtol=1e-5)
+
+
+def test_qk_rmsnorm_heads_are_independent_and_weights_per_element():
+    """Scaling one head by 2^k leaves the others unchanged and (eps = 0) its
+    own output unchanged; weights multiply element by element."""
+    nh, hd = 4, 32
+    x = orc.normal(5, nh * hd)
+    w = (1 + 0.5 * orc.normal(6, hd)).astype(np.float32)
+    y = orc.qk_rmsnorm(x, w, nh, hd, 0.0)
+    x2 = x.copy()
+    x2[hd:2 * hd] *= np.float32(8.0)
+    y2 = orc.qk_rmsnorm(x2, w, nh, hd, 0.0)
+    assert np.array_equal(y, y2)
+    y1 = orc.qk_rmsnorm(x, np.ones(hd, np.float32), nh, hd, 0.0)
+    assert np.allclose(y.reshape(nh, hd), (y1.reshape(nh, hd) * w), rtol=3e-7, atol=0)
+
+
+def test_qk_rmsnorm_zero_head_and_eps():
+    """A zero head stays zero (0 * 1/sqrt(eps)); eps alone sets the scale of a
+    head whose mean square is far below it."""
+    hd = 16
+    z = orc.qk_rmsnorm(np.zeros(hd, np.float32), np.ones(hd, np.float32), 1, hd, 1e-6)
+    assert np.array_equal(z, np.zeros(hd, np.float32))
+    x = np.full(hd, 1e-9, np.float32)
+    y = orc.qk_rmsnorm(x, np.ones(hd, np.float32), 1, hd, 1e-2)
+    assert np.allclose(y, 1e-9 / np.sqrt(1e-2 + 1e-18), rtol=1e-6)
+
