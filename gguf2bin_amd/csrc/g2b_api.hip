@@ -165,8 +165,8 @@ int ensure_rope(g2b_ctx *c, int32_t len) {
 // work per workgroup they start and finish together, and the launch has no
 // partly idle tail.  One round when the work allows it; otherwise as many
 // rounds as the minimum split length forces.  At most 512 splits per
-// sequence (the combine stages 4 weights per split in LDS) and the generic
-// kernel's LDS limit apply.
+// sequence (each is one partial per head for the combine, which stages a
+// weight per partial in LDS) and the generic kernel's LDS limit apply.
 int32_t choose_split(const g2b_ctx *c, int64_t total_pos, int32_t max_pos, int32_t n_layers,
                      bool fast) {
   const int64_t work = total_pos * (int64_t)n_layers;
@@ -200,7 +200,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
 
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
-                             kWavesPerSplit * (size_t)(kPartHead + hd);
+                             (size_t)(kPartHead + hd);
   if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
   if (!fast) {
     if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;

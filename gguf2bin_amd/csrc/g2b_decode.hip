@@ -562,22 +562,47 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       m[i] = gather ? M : m[i];
     }
   }
-  const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
-  const size_t pstr = (size_t)(kPartHead + HD);
+  // Merge the four waves' states in LDS (the rows and q there are no longer
+  // read once every wave is past this barrier) and write one partial per
+  // head for the split.  LDS: [wave][head][kPartHead + HD] floats.
+  constexpr int pstr = kPartHead + HD;
+  __syncthreads();
+  float *ws = reinterpret_cast<float *>(lds);
   if (slot == 0) {
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      const int h = g * G + i;
-      float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * nparts +
-                            (size_t)split * kWavesPerSplit + (size_t)wave) * pstr;
+      float *pw = ws + ((size_t)wave * n_heads + (size_t)(g * G + i)) * pstr;
       if (c == 0) {
-        pp[0] = m[i];
-        pp[1] = l[i];
+        pw[0] = m[i];
+        pw[1] = l[i];
       }
 #pragma unroll
       for (int j = 0; j < CD; j += 4)
-        *reinterpret_cast<float4 *>(pp + kPartHead + c * CD + j) =
+        *reinterpret_cast<float4 *>(pw + kPartHead + c * CD + j) =
             make_float4(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3]);
+    }
+  }
+  __syncthreads();
+  const size_t wstr = (size_t)n_heads * pstr;
+  for (int e = threadIdx.x; e < n_heads * HD; e += blockDim.x) {
+    const int h = e / HD, d = e - h * HD;
+    const float *pw = ws + (size_t)h * pstr;
+    float M = pw[0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
+    float o = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerSplit; w++) {
+      const float f = exp2f(pw[w * wstr] - M);
+      o = fmaf(pw[w * wstr + kPartHead + d], f, o);
+      lsum = fmaf(pw[w * wstr + 1], f, lsum);
+    }
+    float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
+                          (size_t)split) * pstr;
+    pp[kPartHead + d] = o;
+    if (d == 0) {
+      pp[0] = M;
+      pp[1] = lsum;
     }
   }
 }
@@ -624,7 +649,6 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
   const size_t row = P.sh.row_bytes;
   const uint8_t *kb = sd.k + (size_t)layer * (size_t)sd.ctx_cap * row;
   const uint8_t *vb = sd.v + (size_t)layer * (size_t)sd.ctx_cap * row;
-  const size_t nparts = (size_t)P.max_splits * kWavesPerSplit;
   for (int h = 0; h < nh; h++) {
     const int e0 = (h / group) * HD;
     const float *qh = P.q_rot + sidx * (size_t)(nh * HD) + (size_t)h * HD;
@@ -648,62 +672,118 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
     }
     const float L = block_reduce(sum, false, red);
     __syncthreads();
-    float *pp = P.part + ((sidx * nh + h) * nparts + (size_t)split * kWavesPerSplit) *
+    float *pp = P.part + ((sidx * nh + h) * (size_t)P.max_splits + (size_t)split) *
                              (size_t)(kPartHead + HD);
     for (int d = threadIdx.x; d < HD; d += blockDim.x) {
       float a = 0.f;
       for (int t = 0; t < n; t++) a = fmaf(sc[t], kv_elem(vb + (size_t)(t0 + t) * row, e0 + d, P.sh.kv_q8), a);
       pp[kPartHead + d] = a;
-      for (int w = 1; w < kWavesPerSplit; w++) pp[(size_t)w * (kPartHead + HD) + kPartHead + d] = 0.f;
     }
     if (threadIdx.x == 0) {
       pp[0] = M;
       pp[1] = L;
-      for (int w = 1; w < kWavesPerSplit; w++) {
-        pp[(size_t)w * (kPartHead + HD)] = kNegBig;
-        pp[(size_t)w * (kPartHead + HD) + 1] = 0.f;
-      }
     }
     __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------- combine
-constexpr int kCombineThreads = 128;
+// One workgroup per (head, seq, layer) merges that head's split partials:
+// M = max m_p, w_p = exp2(m_p - M), L = sum l_p w_p, out = sum acc_p w_p / L,
+// written over q.  Up to 2048 partials (one per split) per head: the
+// max and the sum are block reductions, and the weighted sum of the
+// accumulators splits the partials over 256/HD thread groups with four
+// independent chains per thread, so the merge is bandwidth- and not
+// latency-bound.  The sums are float64: a serial fp32 sum of that many terms
+// drifts by ~1e-5 relative once one partial dominates.
+constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 2048;
+
+__device__ inline float block_max_f(float x, float *red) {
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = x;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); w++) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+__device__ inline double block_sum_d(double x, double *red) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = x;
+  __syncthreads();
+  double r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); w++) r += red[w];
+  __syncthreads();
+  return r;
+}
 
 __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, float *q_out) {
   __shared__ float w[kCombineMaxParts];
+  __shared__ double part_sum[kCombineThreads];
+  __shared__ double red[kCombineThreads / 64];
   const int h = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
   const int npos = sd.pos + 1;
   const int nsplit = (npos + P.split_len - 1) / P.split_len;
-  const int np = nsplit * kWavesPerSplit;
+  const int np = nsplit;
   const int HD = P.sh.head_dim, nh = P.sh.n_heads;
   const size_t pstr = (size_t)(kPartHead + HD);
   const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
   const float *base =
-      P.part + (sidx * nh + h) * (size_t)P.max_splits * kWavesPerSplit * pstr;
-  // The merge over up to 2048 partials is accumulated in float64: a serial
-  // fp32 sum of that many terms drifts by ~1e-5 relative once one partial
-  // dominates.  This kernel moves a few KB per head, so the cost is nil.
-  float M = kNegBig;
-  for (int p = 0; p < np; p++) M = fmaxf(M, base[p * pstr]);
-  for (int p = threadIdx.x; p < np; p += blockDim.x) w[p] = exp2f(base[p * pstr] - M);
-  __syncthreads();
-  double L = 0.0;
-  for (int p = 0; p < np; p++) L = fma((double)base[p * pstr + 1], (double)w[p], L);
+      P.part + (sidx * nh + h) * (size_t)P.max_splits * pstr;
+  const int tid = threadIdx.x;
+
+  float mx = kNegBig;
+  for (int p = tid; p < np; p += blockDim.x) mx = fmaxf(mx, base[p * pstr]);
+  const float M = block_max_f(mx, reinterpret_cast<float *>(red));
+  double lsum = 0.0;
+  for (int p = tid; p < np; p += blockDim.x) {
+    const float wp = exp2f(base[p * pstr] - M);
+    w[p] = wp;
+    lsum = fma((double)base[p * pstr + 1], (double)wp, lsum);
+  }
+  const double L = block_sum_d(lsum, red);  // (its barriers also publish w)
+
   float *out = q_out + sidx * (size_t)(nh * HD) + (size_t)h * HD;
-  for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-    double o = 0.0;
-    for (int p = 0; p < np; p++) o = fma((double)base[p * pstr + kPartHead + d], (double)w[p], o);
-    out[d] = (float)(o / L);
+  const int ngrp = HD <= (int)blockDim.x ? (int)blockDim.x / HD : 1;
+  const int grp = tid / HD;
+  for (int d = tid % HD; d < HD; d += blockDim.x) {
+    double o0 = 0.0, o1 = 0.0, o2 = 0.0, o3 = 0.0;
+    if (grp < ngrp) {
+      const float *a = base + kPartHead + d;
+      int p = grp;
+      for (; p + 3 * ngrp < np; p += 4 * ngrp) {
+        o0 = fma((double)a[(size_t)p * pstr], (double)w[p], o0);
+        o1 = fma((double)a[(size_t)(p + ngrp) * pstr], (double)w[p + ngrp], o1);
+        o2 = fma((double)a[(size_t)(p + 2 * ngrp) * pstr], (double)w[p + 2 * ngrp], o2);
+        o3 = fma((double)a[(size_t)(p + 3 * ngrp) * pstr], (double)w[p + 3 * ngrp], o3);
+      }
+      for (; p < np; p += ngrp) o0 = fma((double)a[(size_t)p * pstr], (double)w[p], o0);
+    }
+    const double o = (o0 + o1) + (o2 + o3);
+    if (ngrp == 1) {
+      out[d] = (float)(o / L);
+    } else if (grp < ngrp) {
+      part_sum[grp * HD + d] = o;
+    }
+  }
+  if (ngrp > 1) {
+    __syncthreads();
+    for (int d = tid; d < HD; d += blockDim.x) {
+      double o = 0.0;
+      for (int g = 0; g < ngrp; g++) o += part_sum[g * HD + d];
+      out[d] = (float)(o / L);
+    }
   }
   if (P.att) {
     // weights of the scores this kernel used, normalised without an fp32
     // rounding of (score - max)
     float *a = P.att + (sidx * nh + h) * (size_t)P.att_stride;
-    for (int t = threadIdx.x; t < npos; t += blockDim.x)
+    for (int t = tid; t < npos; t += blockDim.x)
       a[t] = (float)(exp2((double)a[t] - (double)M) / L);
   }
 }
@@ -714,7 +794,8 @@ size_t layer_lds_bytes(const ShapeDev &sh) {
   const size_t nq = (size_t)sh.n_heads * sh.head_dim;
   const size_t nkv = (size_t)sh.n_kv_heads * sh.head_dim;
   const size_t a = (nkv * 4 + 15) & ~(size_t)15, rb = ((size_t)sh.row_bytes + 15) & ~(size_t)15;
-  return nq * 4 + a + 2 * rb + (size_t)sh.n_heads * 4;
+  const size_t merge = (size_t)kWavesPerSplit * sh.n_heads * (kPartHead + sh.head_dim) * 4;
+  return std::max(nq * 4 + a + 2 * rb + (size_t)sh.n_heads * 4, merge);
 }
 
 template <int FMT, int HD, int CD, int G, int U>
@@ -829,7 +910,7 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int
 }
 
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s) {
-  (void)kCombineMaxParts;
+  if (p.max_splits > kCombineMaxParts) return hipErrorInvalidValue;
   dim3 grid(p.sh.n_heads, p.n_seq, n_layers);
   hipLaunchKernelGGL(k_combine, grid, dim3(kCombineThreads), 0, s, p, p.q_out);
   return hipGetLastError();

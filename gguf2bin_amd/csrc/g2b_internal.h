@@ -9,11 +9,11 @@
 
 namespace g2b {
 
-// Partial state of one wave of one split for one q head:
+// Partial state of one split for one q head:
 // [m, l, 0, 0, acc[head_dim]] in the log2 domain (m = running max of the
 // scaled scores, l = sum of exp2(score - m), acc = sum of exp2(score - m)*v).
 constexpr int kPartHead = 4;
-constexpr int kWavesPerSplit = 4;      // one partial per wave of a 256-thread split
+constexpr int kWavesPerSplit = 4;      // waves of a 256-thread split workgroup
 constexpr int kThreads = 256;
 constexpr int kGenericMaxSplit = 1024;  // positions per split in the generic kernel
 
@@ -45,7 +45,7 @@ struct DecodeParams {
   const float *v_in;   // [L][n_seq][nkv] new v (single-launch path)
   const float *rope;   // [rope_len][head_dim] cos/sin pairs, or nullptr
   NormDev norm;        // QK-RMSNorm weights (norm.w == nullptr: none)
-  float *part;         // [L][n_seq][n_heads][max_splits*kWavesPerSplit][kPartHead+hd]
+  float *part;         // [L][n_seq][n_heads][max_splits][kPartHead+hd]
   float *att;          // nullable: [L][n_seq][n_heads][att_stride]
   int32_t att_stride;
   float qscale;        // (1/sqrtf(hd)) * log2(e)
