@@ -116,7 +116,7 @@ def lib() -> C.CDLL:
                                   C.c_int),
             "g2b_synth_copy": ([vp, vp, vp, u64], C.c_int),
             "g2b_ctx_profile": ([vp, i32], C.c_int),
-            "g2b_ctx_tune": ([vp, i32, i32, i32], C.c_int),
+            "g2b_ctx_tune": ([vp, i32, i32, i32, i32], C.c_int),
             "g2b_ctx_profile_read": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)],
                                      C.c_int),
         }
@@ -266,9 +266,10 @@ class Context:
     def synth_copy(self, dst: int, src: int, nbytes: int):
         self._check(lib().g2b_synth_copy(self.h, dst, src, nbytes), "g2b_synth_copy")
 
-    def tune(self, split_len: int = 0, unroll: int = 0, chunk: int = 0):
-        """Decode-kernel tuning (0 = automatic): split length, unroll, Q8 chunk."""
-        self._check(lib().g2b_ctx_tune(self.h, split_len, unroll, chunk), "g2b_ctx_tune")
+    def tune(self, split_len: int = 0, unroll: int = 0, chunk: int = 0, stage: int = 0):
+        """Decode-kernel tuning (0 = automatic): split length, unroll, Q8 chunk,
+        KV row path (-1 per-lane HBM loads, 1 / 2 staged through LDS)."""
+        self._check(lib().g2b_ctx_tune(self.h, split_len, unroll, chunk, stage), "g2b_ctx_tune")
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

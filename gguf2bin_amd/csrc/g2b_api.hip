@@ -56,6 +56,7 @@ struct g2b_ctx {
   int32_t slots = 0;           // resident decode workgroups on the device
   int32_t split_override = 0;  // g2b_ctx_tune
   int32_t tune_unroll = 0, tune_chunk = 0;
+  int32_t tune_stage = 0;      // -1: k_layer loads straight from HBM; 1, 2: staging mode
 
   // decode-launch timing (g2b_ctx_profile)
   bool prof = false;
@@ -229,6 +230,9 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
+  dp.stage_mode = c->tune_stage < 0 ? 0 : c->tune_stage > 0 ? c->tune_stage : kDefaultStageMode;
+  dp.stage_rows = decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode);
+  if (dp.stage_rows == 0) dp.stage_mode = 0;
 
   if (!fast) {  // generic shapes: append, decode, combine
     AppendParams ap{};
@@ -620,13 +624,14 @@ int g2b_synth_copy(g2b_ctx *c, void *dst, const void *src, uint64_t nbytes) {
   return G2B_OK;
 }
 
-int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t unroll, int32_t chunk) {
+int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t unroll, int32_t chunk, int32_t stage) {
   if (!c || split_len < 0 || (unroll != 0 && unroll != 2 && unroll != 4) ||
-      (chunk != 0 && chunk != 16 && chunk != 32))
+      (chunk != 0 && chunk != 16 && chunk != 32) || stage < -1 || stage > 2)
     return G2B_EINVAL;
   c->split_override = split_len;
   c->tune_unroll = unroll;
   c->tune_chunk = chunk;
+  c->tune_stage = stage;
   return G2B_OK;
 }
 

@@ -99,6 +99,17 @@ __device__ __forceinline__ float half_bits_to_f32(uint32_t h) {
   return __uint_as_float(sign | (e8 << 23) | (m10 << 13));
 }
 
+// fp16 bits (low 16 bits of h) -> fp32 by the hardware conversion
+// (v_cvt_f32_f16).  Exact for every finite or infinite half, subnormals
+// included: the kernels run with fp16 denormals preserved
+// (float_denorm_mode_16_64 = 3).  It differs from half_bits_to_f32 only in
+// the payload of a NaN, which no attention output can show (a NaN block
+// scale makes the output NaN either way).  The attention loops use it for
+// block scales; everything that writes KV bytes uses half_bits_to_f32.
+__device__ __forceinline__ float half_bits_to_f32_hw(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
 // (int32)lroundf(r) as glibc on x86-64 gives it: round half away from zero,
 // out-of-range and NaN produce LONG_MIN, whose low 32 bits are 0.
 __device__ __forceinline__ int32_t lround_i32_like_host(float r) {

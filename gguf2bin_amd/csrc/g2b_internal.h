@@ -17,6 +17,49 @@ constexpr int kWavesPerSplit = 4;      // waves of a 256-thread split workgroup
 constexpr int kThreads = 256;
 constexpr int kGenericMaxSplit = 1024;  // positions per split in the generic kernel
 
+// Staged streaming in k_layer: each wave moves chunks of stage_rows
+// contiguous K and V rows into its own LDS region with coalesced 16-byte
+// non-temporal loads, and its lanes read their blocks from there.  Needs
+// rows that are whole 16-byte pieces.  Mode 1 (global_load_lds straight into
+// LDS) uses chunks of about 8704 bytes of K (and as much of V); mode 2
+// (registers one chunk ahead, then LDS) about 4352 bytes, at most
+// kStageLoads pieces per lane and tensor.  A chunk is a whole number of
+// wave-steps (positions_per_wave_step positions each).  0 = not staged.
+constexpr int kStageLoads = 5;
+__host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
+                                                 int32_t positions_per_wave_step, int32_t mode) {
+  if (row_bytes == 0 || (row_bytes & 15u) || positions_per_wave_step < 1) return 0;
+  if (mode != 1 && mode != 2) return 0;
+  const uint32_t target = mode == 1 ? 8704u : 4352u;
+  const uint32_t per_step = row_bytes * (uint32_t)positions_per_wave_step;
+  const uint32_t steps = per_step >= target ? 1u : target / per_step;
+  if (mode == 2 && steps * per_step > 1024u * (uint32_t)kStageLoads) return 0;
+  return (int32_t)steps * positions_per_wave_step;
+}
+
+// k_layer's dynamic LDS: [0, rows) holds the rotated q and new k before the
+// stream starts and the waves' staging regions (stage_rows > 0) during it;
+// then the new K and V rows (row_pad bytes each) and n_heads floats of
+// QK-RMSNorm scratch.  After the stream, the wave merge of the partials
+// ([wave][head][kPartHead + head_dim] floats) reuses everything from 0.
+struct LdsLayout {
+  uint32_t rows, row_pad, total;
+};
+__host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows) {
+  const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
+  const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
+  const uint32_t pre = nq * 4u + ((nkv * 4u + 15u) & ~15u);
+  const uint32_t stage = (uint32_t)kWavesPerSplit * 2u * (uint32_t)stage_rows * sh.row_bytes;
+  const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)sh.n_heads *
+                         (uint32_t)(kPartHead + sh.head_dim) * 4u;
+  LdsLayout l;
+  l.row_pad = (sh.row_bytes + 15u) & ~15u;
+  l.rows = pre > stage ? pre : stage;
+  const uint32_t need = l.rows + 2u * l.row_pad + (uint32_t)sh.n_heads * 4u;
+  l.total = need > merge ? need : merge;
+  return l;
+}
+
 
 struct AppendParams {
   ShapeDev sh;
@@ -51,6 +94,8 @@ struct DecodeParams {
   float qscale;        // (1/sqrtf(hd)) * log2(e)
   int32_t tune_unroll; // 0 = default, else wave-steps per loop trip (2 or 4)
   int32_t tune_chunk;  // 0 = default, else elements per lane for Q8 (16 or 32)
+  int32_t stage_mode;  // k_layer: 0 direct loads, 1 / 2 staged (stage_rows_of)
+  int32_t stage_rows;  // rows per staged chunk (0 with stage_mode 0)
 };
 
 // Launchers: return hipSuccess or the launch error.
@@ -66,6 +111,19 @@ hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 bool decode_fast_available(const ShapeDev &sh);
 // Resident 256-thread decode workgroups per CU for this shape (occupancy).
 int decode_blocks_per_cu(const ShapeDev &sh);
+// DecodeParams.stage_rows for this shape and staging mode (tune_chunk as in
+// DecodeParams): 0 when k_layer must load straight from HBM (no specialised
+// kernel, or rows that are not whole 16-byte pieces).
+int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode);
+// Staging mode k_layer uses unless tuned otherwise.
+constexpr int32_t kDefaultStageMode = 2;
+// k_layer for one (KV format 0 = F32 / 1 = Q8_0, head_dim, GQA group),
+// defined in g2b_layer.h and instantiated by g2b_layer_inst.hip: the launch,
+// and its resident workgroups per CU for a given stage_rows.
+template <int FMT, int HD, int G>
+hipError_t launch_layer(const DecodeParams &p, int n_layers, hipStream_t s);
+template <int FMT, int HD, int G>
+int layer_occupancy(const ShapeDev &sh, int32_t stage_rows);
 
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {

@@ -1,0 +1,794 @@
+// g2b_layer.h - k_layer, the specialised decode kernel, and its launchers.
+// Included only by g2b_layer_inst.hip, which the build compiles once per
+// (KV format, head_dim, GQA group) so that the variants build in parallel;
+// g2b_decode.hip dispatches to those instantiations.
+//
+// Replaces the score / softmax / V-accumulate loops of
+// /root/reference/src/l5_model.c:518-557 (AVX2) and :558-577 (scalar):
+//   att[h][t] = dot(q_h, k_t[h/group]) / sqrt(hd), softmax over t <= pos,
+//   out_h = sum_t att[h][t] * v_t[h/group].
+// The reference dequantises a whole row per position into a scratch buffer
+// (kv_key_row / kv_val_row, l5_model.c:248-265) and walks every q head.  Here
+// the row is never materialised: each lane owns one chunk of the row (one
+// 32-element Q8_0 block, half a block, or 16 F32 values), keeps the q values
+// of the GQA group for that chunk in registers, dequantises in registers,
+// and keeps its own online-softmax state.  A position's partial dot products
+// are summed over the lanes of a head with DPP.  Nothing goes through LDS in
+// the main loop and there is no barrier: each wave streams rows
+// independently with wide loads.  Scores are kept in the log2 domain
+// (q pre-scaled by log2(e)/sqrt(hd)) so that softmax uses v_exp_f32.
+//
+// Splits: workgroup (split, seq, layer) covers positions
+// [split*split_len, min(pos+1, (split+1)*split_len)); its four waves take
+// interleaved groups of PPW positions and each writes one partial
+// (m, l, acc[hd]) per q head.  k_combine merges the partials of a
+// (seq, layer, head), writes the output over q (as l5_model.c:541-557 does)
+// and, when asked, turns the stored scores into the reference's
+// att[h*ctx+t] weights.
+#pragma once
+#include <algorithm>
+#include <type_traits>
+
+#include "g2b_internal.h"
+
+namespace g2b {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of N consecutive lanes; every lane of a group ends
+// with the same value (each step adds two equal-order operands).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+  if constexpr (N >= 2) x += dpp_f<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  if constexpr (N >= 4) x += dpp_f<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  if constexpr (N >= 8) x += dpp_f<0x141>(x);  // row_half_mirror: other quad of 8
+  if constexpr (N >= 16) x += dpp_f<0x140>(x); // row_mirror: other half of 16
+  return x;
+}
+
+__device__ __forceinline__ float i8f(uint32_t w, int byte) {
+  return (float)(int8_t)(uint8_t)(w >> (8 * byte));
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Loads through the global address space (the cache pointers arrive through a
+// descriptor table, so the compiler would otherwise emit flat loads).
+template <typename T>
+__device__ __forceinline__ T gload(const uint8_t *p) {
+  return *(const __attribute__((address_space(1))) T *)(p);
+}
+
+// Cache-policy operand of global_load_lds for a non-temporal (streaming)
+// load: the nt bit.  Two contiguous streams per workgroup read ~12% faster
+// non-temporal than with the default policy on MI355X (7.0 vs 6.2 TB/s), but
+// only when each line is requested once, which the staged path guarantees.
+constexpr int kAuxNT = 2;
+// s_waitcnt operand (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited.
+constexpr int kWaitVmcnt0 = 0x0F70;
+
+// Per-lane addressing of its chunk inside a row.
+struct LaneOff {
+  uint32_t o0, o1, o2;  // byte offsets inside the row
+  uint32_t sel;         // v_perm_b32 selector that realigns quant dwords
+  uint32_t sshift;      // 0 or 16: where the fp16 scale sits in its dword
+};
+
+template <int FMT, int CD>
+struct Codec;
+
+// ---- F32 rows: 16 contiguous floats, four 16-byte loads ----
+template <>
+struct Codec<0, 16> {
+  struct Raw {
+    f32x4 x[4];
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    LaneOff o;
+    o.o0 = (uint32_t)elem0 * 4u;
+    o.o1 = o.o2 = o.sel = o.sshift = 0;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.x[i] = gload<f32x4>(row + o.o0 + 16 * i);
+  }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const float *p = reinterpret_cast<const float *>(row + o.o0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.x[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
+  }
+  static __device__ __forceinline__ void values(const Raw &r, float (&f)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      f[4 * i + 0] = r.x[i].x;
+      f[4 * i + 1] = r.x[i].y;
+      f[4 * i + 2] = r.x[i].z;
+      f[4 * i + 3] = r.x[i].w;
+    }
+  }
+};
+
+// ---- Q8_0, one full 34-byte block per lane ----
+// Block b starts at byte 34b: for even b the dword window starts at the
+// block (scale = low half of dword 0, quants at window bytes 2..33); for odd
+// b it starts two bytes earlier (scale = high half, quants at bytes 4..35).
+// Nine dwords cover the block either way and, because the last block of a
+// row is odd whenever head_dim is a multiple of 64, never leave the row.
+template <>
+struct Codec<1, 32> {
+  struct Raw {
+    u32x4 a, b;
+    uint32_t c;
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u;
+    LaneOff o;
+    o.o0 = (34u * b) & ~3u;
+    o.o1 = o.o2 = 0;
+    o.sel = odd ? 0x07060504u : 0x05040302u;
+    o.sshift = odd ? 16u : 0u;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const uint8_t *p = row + o.o0;
+    r.a = gload<u32x4>(p);
+    r.b = gload<u32x4>(p + 16);
+    r.c = gload<uint32_t>(p + 32);
+  }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + o.o0);
+    r.a = u32x4{p[0], p[1], p[2], p[3]};
+    r.b = u32x4{p[4], p[5], p[6], p[7]};
+    r.c = p[8];
+  }
+  // the 32 int8 quants as 8 aligned dwords, and the block scale
+  static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[8], float &scale,
+                                                const LaneOff &o) {
+    const uint32_t d[9] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c};
+    scale = half_bits_to_f32_hw(d[0] >> o.sshift);
+#pragma unroll
+    for (int j = 0; j < 8; j++) w[j] = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
+  }
+};
+
+// ---- Q8_0, half a block (16 quants) per lane ----
+// Scale dword at (34b)&~3; quant window at (34b+2+16h)&~3 (two bytes early
+// for even b).  For odd b the window is aligned and only four dwords are
+// used; the fifth load is pointed inside the block so it never leaves it.
+template <>
+struct Codec<1, 16> {
+  struct Raw {
+    uint32_t s;
+    u32x4 a;
+    uint32_t c;
+  };
+  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+    const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u, h = ((uint32_t)elem0 >> 4) & 1u;
+    const uint32_t qstart = 34u * b + 2u + 16u * h;
+    LaneOff o;
+    o.o0 = (34u * b) & ~3u;
+    o.o1 = qstart & ~3u;
+    o.o2 = odd ? o.o1 + 12u : o.o1 + 16u;
+    o.sel = odd ? 0x03020100u : 0x05040302u;
+    o.sshift = odd ? 16u : 0u;
+    return o;
+  }
+  static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
+    r.s = gload<uint32_t>(row + o.o0);
+    r.a = gload<u32x4>(row + o.o1);
+    r.c = gload<uint32_t>(row + o.o2);
+  }
+  static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+    r.s = *reinterpret_cast<const uint32_t *>(row + o.o0);
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(row + o.o1);
+    r.a = u32x4{p[0], p[1], p[2], p[3]};
+    r.c = *reinterpret_cast<const uint32_t *>(row + o.o2);
+  }
+  static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[4], float &scale,
+                                                const LaneOff &o) {
+    const uint32_t d[5] = {r.a.x, r.a.y, r.a.z, r.a.w, r.c};
+    scale = half_bits_to_f32_hw(r.s >> o.sshift);
+#pragma unroll
+    for (int j = 0; j < 4; j++) w[j] = __builtin_amdgcn_perm(d[j + 1], d[j], o.sel);
+  }
+};
+
+// q for the integer K dot products: each q value of a (head, chunk) becomes
+// m = rint(q * 2^(22-e)) with 2^e > max|q| (so |m| <= 2^22, 23 bits of the
+// chunk maximum), split into three signed base-256 digits packed four per
+// dword.  sum_j m_j k_j is then three chains of v_dot4_i32_i8 (exact in
+// int32) and one fp32 rounding; the quantisation of q costs at most
+// 2^-23 * max|q| per element, less than an fp32 FMA chain over the same
+// int8 values loses.
+template <int CD>
+struct QDigits {
+  uint32_t d[3][CD / 4];
+  float unit;  // 2^(e-22): value of one m step
+};
+
+template <int CD>
+__device__ __forceinline__ QDigits<CD> make_digits(const float (&q)[CD]) {
+  QDigits<CD> r;
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < CD; j++) mx = fmaxf(mx, fabsf(q[j]));
+  int e = 0;
+  (void)frexpf(mx, &e);
+  const float up = ldexpf(1.f, 22 - e);
+  r.unit = ldexpf(1.f, e - 22);
+#pragma unroll
+  for (int k = 0; k < 3; k++)
+#pragma unroll
+    for (int j = 0; j < CD / 4; j++) r.d[k][j] = 0u;
+#pragma unroll
+  for (int j = 0; j < CD; j++) {
+    const int m = (int)rintf(q[j] * up);
+    const int d0 = ((m + 128) & 255) - 128;
+    const int m1 = (m - d0) >> 8;
+    const int d1 = ((m1 + 128) & 255) - 128;
+    const int d2 = (m1 - d1) >> 8;
+    const int sh = 8 * (j & 3);
+    r.d[0][j >> 2] |= ((uint32_t)d0 & 0xffu) << sh;
+    r.d[1][j >> 2] |= ((uint32_t)d1 & 0xffu) << sh;
+    r.d[2][j >> 2] |= ((uint32_t)d2 & 0xffu) << sh;
+  }
+  return r;
+}
+
+// sum_j m_j * k_j for the chunk, as a float in units of m.
+template <int NW>
+__device__ __forceinline__ float qk_int(const uint32_t (&w)[NW], const uint32_t (&d)[3][NW]) {
+  int s0 = 0, s1 = 0, s2 = 0;
+#pragma unroll
+  for (int j = 0; j < NW; j++) {
+    s0 = __builtin_amdgcn_sdot4((int)w[j], (int)d[0][j], s0, false);
+    s1 = __builtin_amdgcn_sdot4((int)w[j], (int)d[1][j], s1, false);
+    s2 = __builtin_amdgcn_sdot4((int)w[j], (int)d[2][j], s2, false);
+  }
+  // |s2| <= 32*65*127, so s2*256 + s1 fits in int32
+  const int hi = s2 * 256 + s1;
+  return fmaf((float)hi, 256.f, (float)s0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  // v_exp_f32; results below 2^-126 (weights under 1e-38 of the maximum)
+  // may flush to zero, which no output can see.
+  return __builtin_amdgcn_exp2f(x);
+}
+
+// The new row of the workgroup that owns position pos: [QK-RMSNorm,] RoPE(k), then F32 copy
+// or Q8_0 quantisation of k and v into LDS (rowk, rowv), then a copy of both
+// rows to the caches.  The workgroup later reads pos from LDS, so no other
+// workgroup and no cache level is involved.  Every thread calls it.
+__device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
+                                      const float *k, const float *v, const float *rope,
+                                      const NormDev &norm, float *kr, uint8_t *rowk,
+                                      uint8_t *rowv, float *inv) {
+  const int hd = sh.head_dim, half = hd / 2;
+  const int nkv = sh.n_kv_heads * hd;
+  const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
+  for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
+  __syncthreads();
+  if (const float *wk = norm_weights(norm, layer, 1, hd))
+    qk_rmsnorm_block(kr, sh.n_kv_heads, hd, wk, norm.eps, inv);
+  if (cs) {
+    for (int p = threadIdx.x; p < sh.n_kv_heads * half; p += blockDim.x) {
+      const int h = p / half, j = p - h * half;
+      int ia, ib;
+      rope_pair_index(sh.arch_llama, j, half, ia, ib);
+      rope_pair(kr[h * hd + ia], kr[h * hd + ib], cs[2 * j], cs[2 * j + 1]);
+    }
+  }
+  __syncthreads();
+  if (sh.kv_q8) {
+    const int nb = (nkv + 31) / 32;
+    for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
+      const bool is_k = b < nb;
+      const int bb = is_k ? b : b - nb;
+      const int cnt = min(32, nkv - 32 * bb);
+      q8_quant_block(is_k ? kr + 32 * bb : v + 32 * bb, cnt, (is_k ? rowk : rowv) + 34 * bb);
+    }
+  } else {
+    float *fk = reinterpret_cast<float *>(rowk), *fv = reinterpret_cast<float *>(rowv);
+    for (int e = threadIdx.x; e < nkv; e += blockDim.x) {
+      fk[e] = kr[e];
+      fv[e] = v[e];
+    }
+  }
+  __syncthreads();
+  const size_t off = ((size_t)layer * (size_t)sd.ctx_cap + (size_t)pos) * sh.row_bytes;
+  uint32_t *gk = reinterpret_cast<uint32_t *>(sd.k + off);
+  uint32_t *gv = reinterpret_cast<uint32_t *>(sd.v + off);
+  const uint32_t *lk = reinterpret_cast<const uint32_t *>(rowk);
+  const uint32_t *lv = reinterpret_cast<const uint32_t *>(rowv);
+  for (uint32_t i = threadIdx.x; i < sh.row_bytes / 4; i += blockDim.x) {
+    gk[i] = lk[i];
+    gv[i] = lv[i];
+  }
+}
+
+// Specialised shapes: workgroup (split, seq, layer) rotates its q into LDS,
+// appends the new row if its split holds pos (and reads that row back from
+// LDS, not HBM), streams its positions and writes one partial per wave and
+// head; k_combine merges the partials and writes the output over q
+// (l5_model.c:513-578).  A merge inside this kernel (last workgroup of a
+// (seq, layer) by an atomic counter) measured slower: its agent-scope fences
+// and the merge at the tail of every launch cost more than one more launch.
+// FMT: 0 = F32 KV, 1 = Q8_0 KV.  HD: head_dim.  CD: elements per lane.
+// G: q heads per KV head.  U: wave-steps consumed per loop trip.
+// ATT: also write the raw scores for the reference-layout softmax weights.
+// STG: how KV rows reach the lanes.  0: per-lane loads straight from HBM.
+// 1: chunks of P.stage_rows rows pulled into the wave's LDS region by
+// global_load_lds, then read from there.  2: the same chunks loaded into
+// registers with coalesced non-temporal loads one chunk ahead (in flight
+// while the current chunk is consumed) and written to LDS.
+template <int FMT, int HD, int CD, int G, int U, bool ATT, int STG>
+__global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int LPH = HD / CD;  // lanes per head
+  using C = Codec<FMT, CD>;
+  const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  const int t0 = split * P.split_len;
+  if (t0 >= npos) return;  // a shorter sequence of a ragged batch: no split here
+  const int t1 = min(npos, t0 + P.split_len);
+  const bool owns_new = t1 == npos;  // this split holds position pos
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int LPP = P.sh.n_kv_heads * LPH;  // lanes per position (<= 64, checked on host)
+  const int PPW = 64 / LPP;               // positions per wave-step
+  const int slot = lane / LPP;
+  const bool lane_on = slot < PPW;
+  const int slot_ld = lane_on ? slot : 0;  // idle lanes shadow slot 0's rows
+  const int r = lane_on ? lane - slot * LPP : 0;
+  const int g = r / LPH, c = r - g * LPH;
+  const int layer = P.layer0 + li;
+  const int n_heads = P.sh.n_heads;
+  const int nkv = P.sh.n_kv_heads * HD;
+  const size_t nq = (size_t)n_heads * HD;
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const size_t row = P.sh.row_bytes;
+  const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+
+  // LDS: rotated q (nq floats) and rotated new k (nkv floats) at 0 - with
+  // STG, the waves' staging regions overlap them once q is in registers -
+  // then the new K and V rows and the QK-RMSNorm scratch (n_heads floats).
+  const LdsLayout ll = layer_lds_layout(P.sh, STG ? P.stage_rows : 0);
+  float *qrot = reinterpret_cast<float *>(lds);
+  float *kr = reinterpret_cast<float *>(lds + nq * 4);
+  uint8_t *rowk = lds + ll.rows;
+  uint8_t *rowv = rowk + ll.row_pad;
+  float *inv = reinterpret_cast<float *>(rowv + ll.row_pad);
+  {
+    // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by pair
+    // as the append does (l3_math.c:74-101)
+    const float *qi = P.q_in + sidx * nq;
+    if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
+      for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
+      __syncthreads();
+      qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, inv);
+      qi = qrot;  // rotate in place: each pair is read and written by one thread
+    }
+    constexpr int half = HD / 2;
+    for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
+      const int h = pr / half, j = pr - h * half;
+      int ia, ib;
+      rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
+      float a = qi[h * HD + ia], b = qi[h * HD + ib];
+      if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+      qrot[h * HD + ia] = a;
+      qrot[h * HD + ib] = b;
+    }
+  }
+  if (owns_new)  // (its barriers also publish qrot)
+    append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
+                   P.norm, kr, rowk, rowv, inv);
+  else
+    __syncthreads();
+
+  float q[G][CD];
+#pragma unroll
+  for (int i = 0; i < G; i++)
+#pragma unroll
+    for (int j = 0; j < CD; j += 4) {
+      const float4 v4 =
+          *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
+      q[i][j + 0] = v4.x * P.qscale;
+      q[i][j + 1] = v4.y * P.qscale;
+      q[i][j + 2] = v4.z * P.qscale;
+      q[i][j + 3] = v4.w * P.qscale;
+    }
+  [[maybe_unused]] QDigits<CD> qd[G];
+  if constexpr (FMT == 1) {
+#pragma unroll
+    for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
+  }
+  if constexpr (STG != 0) __syncthreads();  // every wave has its q: staging may overwrite qrot
+  const LaneOff lo = C::offsets(g * HD + c * CD);
+  const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
+  const size_t ustep = (size_t)stride * row;  // bytes between them
+  const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+  const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+
+  float m[G], l[G], acc[G][CD];
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    m[i] = kNegBig;
+    l[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < CD; j++) acc[i][j] = 0.f;
+  }
+  [[maybe_unused]] float *att_h = nullptr;
+  if constexpr (ATT)
+    att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
+
+  // Scores, online softmax and V for UU positions already loaded.
+  auto consume = [&](const typename C::Raw *kr_, const typename C::Raw *vr_, const bool *valid,
+                     const int *tpos, auto nu, auto check) {
+    constexpr int UU = decltype(nu)::value;
+    constexpr bool CHECK = decltype(check)::value;
+    float sc[UU][G];
+#pragma unroll
+    for (int u = 0; u < UU; u++) {
+      if constexpr (FMT == 1) {
+        uint32_t w[CD / 4];
+        float ks;
+        C::quants(kr_[u], w, ks, lo);
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
+          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
+        }
+      } else {
+        float kf[CD];
+        C::values(kr_[u], kf);
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+          for (int j = 0; j < CD; j += 2) {
+            s0 = fmaf(q[i][j], kf[j], s0);
+            s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
+          }
+          const float s = group_sum<LPH>(s0 + s1);
+          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
+        }
+      }
+    }
+    bool need = false;
+    float mn[G];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float mx = m[i];
+#pragma unroll
+      for (int u = 0; u < UU; u++) mx = fmaxf(mx, sc[u][i]);
+      mn[i] = mx;
+      need |= mx > m[i];
+    }
+    if (__any(need)) {
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        const float a = fast_exp2(m[i] - mn[i]);
+        l[i] *= a;
+#pragma unroll
+        for (int j = 0; j < CD; j++) acc[i][j] *= a;
+        m[i] = mn[i];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UU; u++) {
+      float p[G];
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        p[i] = fast_exp2(sc[u][i] - m[i]);
+        l[i] += p[i];
+      }
+      if constexpr (FMT == 1) {
+        uint32_t w[CD / 4];
+        float vs;
+        C::quants(vr_[u], w, vs, lo);
+        float pv[G];
+#pragma unroll
+        for (int i = 0; i < G; i++) pv[i] = p[i] * vs;
+#pragma unroll
+        for (int j = 0; j < CD / 4; j++)
+#pragma unroll
+          for (int b = 0; b < 4; b++) {
+            const float x = i8f(w[j], b);
+#pragma unroll
+            for (int i = 0; i < G; i++) acc[i][4 * j + b] = fmaf(pv[i], x, acc[i][4 * j + b]);
+          }
+      } else {
+        float vf[CD];
+        C::values(vr_[u], vf);
+#pragma unroll
+        for (int j = 0; j < CD; j++)
+#pragma unroll
+          for (int i = 0; i < G; i++) acc[i][j] = fmaf(p[i], vf[j], acc[i][j]);
+      }
+      if constexpr (ATT) {
+        if (c == 0 && valid[u]) {
+#pragma unroll
+          for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tpos[u]] = sc[u][i];
+        }
+      }
+    }
+  };
+
+  // Positions [t0, tend) stream from HBM; pos itself, when owned, from LDS.
+  const int tend = owns_new ? t1 - 1 : t1;
+  auto trip = [&](int tb, auto check) {
+    constexpr bool CHECK = decltype(check)::value;
+    typename C::Raw krr[U], vrr[U];
+    bool valid[U];
+    int tpos[U];
+    const size_t base = (size_t)(tb + slot_ld) * row;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      size_t off = base + (size_t)u * ustep;
+      tpos[u] = tb + u * stride + slot;
+      if constexpr (CHECK) {
+        valid[u] = lane_on && tpos[u] < tend;
+        if (!valid[u]) off = (size_t)t0 * row;
+      } else {
+        valid[u] = lane_on;
+      }
+      C::load(krr[u], kb + off, lo);
+      C::load(vrr[u], vb + off, lo);
+    }
+    consume(krr, vrr, valid, tpos, std::integral_constant<int, U>{}, check);
+  };
+  if constexpr (STG != 0) {
+    // Wave w takes chunks of R contiguous positions: [t0 + (w + 4i) R, +R).
+    // A chunk's K and V bytes are contiguous (rows of a layer are), so they
+    // move as 16-byte pieces, lane l taking pieces l, l + 64, ..., into the
+    // wave's LDS region (each HBM byte fetched once, by one lane,
+    // non-temporal); then every lane reads its blocks from there.
+    const int R = P.stage_rows;
+    const uint32_t cbytes = (uint32_t)R * (uint32_t)row;
+    uint8_t *sk = lds + (size_t)wave * 2 * cbytes, *sv = sk + cbytes;
+    const int steps = R / PPW;
+    // U wave-steps of the chunk from LDS; rows past nrows (and idle lanes)
+    // read row 0 of the chunk and are masked out of the softmax.
+    auto lds_trip = [&](int cs, int s, int nrows, auto nu, auto check) {
+      constexpr int UU = decltype(nu)::value;
+      constexpr bool CHECK = decltype(check)::value;
+      typename C::Raw krr[UU], vrr[UU];
+      bool valid[UU];
+      int tpos[UU];
+#pragma unroll
+      for (int u = 0; u < UU; u++) {
+        const int r = (s + u) * PPW + slot;
+        valid[u] = CHECK ? (lane_on && r < nrows) : lane_on;
+        const size_t ro = valid[u] ? (size_t)r * row : 0;
+        tpos[u] = cs + r;
+        C::load_lds(krr[u], sk + ro, lo);
+        C::load_lds(vrr[u], sv + ro, lo);
+      }
+      consume(krr, vrr, valid, tpos, nu, check);
+    };
+    // Every lane's blocks of a chunk of nrows rows, read from LDS.
+    auto consume_chunk = [&](int cs, int nrows) {
+      if (nrows == R) {
+        int s = 0;
+        for (; s + U <= steps; s += U)
+          lds_trip(cs, s, nrows, std::integral_constant<int, U>{}, std::false_type{});
+        for (; s < steps; s++)
+          lds_trip(cs, s, nrows, std::integral_constant<int, 1>{}, std::false_type{});
+      } else {
+        for (int s = 0; s * PPW < nrows; s += U)
+          lds_trip(cs, s, nrows, std::integral_constant<int, U>{}, std::true_type{});
+      }
+    };
+    const int cstride = kWavesPerSplit * R;  // positions between a wave's chunks
+    if constexpr (STG == 1) {
+      for (int cs = t0 + wave * R; cs < tend; cs += cstride) {
+        const int nrows = min(R, tend - cs);
+        const uint32_t np = (uint32_t)nrows * (uint32_t)row / 16u;  // 16-byte pieces
+        const uint8_t *gk = kb + (size_t)cs * row + 16u * (uint32_t)lane;
+        const uint8_t *gv = vb + (size_t)cs * row + 16u * (uint32_t)lane;
+        for (uint32_t i = 0; 64u * i < np; i++) {
+          if (64u * i + (uint32_t)lane < np) {
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(gk + 1024u * i),
+                (__attribute__((address_space(3))) void *)(sk + 1024u * i), 16, 0, kAuxNT);
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void *)(gv + 1024u * i),
+                (__attribute__((address_space(3))) void *)(sv + 1024u * i), 16, 0, kAuxNT);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the chunk is in LDS
+        consume_chunk(cs, nrows);
+        // The next chunk's loads overwrite this region only after every value
+        // read from it above has been used (data dependence orders them).
+      }
+    } else {
+      // Registers hold the next chunk (kStageLoads 16-byte pieces per lane
+      // and tensor at most) while the current one is consumed.
+      u32x4 rk[kStageLoads], rv[kStageLoads];
+      auto issue = [&](int cs) {
+        const uint32_t np = (uint32_t)min(R, tend - cs) * (uint32_t)row / 16u;
+        const uint8_t *gk = kb + (size_t)cs * row + 16u * (uint32_t)lane;
+        const uint8_t *gv = vb + (size_t)cs * row + 16u * (uint32_t)lane;
+#pragma unroll
+        for (int i = 0; i < kStageLoads; i++) {
+          if (64u * (uint32_t)i + (uint32_t)lane < np) {
+            rk[i] = __builtin_nontemporal_load(
+                (const __attribute__((address_space(1))) u32x4 *)(gk + 1024u * i));
+            rv[i] = __builtin_nontemporal_load(
+                (const __attribute__((address_space(1))) u32x4 *)(gv + 1024u * i));
+          }
+        }
+      };
+      auto stash = [&](int cs) {
+        const uint32_t np = (uint32_t)min(R, tend - cs) * (uint32_t)row / 16u;
+#pragma unroll
+        for (int i = 0; i < kStageLoads; i++) {
+          const uint32_t pc = 64u * (uint32_t)i + (uint32_t)lane;
+          if (pc < np) {
+            *reinterpret_cast<u32x4 *>(sk + 16u * pc) = rk[i];
+            *reinterpret_cast<u32x4 *>(sv + 16u * pc) = rv[i];
+          }
+        }
+      };
+      int cs = t0 + wave * R;
+      if (cs < tend) issue(cs);
+      for (; cs < tend; cs += cstride) {
+        // (the previous chunk's LDS reads were all used before this point)
+        stash(cs);
+        if (cs + cstride < tend) issue(cs + cstride);
+        consume_chunk(cs, min(R, tend - cs));
+      }
+    }
+  } else {
+    const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
+    int tb = t0 + wave * PPW;
+    if (tend > t0) {  // (a split of one position may hold only pos)
+      for (; tb + trip_span <= tend; tb += stride * U) trip(tb, std::false_type{});
+      for (; tb < tend; tb += stride * U) trip(tb, std::true_type{});
+    }
+  }
+  if (owns_new) {
+    typename C::Raw krr[1], vrr[1];
+    C::load_lds(krr[0], rowk, lo);
+    C::load_lds(vrr[0], rowv, lo);
+    const bool valid[1] = {wave == 0 && slot == 0};
+    const int tpos[1] = {sd.pos};
+    consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
+  }
+
+  // Fold the PPW position slots of the wave into slot 0.  Every lane takes
+  // part in the shuffles, but only slot-0 lanes update their state, so the
+  // state read from slot k is always slot k's own.
+  const bool gather = slot == 0;
+  for (int k = 1; k < PPW; k++) {
+    const int src = (lane + k * LPP) & 63;
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      const float m2 = __shfl(m[i], src);
+      const float l2 = __shfl(l[i], src);
+      const float M = fmaxf(m[i], m2);
+      const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
+      l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
+#pragma unroll
+      for (int j = 0; j < CD; j++) {
+        const float a2 = __shfl(acc[i][j], src);
+        acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
+      }
+      m[i] = gather ? M : m[i];
+    }
+  }
+  // Merge the four waves' states in LDS (the rows and q there are no longer
+  // read once every wave is past this barrier) and write one partial per
+  // head for the split.  LDS: [wave][head][kPartHead + HD] floats.
+  constexpr int pstr = kPartHead + HD;
+  __syncthreads();
+  float *ws = reinterpret_cast<float *>(lds);
+  if (slot == 0) {
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+      float *pw = ws + ((size_t)wave * n_heads + (size_t)(g * G + i)) * pstr;
+      if (c == 0) {
+        pw[0] = m[i];
+        pw[1] = l[i];
+      }
+#pragma unroll
+      for (int j = 0; j < CD; j += 4)
+        *reinterpret_cast<float4 *>(pw + kPartHead + c * CD + j) =
+            make_float4(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3]);
+    }
+  }
+  __syncthreads();
+  const size_t wstr = (size_t)n_heads * pstr;
+  for (int e = threadIdx.x; e < n_heads * HD; e += blockDim.x) {
+    const int h = e / HD, d = e - h * HD;
+    const float *pw = ws + (size_t)h * pstr;
+    float M = pw[0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
+    float o = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerSplit; w++) {
+      const float f = exp2f(pw[w * wstr] - M);
+      o = fmaf(pw[w * wstr + kPartHead + d], f, o);
+      lsum = fmaf(pw[w * wstr + 1], f, lsum);
+    }
+    float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
+                          (size_t)split) * pstr;
+    pp[kPartHead + d] = o;
+    if (d == 0) {
+      pp[0] = M;
+      pp[1] = lsum;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- launchers
+
+static inline size_t layer_lds_bytes(const ShapeDev &sh, int32_t stage_rows) {
+  return layer_lds_layout(sh, stage_rows).total;
+}
+
+template <int FMT, int HD, int CD, int G, int U, int STG>
+static hipError_t launch_fast_s(const DecodeParams &p, int n_layers, hipStream_t s) {
+  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  const size_t lds = layer_lds_bytes(p.sh, STG ? p.stage_rows : 0);
+  if (p.att)
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG>), grid, dim3(kThreads), lds, s, p);
+  else
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, false, STG>), grid, dim3(kThreads), lds, s, p);
+  return hipGetLastError();
+}
+
+template <int FMT, int HD, int CD, int G, int U>
+static hipError_t launch_fast_u(const DecodeParams &p, int n_layers, hipStream_t s) {
+  if (p.stage_rows > 0 && p.stage_mode == 1) return launch_fast_s<FMT, HD, CD, G, U, 1>(p, n_layers, s);
+  if (p.stage_rows > 0 && p.stage_mode == 2) return launch_fast_s<FMT, HD, CD, G, U, 2>(p, n_layers, s);
+  return launch_fast_s<FMT, HD, CD, G, U, 0>(p, n_layers, s);
+}
+
+template <int FMT, int HD, int CD, int G>
+static hipError_t launch_fast(const DecodeParams &p, int n_layers, hipStream_t s) {
+  if (p.tune_unroll == 4) return launch_fast_u<FMT, HD, CD, G, 4>(p, n_layers, s);
+  return launch_fast_u<FMT, HD, CD, G, 2>(p, n_layers, s);
+}
+
+// Q8_0 with group <= 2 defaults to a whole block per lane (half a block when
+// tuned so); every other shape uses 16 elements per lane.
+template <int FMT, int HD, int G>
+hipError_t launch_layer(const DecodeParams &p, int n_layers, hipStream_t s) {
+  if constexpr (FMT == 1 && G <= 2) {
+    if (p.tune_chunk == 16) return launch_fast<1, HD, 16, G>(p, n_layers, s);
+    return launch_fast<1, HD, 32, G>(p, n_layers, s);
+  } else {
+    return launch_fast<FMT, HD, 16, G>(p, n_layers, s);
+  }
+}
+
+template <int FMT, int HD, int G>
+int layer_occupancy(const ShapeDev &sh, int32_t stage_rows) {
+  constexpr int CD = (FMT == 1 && G <= 2) ? 32 : 16;
+  int n = 0;
+  const hipError_t e =
+      stage_rows > 0 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                           &n, k_layer<FMT, HD, CD, G, 2, false, kDefaultStageMode>, kThreads,
+                           layer_lds_bytes(sh, stage_rows))
+                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                           &n, k_layer<FMT, HD, CD, G, 2, false, 0>, kThreads,
+                           layer_lds_bytes(sh, 0));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return 1;
+  }
+  return n > 0 ? n : 1;
+}
+
+}  // namespace g2b
