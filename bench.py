@@ -125,17 +125,18 @@ def main():
     ap.add_argument("--cpu-min-s", type=float, default=8.0,
                     help="repeat each CPU sample until it has run this long")
     ap.add_argument("--split", type=int, default=0, help="decode split length (0 = automatic)")
-    ap.add_argument("--unroll", type=int, default=0, help="decode wave-steps per trip (0 = auto)")
     ap.add_argument("--chunk", type=int, default=0, help="Q8 elements per lane (0 = auto)")
     ap.add_argument("--stage", type=int, default=0, choices=(-1, 0, 1, 2),
                     help="KV row path: -1 per-lane HBM loads, 1 global_load_lds chunks, "
                          "2 register-pipelined chunks through LDS (0 = automatic)")
+    ap.add_argument("--piece", type=int, default=0,
+                    help="schedule: -1 static splits, >0 work-queue piece length (0 = automatic)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one plain copy kernel of this many MiB (a "
                          "known-size reference for rocprofv3 byte counters)")
     ap.add_argument("--sweep-splits", default="", help="comma list: time layer-serial per split")
     ap.add_argument("--sweep-variants", default="",
-                    help="semicolon list of split,unroll,chunk[,stage]: time layer-serial and fused")
+                    help="semicolon list of split,chunk,stage,piece: time layer-serial and fused")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -162,7 +163,7 @@ def main():
     log(f"{args.config}: {desc}; n_seq={n_seq}, KV {kv_total / 1e9:.2f} GB")
 
     ctx = attn.Context(shape)
-    ctx.tune(args.split, args.unroll, args.chunk, args.stage)
+    ctx.tune(args.split, args.chunk, args.stage, args.piece)
     stream = ctx.stream
     t0 = time.perf_counter()
     kvs = [ctx.kv_alloc(c) for c in caps]
@@ -225,21 +226,21 @@ def main():
 
     if args.sweep_splits:
         for sl in [int(x) for x in args.sweep_splits.split(",")]:
-            ctx.tune(sl, args.unroll, args.chunk, args.stage)
+            ctx.tune(sl, args.chunk, args.stage, args.piece)
             sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
             log(f"split {sl}: {sms * 1e3:.1f} us/step, {step_bytes(shape, poss) / sms / 1e6:.1f} "
                 f"GB/s, k_layer avg {sd / max(sn, 1) * 1e3:.1f} us")
-        ctx.tune(args.split, args.unroll, args.chunk, args.stage)
+        ctx.tune(args.split, args.chunk, args.stage, args.piece)
     if args.sweep_variants:
         for v in args.sweep_variants.split(";"):
-            sl, un, ch, *st = [int(x) for x in v.split(",")]
-            ctx.tune(sl, un, ch, st[0] if st else 0)
+            sl, ch, st, pc = [int(x) for x in v.split(",")]
+            ctx.tune(sl, ch, st, pc)
             sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
             fms, _, fd, fn = timed(step_fused, max(3, args.steps // 2), 1)
-            log(f"variant split={sl} unroll={un} chunk={ch} stage={st[0] if st else 0}: layer-serial {sms * 1e3:.1f} us/step "
+            log(f"variant split={sl} chunk={ch} stage={st} piece={pc}: layer-serial {sms * 1e3:.1f} us/step "
                 f"({step_bytes(shape, poss) / sms / 1e6:.1f} GB/s, k_layer {sd / max(sn, 1) * 1e3:.1f}"
                 f" us), fused {fms * 1e3:.1f} us/step ({step_bytes(shape, poss) / fms / 1e6:.1f} GB/s)")
-        ctx.tune(args.split, args.unroll, args.chunk, args.stage)
+        ctx.tune(args.split, args.chunk, args.stage, args.piece)
 
     ms, wall_ms, dec_ms, dec_n = timed(step_layer_serial, args.steps, args.warmup)
     sb = step_bytes(shape, poss)

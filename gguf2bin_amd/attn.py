@@ -266,10 +266,11 @@ class Context:
     def synth_copy(self, dst: int, src: int, nbytes: int):
         self._check(lib().g2b_synth_copy(self.h, dst, src, nbytes), "g2b_synth_copy")
 
-    def tune(self, split_len: int = 0, unroll: int = 0, chunk: int = 0, stage: int = 0):
-        """Decode-kernel tuning (0 = automatic): split length, unroll, Q8 chunk,
-        KV row path (-1 per-lane HBM loads, 1 / 2 staged through LDS)."""
-        self._check(lib().g2b_ctx_tune(self.h, split_len, unroll, chunk, stage), "g2b_ctx_tune")
+    def tune(self, split_len: int = 0, chunk: int = 0, stage: int = 0, piece: int = 0):
+        """Decode-kernel tuning (0 = automatic): static split length, Q8 chunk,
+        KV row path (-1 per-lane HBM loads, 1 / 2 staged through LDS), schedule
+        (-1 static splits, > 0 work-queue piece length in positions)."""
+        self._check(lib().g2b_ctx_tune(self.h, split_len, chunk, stage, piece), "g2b_ctx_tune")
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

@@ -53,9 +53,17 @@ struct g2b_ctx {
   std::vector<int32_t> qkn_on_h;
   float qkn_eps = 0.f;
 
-  int32_t slots = 0;           // resident decode workgroups on the device
+  int32_t n_cu = 1;            // compute units of the device
+  int32_t occ_cache[2][3][2];  // workgroups per CU by (half-block lanes, stage mode, work queue)
   int32_t split_override = 0;  // g2b_ctx_tune
-  int32_t tune_unroll = 0, tune_chunk = 0;
+  int32_t tune_chunk = 0;
+  int32_t tune_piece = 0;      // -1: static splits only; > 0: work-queue piece length
+
+  // work-queue counters of k_layer: two sets of wq_cap units (DecodeParams.wq)
+  int32_t *wq = nullptr;
+  int32_t wq_cap = 0, wq_set = 0;
+  int32_t wq_dirty[2] = {0, 0};  // units of each set a launch may have left non-zero
+  bool wq_reset = false;         // a launch failed after using the counters
   int32_t tune_stage = 0;      // -1: k_layer loads straight from HBM; 1, 2: staging mode
 
   // decode-launch timing (g2b_ctx_profile)
@@ -168,10 +176,16 @@ int ensure_rope(g2b_ctx *c, int32_t len) {
 // rounds as the minimum split length forces.  At most 512 splits per
 // sequence (each is one partial per head for the combine, which stages a
 // weight per partial in LDS) and the generic kernel's LDS limit apply.
-int32_t choose_split(const g2b_ctx *c, int64_t total_pos, int32_t max_pos, int32_t n_layers,
-                     bool fast) {
+// Resident k_layer workgroups on the device for the variant of dp (cached).
+int32_t slots_for(g2b_ctx *c, const DecodeParams &dp, bool wq) {
+  int32_t &occ = c->occ_cache[dp.tune_chunk == 16 ? 1 : 0][dp.stage_mode][wq ? 1 : 0];
+  if (occ <= 0) occ = decode_blocks_per_cu(c->sh, dp.tune_chunk, dp.stage_mode, dp.stage_rows, wq);
+  return std::max(1, c->n_cu) * std::max(1, occ);
+}
+
+int32_t choose_split(const g2b_ctx *c, int64_t slots, int64_t total_pos, int32_t max_pos,
+                     int32_t n_layers, bool fast) {
   const int64_t work = total_pos * (int64_t)n_layers;
-  const int64_t slots = std::max<int64_t>(c->slots, 1);
   int64_t sl = c->split_override > 0 ? c->split_override : (work + slots - 1) / slots;
   if (c->split_override <= 0) sl = std::max<int64_t>(sl, 64);
   const int64_t min_for_cap = ((int64_t)max_pos + 1 + 511) / 512;
@@ -195,17 +209,6 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   const int32_t nh = c->shape.n_heads, hd = c->shape.head_dim;
   const size_t nq = (size_t)nh * hd;
   const bool fast = decode_fast_available(c->sh);
-  const int32_t split_len = choose_split(c, total_pos, max_pos, n_layers, fast);
-  const int32_t max_splits = (max_pos + 1 + split_len - 1) / split_len;
-  if (max_splits > 512)
-    return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
-
-  const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
-                             (size_t)(kPartHead + hd);
-  if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
-  if (!fast) {
-    if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
-  }
 
   DecodeParams dp{};
   dp.sh = c->sh;
@@ -213,8 +216,6 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.one = one;
   dp.n_seq = n_seq;
   dp.layer0 = layer0;
-  dp.split_len = split_len;
-  dp.max_splits = max_splits;
   dp.q_rot = c->qrot;
   dp.q_out = q;
   dp.q_in = q;
@@ -222,17 +223,82 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.v_in = v;
   dp.rope = c->rope;
   dp.norm = norm_of(c);
-  dp.part = c->part;
   dp.att = att;
   dp.att_stride = att_stride;
   dp.qscale = c->qscale;
-  dp.tune_unroll = c->tune_unroll;
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
   dp.stage_mode = c->tune_stage < 0 ? 0 : c->tune_stage > 0 ? c->tune_stage : kDefaultStageMode;
-  dp.stage_rows = decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode);
+  dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
+  dp.n_layers_call = n_layers;
+
+  // Work queue when every unit (sequence, layer) can have a resident
+  // workgroup and few enough waves share each unit's counters; otherwise
+  // static splits, sized so the launch's workgroups form whole rounds.
+  const int64_t n_units = (int64_t)n_seq * n_layers;
+  const int64_t wq_slots = fast && dp.stage_mode != 0 ? slots_for(c, dp, true) : 0;
+  const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 && n_units <= wq_slots &&
+                      (c->tune_piece > 0 ||
+                       wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
+  const int64_t slots = use_wq ? wq_slots : slots_for(c, dp, false);
+  int32_t max_splits;
+  if (use_wq) {
+    if (n_units > c->wq_cap) {
+      G2B_HIP(c, hipStreamSynchronize(c->stream));
+      if (c->wq) G2B_HIP(c, hipFree(c->wq));
+      c->wq = nullptr;
+      c->wq_cap = 0;
+      const int32_t cap = (int32_t)std::max<int64_t>(n_units, 256);
+      const size_t bytes = (size_t)2 * cap * kWqStride * sizeof(int32_t);
+      if (hipMalloc((void **)&c->wq, bytes) != hipSuccess) {
+        c->wq = nullptr;
+        (void)hipGetLastError();
+        return fail(c, G2B_ENOMEM, "work-queue counters");
+      }
+      c->wq_cap = cap;
+      c->wq_reset = true;
+    }
+    if (c->wq_reset) {
+      G2B_HIP(c, hipMemsetAsync(c->wq, 0, (size_t)2 * c->wq_cap * kWqStride * sizeof(int32_t),
+                                c->stream));
+      c->wq_set = 0;
+      c->wq_dirty[0] = c->wq_dirty[1] = 0;
+      c->wq_reset = false;
+    }
+    max_splits = (int32_t)std::min<int64_t>(
+        std::max<int64_t>(kWqMinParts, (slots + n_units - 1) / n_units + 8), 2048);
+    const int32_t R = dp.stage_rows;
+    const int64_t streamed = (total_pos - n_seq) * (int64_t)n_layers;  // positions [0, pos)
+    int64_t pl = c->tune_piece > 0 ? c->tune_piece
+                                   : streamed / (slots * kWavesPerSplit * kWqClaimsPerWave);
+    pl = std::min<int64_t>(std::max<int64_t>(pl, R), (int64_t)64 * R);
+    dp.piece_len = (int32_t)(pl - pl % R);
+    dp.piece_big = dp.piece_len * kWqBigFactor;
+    dp.wq = c->wq;
+    dp.wq_set = c->wq_set;
+    dp.wq_cap = c->wq_cap;
+    dp.wq_zero_units = c->wq_dirty[c->wq_set ^ 1];
+    dp.wq_grid = (int32_t)slots;
+    dp.split_len = 0;
+  } else {
+    const int32_t split_len = choose_split(c, slots, total_pos, max_pos, n_layers, fast);
+    max_splits = (max_pos + 1 + split_len - 1) / split_len;
+    if (max_splits > 512)
+      return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
+    dp.split_len = split_len;
+  }
+  dp.max_splits = max_splits;
+
+  const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
+                             (size_t)(kPartHead + hd);
+  if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
+  if (!fast) {
+    if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
+  }
+  dp.part = c->part;
+  dp.q_rot = c->qrot;
 
   if (!fast) {  // generic shapes: append, decode, combine
     AppendParams ap{};
@@ -264,9 +330,17 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     c->prof_used += 2;
     G2B_HIP(c, hipEventRecord(ev0, c->stream));
   }
+  if (use_wq) c->wq_reset = true;  // until both launches below are queued
   G2B_HIP(c, launch_decode(dp, n_layers, c->stream, &used_fast));
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
   G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
+  if (use_wq) {
+    // this launch dirtied its set; the combine zeroed the other one
+    c->wq_dirty[c->wq_set] = std::max<int32_t>(c->wq_dirty[c->wq_set], (int32_t)n_units);
+    c->wq_dirty[c->wq_set ^ 1] = 0;
+    c->wq_set ^= 1;
+    c->wq_reset = false;
+  }
   return G2B_OK;
 }
 
@@ -341,7 +415,8 @@ int g2b_ctx_create(g2b_ctx **out, int32_t device, const g2b_shape *s) {
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     n_cu = 0;
   (void)hipGetLastError();
-  c->slots = std::max(1, n_cu) * decode_blocks_per_cu(c->sh);
+  c->n_cu = std::max(1, n_cu);
+  memset(c->occ_cache, 0, sizeof c->occ_cache);
   *out = c;
   return G2B_OK;
 }
@@ -359,6 +434,7 @@ int g2b_ctx_destroy(g2b_ctx *c) {
   if (c->hstage) (void)hipFree(c->hstage);
   if (c->qkn_w) (void)hipFree(c->qkn_w);
   if (c->qkn_on) (void)hipFree(c->qkn_on);
+  if (c->wq) (void)hipFree(c->wq);
   if (c->seqs_ev) (void)hipEventDestroy(c->seqs_ev);
   for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -624,14 +700,14 @@ int g2b_synth_copy(g2b_ctx *c, void *dst, const void *src, uint64_t nbytes) {
   return G2B_OK;
 }
 
-int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t unroll, int32_t chunk, int32_t stage) {
-  if (!c || split_len < 0 || (unroll != 0 && unroll != 2 && unroll != 4) ||
-      (chunk != 0 && chunk != 16 && chunk != 32) || stage < -1 || stage > 2)
+int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t chunk, int32_t stage, int32_t piece) {
+  if (!c || split_len < 0 || (chunk != 0 && chunk != 16 && chunk != 32) || stage < -1 ||
+      stage > 2 || piece < -1)
     return G2B_EINVAL;
   c->split_override = split_len;
-  c->tune_unroll = unroll;
   c->tune_chunk = chunk;
   c->tune_stage = stage;
+  c->tune_piece = piece;
   return G2B_OK;
 }
 

@@ -134,8 +134,20 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
   const int h = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
   const int npos = sd.pos + 1;
-  const int nsplit = (npos + P.split_len - 1) / P.split_len;
-  const int np = nsplit;
+  const size_t unit = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  int np;
+  if (P.wq) {  // work queue: the partial slots the visits reserved
+    const int32_t *ctr = P.wq + ((size_t)P.wq_set * P.wq_cap + unit) * kWqStride;
+    np = min(ctr[1], P.max_splits);
+    // zero the next launch's counter set (its used extent, from the host)
+    int32_t *nxt = P.wq + (size_t)(P.wq_set ^ 1) * P.wq_cap * kWqStride;
+    const size_t nblk = (size_t)gridDim.x * gridDim.y * gridDim.z;
+    const size_t bid = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z);
+    for (size_t uu = bid; uu < (size_t)P.wq_zero_units; uu += nblk)
+      if (threadIdx.x < 2) nxt[uu * kWqStride + threadIdx.x] = 0;
+  } else {
+    np = (npos + P.split_len - 1) / P.split_len;
+  }
   const int HD = P.sh.head_dim, nh = P.sh.n_heads;
   const size_t pstr = (size_t)(kPartHead + HD);
   const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
@@ -211,16 +223,18 @@ int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode) 
 }
 
 template <int FMT, int HD>
-static int occupancy_hd(const ShapeDev &sh, int group, int32_t sr) {
+static int occupancy_hd(const ShapeDev &sh, int group, int32_t chunk, int32_t mode, int32_t sr,
+                        bool wq) {
   switch (group) {
-    case 1: return layer_occupancy<FMT, HD, 1>(sh, sr);
-    case 2: return layer_occupancy<FMT, HD, 2>(sh, sr);
-    case 3: return layer_occupancy<FMT, HD, 3>(sh, sr);
-    default: return layer_occupancy<FMT, HD, 4>(sh, sr);
+    case 1: return layer_occupancy<FMT, HD, 1>(sh, chunk, mode, sr, wq);
+    case 2: return layer_occupancy<FMT, HD, 2>(sh, chunk, mode, sr, wq);
+    case 3: return layer_occupancy<FMT, HD, 3>(sh, chunk, mode, sr, wq);
+    default: return layer_occupancy<FMT, HD, 4>(sh, chunk, mode, sr, wq);
   }
 }
 
-int decode_blocks_per_cu(const ShapeDev &sh) {
+int decode_blocks_per_cu(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
+                         int32_t stage_rows, bool wq) {
   if (!decode_fast_available(sh)) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_decode_generic, kThreads, 0) !=
@@ -231,12 +245,11 @@ int decode_blocks_per_cu(const ShapeDev &sh) {
     return n > 0 ? n : 1;
   }
   const int group = sh.n_heads / sh.n_kv_heads;
-  const int32_t sr = decode_stage_rows(sh, 0, kDefaultStageMode);
   if (sh.kv_q8)
-    return sh.head_dim == 128 ? occupancy_hd<1, 128>(sh, group, sr)
-                              : occupancy_hd<1, 64>(sh, group, sr);
-  return sh.head_dim == 128 ? occupancy_hd<0, 128>(sh, group, sr)
-                            : occupancy_hd<0, 64>(sh, group, sr);
+    return sh.head_dim == 128 ? occupancy_hd<1, 128>(sh, group, tune_chunk, stage_mode, stage_rows, wq)
+                              : occupancy_hd<1, 64>(sh, group, tune_chunk, stage_mode, stage_rows, wq);
+  return sh.head_dim == 128 ? occupancy_hd<0, 128>(sh, group, tune_chunk, stage_mode, stage_rows, wq)
+                            : occupancy_hd<0, 64>(sh, group, tune_chunk, stage_mode, stage_rows, wq);
 }
 
 bool decode_fast_available(const ShapeDev &sh) {

@@ -21,16 +21,16 @@ constexpr int kGenericMaxSplit = 1024;  // positions per split in the generic ke
 // contiguous K and V rows into its own LDS region with coalesced 16-byte
 // non-temporal loads, and its lanes read their blocks from there.  Needs
 // rows that are whole 16-byte pieces.  Mode 1 (global_load_lds straight into
-// LDS) uses chunks of about 8704 bytes of K (and as much of V); mode 2
-// (registers one chunk ahead, then LDS) about 4352 bytes, at most
-// kStageLoads pieces per lane and tensor.  A chunk is a whole number of
-// wave-steps (positions_per_wave_step positions each).  0 = not staged.
+// LDS) and mode 2 (registers one chunk ahead, then LDS) use chunks of about
+// 4352 bytes of K (and as much of V); mode 2 at most kStageLoads pieces per
+// lane and tensor.  A chunk is a whole number of wave-steps
+// (positions_per_wave_step positions each).  0 = not staged.
 constexpr int kStageLoads = 5;
 __host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
                                                  int32_t positions_per_wave_step, int32_t mode) {
   if (row_bytes == 0 || (row_bytes & 15u) || positions_per_wave_step < 1) return 0;
   if (mode != 1 && mode != 2) return 0;
-  const uint32_t target = mode == 1 ? 8704u : 4352u;
+  const uint32_t target = 4352u;
   const uint32_t per_step = row_bytes * (uint32_t)positions_per_wave_step;
   const uint32_t steps = per_step >= target ? 1u : target / per_step;
   if (mode == 2 && steps * per_step > 1024u * (uint32_t)kStageLoads) return 0;
@@ -92,11 +92,56 @@ struct DecodeParams {
   float *att;          // nullable: [L][n_seq][n_heads][att_stride]
   int32_t att_stride;
   float qscale;        // (1/sqrtf(hd)) * log2(e)
-  int32_t tune_unroll; // 0 = default, else wave-steps per loop trip (2 or 4)
   int32_t tune_chunk;  // 0 = default, else elements per lane for Q8 (16 or 32)
   int32_t stage_mode;  // k_layer: 0 direct loads, 1 / 2 staged (stage_rows_of)
   int32_t stage_rows;  // rows per staged chunk (0 with stage_mode 0)
+  // Work-queue mode of k_layer (wq != nullptr; stage_mode 2 only): units are
+  // (seq, layer) pairs, u = li*n_seq + seq.  wq holds two counter sets of
+  // wq_cap units x kWqStride int32 each: [0] = pieces claimed, [1] = partial
+  // slots reserved.  The launch uses set wq_set; k_combine reads it and
+  // zeroes units [0, wq_zero_units) of the other set.
+  int32_t *wq;
+  int32_t wq_set, wq_cap, wq_zero_units;
+  int32_t wq_grid;      // workgroups of the launch
+  int32_t piece_len;    // positions per small claimed piece (a multiple of stage_rows)
+  int32_t piece_big;    // positions per big piece (a multiple of piece_len)
+  int32_t n_layers_call;
 };
+constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte line each
+constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit
+constexpr int kWqMinParts = 16;  // partial slots per unit at least
+constexpr int kWqClaimsPerWave = 64;   // automatic small piece: about this many per wave
+constexpr int kWqMaxWavesPerUnit = 64; // more waves per unit than this: static splits instead
+constexpr int kWqBigFactor = 8;        // big piece = this many small pieces
+constexpr int kWqTailDiv = 8;          // the last 1/kWqTailDiv of a unit goes in small pieces
+
+// Work-queue pieces of a unit that streams positions [0, n) (guided
+// self-scheduling in two sizes): whole big pieces up to n - n/kWqTailDiv,
+// then small pieces to the end.  Piece c < nbig covers [c*big, (c+1)*big),
+// piece nbig + j covers [small0 + j*small, min(small0 + (j+1)*small, n)).
+struct PieceMap {
+  int32_t big, small, nbig, small0, npieces;
+};
+__host__ __device__ inline PieceMap piece_map(int32_t n, int32_t big, int32_t small) {
+  PieceMap m;
+  m.big = big;
+  m.small = small;
+  const int32_t head = n - n / kWqTailDiv;
+  m.nbig = head > 0 ? head / big : 0;
+  m.small0 = m.nbig * big;
+  m.npieces = m.nbig + (n - m.small0 + small - 1) / small;
+  return m;
+}
+__host__ __device__ inline void piece_range(const PieceMap &m, int32_t c, int32_t n, int32_t &lo,
+                                            int32_t &hi) {
+  if (c < m.nbig) {
+    lo = c * m.big;
+    hi = lo + m.big;
+  } else {
+    lo = m.small0 + (c - m.nbig) * m.small;
+    hi = lo + m.small < n ? lo + m.small : n;
+  }
+}
 
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_append_batch(const AppendParams &p, int n_layers, hipStream_t s);
@@ -109,8 +154,11 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 // Whether a specialised decode kernel exists for this shape.
 bool decode_fast_available(const ShapeDev &sh);
-// Resident 256-thread decode workgroups per CU for this shape (occupancy).
-int decode_blocks_per_cu(const ShapeDev &sh);
+// Resident 256-thread decode workgroups per CU for this shape and the
+// k_layer variant DecodeParams' tune_chunk / stage_mode / stage_rows / wq
+// select (occupancy).
+int decode_blocks_per_cu(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
+                         int32_t stage_rows, bool wq);
 // DecodeParams.stage_rows for this shape and staging mode (tune_chunk as in
 // DecodeParams): 0 when k_layer must load straight from HBM (no specialised
 // kernel, or rows that are not whole 16-byte pieces).
@@ -119,11 +167,12 @@ int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode);
 constexpr int32_t kDefaultStageMode = 2;
 // k_layer for one (KV format 0 = F32 / 1 = Q8_0, head_dim, GQA group),
 // defined in g2b_layer.h and instantiated by g2b_layer_inst.hip: the launch,
-// and its resident workgroups per CU for a given stage_rows.
+// and the resident workgroups per CU of the variant a launch would use.
 template <int FMT, int HD, int G>
 hipError_t launch_layer(const DecodeParams &p, int n_layers, hipStream_t s);
 template <int FMT, int HD, int G>
-int layer_occupancy(const ShapeDev &sh, int32_t stage_rows);
+int layer_occupancy(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
+                    int32_t stage_rows, bool wq);
 
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {

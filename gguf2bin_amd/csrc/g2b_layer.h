@@ -313,33 +313,45 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
   }
 }
 
-// Specialised shapes: workgroup (split, seq, layer) rotates its q into LDS,
-// appends the new row if its split holds pos (and reads that row back from
-// LDS, not HBM), streams its positions and writes one partial per wave and
-// head; k_combine merges the partials and writes the output over q
-// (l5_model.c:513-578).  A merge inside this kernel (last workgroup of a
-// (seq, layer) by an atomic counter) measured slower: its agent-scope fences
-// and the merge at the tail of every launch cost more than one more launch.
+// Specialised shapes.  A workgroup "visit" handles one unit (sequence,
+// layer) over a set of positions: it [QK-RMSNorms and] rotates the unit's q
+// into LDS, appends the new row if it owns pos (and reads that row back from
+// LDS, not HBM), streams its positions, merges its four waves' softmax
+// states and writes one partial per head into its partial slot; k_combine
+// merges the partials and writes the output over q (l5_model.c:513-578).
+//
+// Static mode (WQ = false): workgroup (split, seq, layer) visits positions
+// [split*split_len, min(pos+1, (split+1)*split_len)) of its unit once, and
+// the split that holds pos appends.  Work-queue mode (WQ = true, STG = 2): a
+// grid of resident workgroups, each starting at home unit blockIdx.x %
+// n_units; positions [0, pos) of a unit are cut into pieces of
+// P.piece_len positions that the waves of every workgroup visiting the unit
+// claim one by one from the unit's counter (relaxed device-scope atomics,
+// one claim ahead), so workgroups on busier parts of the memory system take
+// fewer pieces.  A workgroup whose unit has no pieces left moves to another
+// unit with pieces left.  Each visit first reserves a partial slot from the
+// unit's slot counter; the visit that gets slot 0 appends and consumes pos.
+// At most P.max_splits visits per unit are admitted, and both counters only
+// grow, so every workgroup finishes.  k_combine reads the slot count and
+// zeroes the counter set of the next launch.
+// A merge of the partials inside this kernel (last workgroup of a unit by
+// an atomic counter) measured slower than the separate k_combine launch:
+// its agent-scope fences cost more than one more launch.
 // FMT: 0 = F32 KV, 1 = Q8_0 KV.  HD: head_dim.  CD: elements per lane.
-// G: q heads per KV head.  U: wave-steps consumed per loop trip.
+// G: q heads per KV head.  U: wave-steps per loop trip of the per-lane (STG = 0) path.
 // ATT: also write the raw scores for the reference-layout softmax weights.
 // STG: how KV rows reach the lanes.  0: per-lane loads straight from HBM.
 // 1: chunks of P.stage_rows rows pulled into the wave's LDS region by
 // global_load_lds, then read from there.  2: the same chunks loaded into
 // registers with coalesced non-temporal loads one chunk ahead (in flight
 // while the current chunk is consumed) and written to LDS.
-template <int FMT, int HD, int CD, int G, int U, bool ATT, int STG>
+template <int FMT, int HD, int CD, int G, int U, bool ATT, int STG, bool WQ>
 __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
+  static_assert(!WQ || STG != 0, "the work queue streams through LDS");
   extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ int32_t s_bcast;
   constexpr int LPH = HD / CD;  // lanes per head
   using C = Codec<FMT, CD>;
-  const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
-  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
-  const int npos = sd.pos + 1;
-  const int t0 = split * P.split_len;
-  if (t0 >= npos) return;  // a shorter sequence of a ragged batch: no split here
-  const int t1 = min(npos, t0 + P.split_len);
-  const bool owns_new = t1 == npos;  // this split holds position pos
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -350,13 +362,13 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   const int slot_ld = lane_on ? slot : 0;  // idle lanes shadow slot 0's rows
   const int r = lane_on ? lane - slot * LPP : 0;
   const int g = r / LPH, c = r - g * LPH;
-  const int layer = P.layer0 + li;
   const int n_heads = P.sh.n_heads;
   const int nkv = P.sh.n_kv_heads * HD;
   const size_t nq = (size_t)n_heads * HD;
-  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
   const size_t row = P.sh.row_bytes;
-  const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+  const LaneOff lo = C::offsets(g * HD + c * CD);
+  const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
+  const size_t ustep = (size_t)stride * row;  // bytes between them
 
   // LDS: rotated q (nq floats) and rotated new k (nkv floats) at 0 - with
   // STG, the waves' staging regions overlap them once q is in registers -
@@ -367,366 +379,485 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   uint8_t *rowk = lds + ll.rows;
   uint8_t *rowv = rowk + ll.row_pad;
   float *inv = reinterpret_cast<float *>(rowv + ll.row_pad);
-  {
-    // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by pair
-    // as the append does (l3_math.c:74-101)
-    const float *qi = P.q_in + sidx * nq;
-    if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
-      for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
-      __syncthreads();
-      qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, inv);
-      qi = qrot;  // rotate in place: each pair is read and written by one thread
-    }
-    constexpr int half = HD / 2;
-    for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
-      const int h = pr / half, j = pr - h * half;
-      int ia, ib;
-      rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
-      float a = qi[h * HD + ia], b = qi[h * HD + ib];
-      if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
-      qrot[h * HD + ia] = a;
-      qrot[h * HD + ib] = b;
-    }
-  }
-  if (owns_new)  // (its barriers also publish qrot)
-    append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
-                   P.norm, kr, rowk, rowv, inv);
-  else
-    __syncthreads();
 
-  float q[G][CD];
-#pragma unroll
-  for (int i = 0; i < G; i++)
-#pragma unroll
-    for (int j = 0; j < CD; j += 4) {
-      const float4 v4 =
-          *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
-      q[i][j + 0] = v4.x * P.qscale;
-      q[i][j + 1] = v4.y * P.qscale;
-      q[i][j + 2] = v4.z * P.qscale;
-      q[i][j + 3] = v4.w * P.qscale;
-    }
-  [[maybe_unused]] QDigits<CD> qd[G];
-  if constexpr (FMT == 1) {
-#pragma unroll
-    for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
-  }
-  if constexpr (STG != 0) __syncthreads();  // every wave has its q: staging may overwrite qrot
-  const LaneOff lo = C::offsets(g * HD + c * CD);
-  const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
-  const size_t ustep = (size_t)stride * row;  // bytes between them
-  const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
-  const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
-
-  float m[G], l[G], acc[G][CD];
-#pragma unroll
-  for (int i = 0; i < G; i++) {
-    m[i] = kNegBig;
-    l[i] = 0.f;
-#pragma unroll
-    for (int j = 0; j < CD; j++) acc[i][j] = 0.f;
-  }
-  [[maybe_unused]] float *att_h = nullptr;
-  if constexpr (ATT)
-    att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
-
-  // Scores, online softmax and V for UU positions already loaded.
-  auto consume = [&](const typename C::Raw *kr_, const typename C::Raw *vr_, const bool *valid,
-                     const int *tpos, auto nu, auto check) {
-    constexpr int UU = decltype(nu)::value;
-    constexpr bool CHECK = decltype(check)::value;
-    float sc[UU][G];
-#pragma unroll
-    for (int u = 0; u < UU; u++) {
-      if constexpr (FMT == 1) {
-        uint32_t w[CD / 4];
-        float ks;
-        C::quants(kr_[u], w, ks, lo);
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-          const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
-          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
-        }
-      } else {
-        float kf[CD];
-        C::values(kr_[u], kf);
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-          float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-          for (int j = 0; j < CD; j += 2) {
-            s0 = fmaf(q[i][j], kf[j], s0);
-            s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
-          }
-          const float s = group_sum<LPH>(s0 + s1);
-          sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
-        }
+  // One visit of unit (seq, li): positions [t0, tend) from HBM (static
+  // mode) or the unit's claimed pieces (work queue), plus pos itself when
+  // owns_new; the merged state goes to partial slot `pslot`.
+  // (sd must be wave-uniform - loaded with a uniform index - or every KV
+  // address derived from it lives in VGPRs.)
+  auto visit = [&](const SeqDev &sd, int seq, int li, int t0, int tend, bool owns_new,
+                   int pslot, int32_t *ctr) {
+    const int layer = P.layer0 + li;
+    const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+    const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+    {
+      // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by
+      // pair as the append does (l3_math.c:74-101)
+      const float *qi = P.q_in + sidx * nq;
+      if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
+        for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
+        __syncthreads();
+        qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, inv);
+        qi = qrot;  // rotate in place: each pair is read and written by one thread
+      }
+      constexpr int half = HD / 2;
+      for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
+        const int h = pr / half, j = pr - h * half;
+        int ia, ib;
+        rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
+        float a = qi[h * HD + ia], b = qi[h * HD + ib];
+        if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+        qrot[h * HD + ia] = a;
+        qrot[h * HD + ib] = b;
       }
     }
-    bool need = false;
-    float mn[G];
+    if (owns_new)  // (its barriers also publish qrot)
+      append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
+                     P.norm, kr, rowk, rowv, inv);
+    else
+      __syncthreads();
+
+    float q[G][CD];
+#pragma unroll
+    for (int i = 0; i < G; i++)
+#pragma unroll
+      for (int j = 0; j < CD; j += 4) {
+        const float4 v4 =
+            *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
+        q[i][j + 0] = v4.x * P.qscale;
+        q[i][j + 1] = v4.y * P.qscale;
+        q[i][j + 2] = v4.z * P.qscale;
+        q[i][j + 3] = v4.w * P.qscale;
+      }
+    [[maybe_unused]] QDigits<CD> qd[G];
+    if constexpr (FMT == 1) {
+#pragma unroll
+      for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
+    }
+    if constexpr (STG != 0) __syncthreads();  // every wave has its q: staging may overwrite qrot
+    const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+    const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+
+    float m[G], l[G], acc[G][CD];
 #pragma unroll
     for (int i = 0; i < G; i++) {
-      float mx = m[i];
+      m[i] = kNegBig;
+      l[i] = 0.f;
 #pragma unroll
-      for (int u = 0; u < UU; u++) mx = fmaxf(mx, sc[u][i]);
-      mn[i] = mx;
-      need |= mx > m[i];
+      for (int j = 0; j < CD; j++) acc[i][j] = 0.f;
     }
-    if (__any(need)) {
-#pragma unroll
-      for (int i = 0; i < G; i++) {
-        const float a = fast_exp2(m[i] - mn[i]);
-        l[i] *= a;
-#pragma unroll
-        for (int j = 0; j < CD; j++) acc[i][j] *= a;
-        m[i] = mn[i];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < UU; u++) {
-      float p[G];
-#pragma unroll
-      for (int i = 0; i < G; i++) {
-        p[i] = fast_exp2(sc[u][i] - m[i]);
-        l[i] += p[i];
-      }
-      if constexpr (FMT == 1) {
-        uint32_t w[CD / 4];
-        float vs;
-        C::quants(vr_[u], w, vs, lo);
-        float pv[G];
-#pragma unroll
-        for (int i = 0; i < G; i++) pv[i] = p[i] * vs;
-#pragma unroll
-        for (int j = 0; j < CD / 4; j++)
-#pragma unroll
-          for (int b = 0; b < 4; b++) {
-            const float x = i8f(w[j], b);
-#pragma unroll
-            for (int i = 0; i < G; i++) acc[i][4 * j + b] = fmaf(pv[i], x, acc[i][4 * j + b]);
-          }
-      } else {
-        float vf[CD];
-        C::values(vr_[u], vf);
-#pragma unroll
-        for (int j = 0; j < CD; j++)
-#pragma unroll
-          for (int i = 0; i < G; i++) acc[i][j] = fmaf(p[i], vf[j], acc[i][j]);
-      }
-      if constexpr (ATT) {
-        if (c == 0 && valid[u]) {
-#pragma unroll
-          for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tpos[u]] = sc[u][i];
-        }
-      }
-    }
-  };
+    [[maybe_unused]] float *att_h = nullptr;
+    if constexpr (ATT)
+      att_h = P.att + (sidx * (size_t)n_heads + (size_t)g * G) * (size_t)P.att_stride;
 
-  // Positions [t0, tend) stream from HBM; pos itself, when owned, from LDS.
-  const int tend = owns_new ? t1 - 1 : t1;
-  auto trip = [&](int tb, auto check) {
-    constexpr bool CHECK = decltype(check)::value;
-    typename C::Raw krr[U], vrr[U];
-    bool valid[U];
-    int tpos[U];
-    const size_t base = (size_t)(tb + slot_ld) * row;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      size_t off = base + (size_t)u * ustep;
-      tpos[u] = tb + u * stride + slot;
-      if constexpr (CHECK) {
-        valid[u] = lane_on && tpos[u] < tend;
-        if (!valid[u]) off = (size_t)t0 * row;
-      } else {
-        valid[u] = lane_on;
-      }
-      C::load(krr[u], kb + off, lo);
-      C::load(vrr[u], vb + off, lo);
-    }
-    consume(krr, vrr, valid, tpos, std::integral_constant<int, U>{}, check);
-  };
-  if constexpr (STG != 0) {
-    // Wave w takes chunks of R contiguous positions: [t0 + (w + 4i) R, +R).
-    // A chunk's K and V bytes are contiguous (rows of a layer are), so they
-    // move as 16-byte pieces, lane l taking pieces l, l + 64, ..., into the
-    // wave's LDS region (each HBM byte fetched once, by one lane,
-    // non-temporal); then every lane reads its blocks from there.
-    const int R = P.stage_rows;
-    const uint32_t cbytes = (uint32_t)R * (uint32_t)row;
-    uint8_t *sk = lds + (size_t)wave * 2 * cbytes, *sv = sk + cbytes;
-    const int steps = R / PPW;
-    // U wave-steps of the chunk from LDS; rows past nrows (and idle lanes)
-    // read row 0 of the chunk and are masked out of the softmax.
-    auto lds_trip = [&](int cs, int s, int nrows, auto nu, auto check) {
+    // Scores, online softmax and V for UU positions already loaded.
+    auto consume = [&](const typename C::Raw *kr_, const typename C::Raw *vr_,
+                       const bool *valid, const int *tpos, auto nu, auto check) {
       constexpr int UU = decltype(nu)::value;
       constexpr bool CHECK = decltype(check)::value;
-      typename C::Raw krr[UU], vrr[UU];
-      bool valid[UU];
-      int tpos[UU];
+      float sc[UU][G];
 #pragma unroll
       for (int u = 0; u < UU; u++) {
-        const int r = (s + u) * PPW + slot;
-        valid[u] = CHECK ? (lane_on && r < nrows) : lane_on;
-        const size_t ro = valid[u] ? (size_t)r * row : 0;
-        tpos[u] = cs + r;
-        C::load_lds(krr[u], sk + ro, lo);
-        C::load_lds(vrr[u], sv + ro, lo);
-      }
-      consume(krr, vrr, valid, tpos, nu, check);
-    };
-    // Every lane's blocks of a chunk of nrows rows, read from LDS.
-    auto consume_chunk = [&](int cs, int nrows) {
-      if (nrows == R) {
-        int s = 0;
-        for (; s + U <= steps; s += U)
-          lds_trip(cs, s, nrows, std::integral_constant<int, U>{}, std::false_type{});
-        for (; s < steps; s++)
-          lds_trip(cs, s, nrows, std::integral_constant<int, 1>{}, std::false_type{});
-      } else {
-        for (int s = 0; s * PPW < nrows; s += U)
-          lds_trip(cs, s, nrows, std::integral_constant<int, U>{}, std::true_type{});
-      }
-    };
-    const int cstride = kWavesPerSplit * R;  // positions between a wave's chunks
-    if constexpr (STG == 1) {
-      for (int cs = t0 + wave * R; cs < tend; cs += cstride) {
-        const int nrows = min(R, tend - cs);
-        const uint32_t np = (uint32_t)nrows * (uint32_t)row / 16u;  // 16-byte pieces
-        const uint8_t *gk = kb + (size_t)cs * row + 16u * (uint32_t)lane;
-        const uint8_t *gv = vb + (size_t)cs * row + 16u * (uint32_t)lane;
-        for (uint32_t i = 0; 64u * i < np; i++) {
-          if (64u * i + (uint32_t)lane < np) {
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(gk + 1024u * i),
-                (__attribute__((address_space(3))) void *)(sk + 1024u * i), 16, 0, kAuxNT);
-            __builtin_amdgcn_global_load_lds(
-                (const __attribute__((address_space(1))) void *)(gv + 1024u * i),
-                (__attribute__((address_space(3))) void *)(sv + 1024u * i), 16, 0, kAuxNT);
+        if constexpr (FMT == 1) {
+          uint32_t w[CD / 4];
+          float ks;
+          C::quants(kr_[u], w, ks, lo);
+#pragma unroll
+          for (int i = 0; i < G; i++) {
+            const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
+            sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
+          }
+        } else {
+          float kf[CD];
+          C::values(kr_[u], kf);
+#pragma unroll
+          for (int i = 0; i < G; i++) {
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int j = 0; j < CD; j += 2) {
+              s0 = fmaf(q[i][j], kf[j], s0);
+              s1 = fmaf(q[i][j + 1], kf[j + 1], s1);
+            }
+            const float s = group_sum<LPH>(s0 + s1);
+            sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
           }
         }
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the chunk is in LDS
-        consume_chunk(cs, nrows);
-        // The next chunk's loads overwrite this region only after every value
-        // read from it above has been used (data dependence orders them).
+      }
+      bool need = false;
+      float mn[G];
+#pragma unroll
+      for (int i = 0; i < G; i++) {
+        float mx = m[i];
+#pragma unroll
+        for (int u = 0; u < UU; u++) mx = fmaxf(mx, sc[u][i]);
+        mn[i] = mx;
+        need |= mx > m[i];
+      }
+      if (__any(need)) {
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          const float a = fast_exp2(m[i] - mn[i]);
+          l[i] *= a;
+#pragma unroll
+          for (int j = 0; j < CD; j++) acc[i][j] *= a;
+          m[i] = mn[i];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UU; u++) {
+        float p[G];
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          p[i] = fast_exp2(sc[u][i] - m[i]);
+          l[i] += p[i];
+        }
+        if constexpr (FMT == 1) {
+          uint32_t w[CD / 4];
+          float vs;
+          C::quants(vr_[u], w, vs, lo);
+          float pv[G];
+#pragma unroll
+          for (int i = 0; i < G; i++) pv[i] = p[i] * vs;
+#pragma unroll
+          for (int j = 0; j < CD / 4; j++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+              const float x = i8f(w[j], b);
+#pragma unroll
+              for (int i = 0; i < G; i++) acc[i][4 * j + b] = fmaf(pv[i], x, acc[i][4 * j + b]);
+            }
+        } else {
+          float vf[CD];
+          C::values(vr_[u], vf);
+#pragma unroll
+          for (int j = 0; j < CD; j++)
+#pragma unroll
+            for (int i = 0; i < G; i++) acc[i][j] = fmaf(p[i], vf[j], acc[i][j]);
+        }
+        if constexpr (ATT) {
+          if (c == 0 && valid[u]) {
+#pragma unroll
+            for (int i = 0; i < G; i++) att_h[(size_t)i * P.att_stride + tpos[u]] = sc[u][i];
+          }
+        }
+      }
+    };
+
+    if constexpr (STG != 0) {
+      // Chunks of R contiguous positions.  A chunk's K and V bytes are
+      // contiguous (rows of a layer are), so they move as 16-byte pieces,
+      // lane l taking pieces l, l + 64, ..., into the wave's LDS region (each
+      // HBM byte fetched once, by one lane, non-temporal); then every lane
+      // reads its blocks from there.
+      const int R = P.stage_rows;
+      const uint32_t cbytes = (uint32_t)R * (uint32_t)row;
+      uint8_t *sk = lds + (size_t)wave * 2 * cbytes, *sv = sk + cbytes;
+      const int steps = R / PPW;
+      // U wave-steps of the chunk from LDS; rows past nrows (and idle lanes)
+      // read row 0 of the chunk and are masked out of the softmax.
+      auto lds_trip = [&](int cs0, int s, int nrows, auto nu, auto check) {
+        constexpr int UU = decltype(nu)::value;
+        constexpr bool CHECK = decltype(check)::value;
+        typename C::Raw krr[UU], vrr[UU];
+        bool valid[UU];
+        int tpos[UU];
+#pragma unroll
+        for (int u = 0; u < UU; u++) {
+          const int rr = (s + u) * PPW + slot;
+          valid[u] = CHECK ? (lane_on && rr < nrows) : lane_on;
+          const size_t ro = valid[u] ? (size_t)rr * row : 0;
+          tpos[u] = cs0 + rr;
+          C::load_lds(krr[u], sk + ro, lo);
+          C::load_lds(vrr[u], sv + ro, lo);
+        }
+        consume(krr, vrr, valid, tpos, nu, check);
+      };
+      // Every lane's blocks of a chunk of nrows rows, read from LDS.
+      auto consume_chunk = [&](int cs0, int nrows) {
+        if (nrows == R) {
+          for (int s = 0; s < steps; s++)
+            lds_trip(cs0, s, nrows, std::integral_constant<int, 1>{}, std::false_type{});
+        } else {
+          for (int s = 0; s * PPW < nrows; s++)
+            lds_trip(cs0, s, nrows, std::integral_constant<int, 1>{}, std::true_type{});
+        }
+      };
+      const int cstride = kWavesPerSplit * R;  // positions between a wave's chunks (static)
+      // Work queue: pieces of [0, tend) (piece_map: big ones, then small
+      // ones for the last part; multiples of R) claimed from ctr[0], two
+      // claims in flight while a piece is streamed.  Chunks never cross a
+      // piece boundary.
+      [[maybe_unused]] const PieceMap pm = piece_map(WQ ? tend : 0, P.piece_big, P.piece_len);
+      [[maybe_unused]] const int npieces = WQ ? pm.npieces : 0;
+      // A claim returns lane 0's fetched value in a VGPR without waiting for
+      // it; the value is read (readfirstlane, which waits) only at the next
+      // piece switch, so the atomic's latency overlaps a whole piece.
+      [[maybe_unused]] auto claim_async = [&]() {
+        int32_t v = 0;
+        if (lane == 0)
+          v = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return v;
+      };
+      if constexpr (STG == 1) {
+        auto dma_chunk = [&](int cs0, int nrows) {
+          const uint32_t np = (uint32_t)nrows * (uint32_t)row / 16u;  // 16-byte pieces
+          const uint8_t *gk = kb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+          const uint8_t *gv = vb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+          for (uint32_t i = 0; 64u * i < np; i++) {
+            if (64u * i + (uint32_t)lane < np) {
+              __builtin_amdgcn_global_load_lds(
+                  (const __attribute__((address_space(1))) void *)(gk + 1024u * i),
+                  (__attribute__((address_space(3))) void *)(sk + 1024u * i), 16, 0, kAuxNT);
+              __builtin_amdgcn_global_load_lds(
+                  (const __attribute__((address_space(1))) void *)(gv + 1024u * i),
+                  (__attribute__((address_space(3))) void *)(sv + 1024u * i), 16, 0, kAuxNT);
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the chunk is in LDS
+          consume_chunk(cs0, nrows);
+          // The next chunk's loads overwrite this region only after every
+          // value read from it above has been used (data dependence orders them).
+        };
+        if constexpr (!WQ) {
+          for (int cs0 = t0 + wave * R; cs0 < tend; cs0 += cstride)
+            dma_chunk(cs0, min(R, tend - cs0));
+        } else {
+          int pc = __builtin_amdgcn_readfirstlane(claim_async());
+          int32_t pn1 = claim_async(), pn2 = claim_async();
+          while (pc < npieces) {
+            int ps, pe;
+            piece_range(pm, pc, tend, ps, pe);
+            for (int cs0 = ps; cs0 < pe; cs0 += R) dma_chunk(cs0, min(R, pe - cs0));
+            pc = __builtin_amdgcn_readfirstlane(pn1);
+            pn1 = pn2;
+            if (pc < npieces) pn2 = claim_async();
+          }
+        }
+      } else {
+        // Registers hold the next chunk (kStageLoads 16-byte pieces per lane
+        // and tensor at most) while the current one is consumed.
+        u32x4 rk[kStageLoads], rv[kStageLoads];
+        auto issue = [&](int cs0) {
+          const uint32_t np = (uint32_t)min(R, tend - cs0) * (uint32_t)row / 16u;
+          const uint8_t *gk = kb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+          const uint8_t *gv = vb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+#pragma unroll
+          for (int i = 0; i < kStageLoads; i++) {
+            if (64u * (uint32_t)i + (uint32_t)lane < np) {
+              rk[i] = __builtin_nontemporal_load(
+                  (const __attribute__((address_space(1))) u32x4 *)(gk + 1024u * i));
+              rv[i] = __builtin_nontemporal_load(
+                  (const __attribute__((address_space(1))) u32x4 *)(gv + 1024u * i));
+            }
+          }
+        };
+        auto stash = [&](int cs0) {
+          const uint32_t np = (uint32_t)min(R, tend - cs0) * (uint32_t)row / 16u;
+#pragma unroll
+          for (int i = 0; i < kStageLoads; i++) {
+            const uint32_t pc = 64u * (uint32_t)i + (uint32_t)lane;
+            if (pc < np) {
+              *reinterpret_cast<u32x4 *>(sk + 16u * pc) = rk[i];
+              *reinterpret_cast<u32x4 *>(sv + 16u * pc) = rv[i];
+            }
+          }
+        };
+        if constexpr (!WQ) {
+          int cs0 = t0 + wave * R;
+          if (cs0 < tend) issue(cs0);
+          for (; cs0 < tend; cs0 += cstride) {
+            // (the previous chunk's LDS reads were all used before this point)
+            stash(cs0);
+            if (cs0 + cstride < tend) issue(cs0 + cstride);
+            consume_chunk(cs0, min(R, tend - cs0));
+          }
+        } else {
+          int pc = __builtin_amdgcn_readfirstlane(claim_async());
+          int32_t pn1 = claim_async(), pn2 = claim_async();
+          int cs0 = 0, ce = 0;
+          if (pc < npieces) {
+            piece_range(pm, pc, tend, cs0, ce);
+            issue(cs0);
+          }
+          while (pc < npieces) {
+            stash(cs0);
+            int ns = cs0 + R, nce = ce, nc = pc;
+            if (ns >= ce) {  // next piece
+              nc = __builtin_amdgcn_readfirstlane(pn1);
+              pn1 = pn2;
+              if (nc < npieces) {
+                piece_range(pm, nc, tend, ns, nce);
+                pn2 = claim_async();
+              }
+            }
+            if (nc < npieces) issue(ns);
+            consume_chunk(cs0, min(R, ce - cs0));
+            pc = nc;
+            cs0 = ns;
+            ce = nce;
+          }
+        }
       }
     } else {
-      // Registers hold the next chunk (kStageLoads 16-byte pieces per lane
-      // and tensor at most) while the current one is consumed.
-      u32x4 rk[kStageLoads], rv[kStageLoads];
-      auto issue = [&](int cs) {
-        const uint32_t np = (uint32_t)min(R, tend - cs) * (uint32_t)row / 16u;
-        const uint8_t *gk = kb + (size_t)cs * row + 16u * (uint32_t)lane;
-        const uint8_t *gv = vb + (size_t)cs * row + 16u * (uint32_t)lane;
+      // Per-lane loads: positions tb = t0 + wave*PPW + k*stride + slot.
+      auto trip = [&](int tb, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
+        typename C::Raw krr[U], vrr[U];
+        bool valid[U];
+        int tpos[U];
+        const size_t base = (size_t)(tb + slot_ld) * row;
 #pragma unroll
-        for (int i = 0; i < kStageLoads; i++) {
-          if (64u * (uint32_t)i + (uint32_t)lane < np) {
-            rk[i] = __builtin_nontemporal_load(
-                (const __attribute__((address_space(1))) u32x4 *)(gk + 1024u * i));
-            rv[i] = __builtin_nontemporal_load(
-                (const __attribute__((address_space(1))) u32x4 *)(gv + 1024u * i));
+        for (int u = 0; u < U; u++) {
+          size_t off = base + (size_t)u * ustep;
+          tpos[u] = tb + u * stride + slot;
+          if constexpr (CHECK) {
+            valid[u] = lane_on && tpos[u] < tend;
+            if (!valid[u]) off = (size_t)t0 * row;
+          } else {
+            valid[u] = lane_on;
           }
+          C::load(krr[u], kb + off, lo);
+          C::load(vrr[u], vb + off, lo);
         }
+        consume(krr, vrr, valid, tpos, std::integral_constant<int, U>{}, check);
       };
-      auto stash = [&](int cs) {
-        const uint32_t np = (uint32_t)min(R, tend - cs) * (uint32_t)row / 16u;
-#pragma unroll
-        for (int i = 0; i < kStageLoads; i++) {
-          const uint32_t pc = 64u * (uint32_t)i + (uint32_t)lane;
-          if (pc < np) {
-            *reinterpret_cast<u32x4 *>(sk + 16u * pc) = rk[i];
-            *reinterpret_cast<u32x4 *>(sv + 16u * pc) = rv[i];
-          }
-        }
-      };
-      int cs = t0 + wave * R;
-      if (cs < tend) issue(cs);
-      for (; cs < tend; cs += cstride) {
-        // (the previous chunk's LDS reads were all used before this point)
-        stash(cs);
-        if (cs + cstride < tend) issue(cs + cstride);
-        consume_chunk(cs, min(R, tend - cs));
+      const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
+      int tb = t0 + wave * PPW;
+      if (tend > t0) {  // (a split of one position may hold only pos)
+        for (; tb + trip_span <= tend; tb += stride * U) trip(tb, std::false_type{});
+        for (; tb < tend; tb += stride * U) trip(tb, std::true_type{});
       }
     }
-  } else {
-    const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
-    int tb = t0 + wave * PPW;
-    if (tend > t0) {  // (a split of one position may hold only pos)
-      for (; tb + trip_span <= tend; tb += stride * U) trip(tb, std::false_type{});
-      for (; tb < tend; tb += stride * U) trip(tb, std::true_type{});
+    if (owns_new) {
+      typename C::Raw krr[1], vrr[1];
+      C::load_lds(krr[0], rowk, lo);
+      C::load_lds(vrr[0], rowv, lo);
+      const bool valid[1] = {wave == 0 && slot == 0};
+      const int tpos[1] = {sd.pos};
+      consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
     }
-  }
-  if (owns_new) {
-    typename C::Raw krr[1], vrr[1];
-    C::load_lds(krr[0], rowk, lo);
-    C::load_lds(vrr[0], rowv, lo);
-    const bool valid[1] = {wave == 0 && slot == 0};
-    const int tpos[1] = {sd.pos};
-    consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
-  }
 
-  // Fold the PPW position slots of the wave into slot 0.  Every lane takes
-  // part in the shuffles, but only slot-0 lanes update their state, so the
-  // state read from slot k is always slot k's own.
-  const bool gather = slot == 0;
-  for (int k = 1; k < PPW; k++) {
-    const int src = (lane + k * LPP) & 63;
+    // Fold the PPW position slots of the wave into slot 0.  Every lane takes
+    // part in the shuffles, but only slot-0 lanes update their state, so the
+    // state read from slot k is always slot k's own.
+    const bool gather = slot == 0;
+    for (int k = 1; k < PPW; k++) {
+      const int src = (lane + k * LPP) & 63;
 #pragma unroll
-    for (int i = 0; i < G; i++) {
-      const float m2 = __shfl(m[i], src);
-      const float l2 = __shfl(l[i], src);
-      const float M = fmaxf(m[i], m2);
-      const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
-      l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
+      for (int i = 0; i < G; i++) {
+        const float m2 = __shfl(m[i], src);
+        const float l2 = __shfl(l[i], src);
+        const float M = fmaxf(m[i], m2);
+        const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
+        l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
 #pragma unroll
-      for (int j = 0; j < CD; j++) {
-        const float a2 = __shfl(acc[i][j], src);
-        acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
+        for (int j = 0; j < CD; j++) {
+          const float a2 = __shfl(acc[i][j], src);
+          acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
+        }
+        m[i] = gather ? M : m[i];
       }
-      m[i] = gather ? M : m[i];
     }
-  }
-  // Merge the four waves' states in LDS (the rows and q there are no longer
-  // read once every wave is past this barrier) and write one partial per
-  // head for the split.  LDS: [wave][head][kPartHead + HD] floats.
-  constexpr int pstr = kPartHead + HD;
-  __syncthreads();
-  float *ws = reinterpret_cast<float *>(lds);
-  if (slot == 0) {
+    // Merge the four waves' states in LDS (the rows and q there are no
+    // longer read once every wave is past this barrier) and write one
+    // partial per head.  LDS: [wave][head][kPartHead + HD] floats.
+    constexpr int pstr = kPartHead + HD;
+    __syncthreads();
+    float *ws = reinterpret_cast<float *>(lds);
+    if (slot == 0) {
 #pragma unroll
-    for (int i = 0; i < G; i++) {
-      float *pw = ws + ((size_t)wave * n_heads + (size_t)(g * G + i)) * pstr;
-      if (c == 0) {
-        pw[0] = m[i];
-        pw[1] = l[i];
+      for (int i = 0; i < G; i++) {
+        float *pw = ws + ((size_t)wave * n_heads + (size_t)(g * G + i)) * pstr;
+        if (c == 0) {
+          pw[0] = m[i];
+          pw[1] = l[i];
+        }
+#pragma unroll
+        for (int j = 0; j < CD; j += 4)
+          *reinterpret_cast<float4 *>(pw + kPartHead + c * CD + j) =
+              make_float4(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3]);
       }
-#pragma unroll
-      for (int j = 0; j < CD; j += 4)
-        *reinterpret_cast<float4 *>(pw + kPartHead + c * CD + j) =
-            make_float4(acc[i][j], acc[i][j + 1], acc[i][j + 2], acc[i][j + 3]);
     }
-  }
-  __syncthreads();
-  const size_t wstr = (size_t)n_heads * pstr;
-  for (int e = threadIdx.x; e < n_heads * HD; e += blockDim.x) {
-    const int h = e / HD, d = e - h * HD;
-    const float *pw = ws + (size_t)h * pstr;
-    float M = pw[0];
+    __syncthreads();
+    const size_t wstr = (size_t)n_heads * pstr;
+    for (int e = threadIdx.x; e < n_heads * HD; e += blockDim.x) {
+      const int h = e / HD, d = e - h * HD;
+      const float *pw = ws + (size_t)h * pstr;
+      float M = pw[0];
 #pragma unroll
-    for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
-    float o = 0.f, lsum = 0.f;
+      for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
+      float o = 0.f, lsum = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWavesPerSplit; w++) {
-      const float f = exp2f(pw[w * wstr] - M);
-      o = fmaf(pw[w * wstr + kPartHead + d], f, o);
-      lsum = fmaf(pw[w * wstr + 1], f, lsum);
+      for (int w = 0; w < kWavesPerSplit; w++) {
+        const float f = exp2f(pw[w * wstr] - M);
+        o = fmaf(pw[w * wstr + kPartHead + d], f, o);
+        lsum = fmaf(pw[w * wstr + 1], f, lsum);
+      }
+      float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
+                            (size_t)pslot) * pstr;
+      pp[kPartHead + d] = o;
+      if (d == 0) {
+        pp[0] = M;
+        pp[1] = lsum;
+      }
     }
-    float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
-                          (size_t)split) * pstr;
-    pp[kPartHead + d] = o;
-    if (d == 0) {
-      pp[0] = M;
-      pp[1] = lsum;
+    __syncthreads();  // LDS is free for the next visit
+  };
+
+  if constexpr (!WQ) {
+    const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+    const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+    const int npos = sd.pos + 1;
+    const int t0 = split * P.split_len;
+    if (t0 >= npos) return;  // a shorter sequence of a ragged batch: no split here
+    const int t1 = min(npos, t0 + P.split_len);
+    const bool owns_new = t1 == npos;  // this split holds position pos
+    // Positions [t0, tend) stream from HBM; pos itself, when owned, from LDS.
+    visit(sd, seq, li, t0, owns_new ? t1 - 1 : t1, owns_new, split, nullptr);
+  } else {
+    const int n_units = P.n_seq * P.n_layers_call;
+    int32_t *const wq = P.wq + (size_t)P.wq_set * (size_t)P.wq_cap * kWqStride;
+    int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)n_units));
+    uint32_t probe = blockIdx.x * 2654435761u;  // where the next search starts
+    for (;;) {
+      int32_t *ctr = wq + (size_t)unit * kWqStride;
+      if (threadIdx.x == 0)
+        s_bcast = __hip_atomic_fetch_add(ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int pslot = __builtin_amdgcn_readfirstlane(s_bcast);
+      __syncthreads();
+      if (pslot < P.max_splits) {
+        const int seq = unit % P.n_seq, li = unit / P.n_seq;
+        const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+        visit(sd, seq, li, 0, sd.pos, pslot == 0, pslot, ctr);
+      }
+      // Next unit: one with at least kWqStealMin unclaimed pieces and a free
+      // partial slot, searched by wave 0 from a per-workgroup offset.
+      if (wave == 0) {
+        int found = -1;
+        probe = probe * 1664525u + 1013904223u;
+        const int start = (int)(probe % (uint32_t)n_units);
+        for (int b = 0; b < n_units && found < 0; b += 64) {
+          const int v = b + lane;
+          bool ok = false;
+          if (v < n_units) {
+            const int uu = (start + v) % n_units;
+            const int32_t *cu = wq + (size_t)uu * kWqStride;
+            const int pos2 = P.seqs ? P.seqs[uu % P.n_seq].pos : P.one.pos;
+            const int np2 = piece_map(pos2, P.piece_big, P.piece_len).npieces;
+            const int32_t nx = __hip_atomic_load(cu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int32_t ns = __hip_atomic_load(cu + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = nx + kWqStealMin <= np2 && ns < P.max_splits;
+          }
+          const uint64_t mask = __ballot(ok);
+          if (mask) found = (start + b + (int)__builtin_ctzll(mask)) % n_units;
+        }
+        if (lane == 0) s_bcast = found;
+      }
+      __syncthreads();
+      unit = __builtin_amdgcn_readfirstlane(s_bcast);
+      __syncthreads();
+      if (unit < 0) break;
     }
   }
 }
@@ -737,27 +868,33 @@ static inline size_t layer_lds_bytes(const ShapeDev &sh, int32_t stage_rows) {
   return layer_lds_layout(sh, stage_rows).total;
 }
 
-template <int FMT, int HD, int CD, int G, int U, int STG>
+template <int FMT, int HD, int CD, int G, int U, int STG, bool WQ>
 static hipError_t launch_fast_s(const DecodeParams &p, int n_layers, hipStream_t s) {
-  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  const dim3 grid = WQ ? dim3(p.wq_grid) : dim3(p.max_splits, p.n_seq, n_layers);
   const size_t lds = layer_lds_bytes(p.sh, STG ? p.stage_rows : 0);
   if (p.att)
-    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG>), grid, dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG, WQ>), grid, dim3(kThreads), lds, s, p);
   else
-    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, false, STG>), grid, dim3(kThreads), lds, s, p);
+    hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, false, STG, WQ>), grid, dim3(kThreads), lds, s,
+                       p);
   return hipGetLastError();
 }
 
 template <int FMT, int HD, int CD, int G, int U>
 static hipError_t launch_fast_u(const DecodeParams &p, int n_layers, hipStream_t s) {
-  if (p.stage_rows > 0 && p.stage_mode == 1) return launch_fast_s<FMT, HD, CD, G, U, 1>(p, n_layers, s);
-  if (p.stage_rows > 0 && p.stage_mode == 2) return launch_fast_s<FMT, HD, CD, G, U, 2>(p, n_layers, s);
-  return launch_fast_s<FMT, HD, CD, G, U, 0>(p, n_layers, s);
+  if (p.stage_rows > 0 && p.stage_mode == 2) {
+    if (p.wq) return launch_fast_s<FMT, HD, CD, G, U, 2, true>(p, n_layers, s);
+    return launch_fast_s<FMT, HD, CD, G, U, 2, false>(p, n_layers, s);
+  }
+  if (p.stage_rows > 0 && p.stage_mode == 1) {
+    if (p.wq) return launch_fast_s<FMT, HD, CD, G, U, 1, true>(p, n_layers, s);
+    return launch_fast_s<FMT, HD, CD, G, U, 1, false>(p, n_layers, s);
+  }
+  return launch_fast_s<FMT, HD, CD, G, U, 0, false>(p, n_layers, s);
 }
 
 template <int FMT, int HD, int CD, int G>
 static hipError_t launch_fast(const DecodeParams &p, int n_layers, hipStream_t s) {
-  if (p.tune_unroll == 4) return launch_fast_u<FMT, HD, CD, G, 4>(p, n_layers, s);
   return launch_fast_u<FMT, HD, CD, G, 2>(p, n_layers, s);
 }
 
@@ -773,22 +910,39 @@ hipError_t launch_layer(const DecodeParams &p, int n_layers, hipStream_t s) {
   }
 }
 
-template <int FMT, int HD, int G>
-int layer_occupancy(const ShapeDev &sh, int32_t stage_rows) {
-  constexpr int CD = (FMT == 1 && G <= 2) ? 32 : 16;
+template <int FMT, int HD, int CD, int G, int STG, bool WQ>
+static int occupancy_of(const ShapeDev &sh, int32_t stage_rows) {
   int n = 0;
-  const hipError_t e =
-      stage_rows > 0 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                           &n, k_layer<FMT, HD, CD, G, 2, false, kDefaultStageMode>, kThreads,
-                           layer_lds_bytes(sh, stage_rows))
-                     : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                           &n, k_layer<FMT, HD, CD, G, 2, false, 0>, kThreads,
-                           layer_lds_bytes(sh, 0));
-  if (e != hipSuccess) {
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_layer<FMT, HD, CD, G, 2, false, STG, WQ>,
+                                                   kThreads,
+                                                   layer_lds_bytes(sh, STG ? stage_rows : 0)) !=
+      hipSuccess) {
     (void)hipGetLastError();
     return 1;
   }
   return n > 0 ? n : 1;
+}
+
+template <int FMT, int HD, int CD, int G>
+static int occupancy_cd(const ShapeDev &sh, int32_t stage_mode, int32_t stage_rows, bool wq) {
+  if (stage_rows > 0 && stage_mode == 2)
+    return wq ? occupancy_of<FMT, HD, CD, G, 2, true>(sh, stage_rows)
+              : occupancy_of<FMT, HD, CD, G, 2, false>(sh, stage_rows);
+  if (stage_rows > 0 && stage_mode == 1)
+    return wq ? occupancy_of<FMT, HD, CD, G, 1, true>(sh, stage_rows)
+              : occupancy_of<FMT, HD, CD, G, 1, false>(sh, stage_rows);
+  return occupancy_of<FMT, HD, CD, G, 0, false>(sh, 0);
+}
+
+template <int FMT, int HD, int G>
+int layer_occupancy(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
+                    int32_t stage_rows, bool wq) {
+  if constexpr (FMT == 1 && G <= 2) {
+    if (tune_chunk == 16) return occupancy_cd<1, HD, 16, G>(sh, stage_mode, stage_rows, wq);
+    return occupancy_cd<1, HD, 32, G>(sh, stage_mode, stage_rows, wq);
+  } else {
+    return occupancy_cd<FMT, HD, 16, G>(sh, stage_mode, stage_rows, wq);
+  }
 }
 
 }  // namespace g2b

@@ -9,5 +9,6 @@
 
 namespace g2b {
 template hipError_t launch_layer<G2B_FMT, G2B_HD, G2B_G>(const DecodeParams &, int, hipStream_t);
-template int layer_occupancy<G2B_FMT, G2B_HD, G2B_G>(const ShapeDev &, int32_t);
+template int layer_occupancy<G2B_FMT, G2B_HD, G2B_G>(const ShapeDev &, int32_t, int32_t, int32_t,
+                                                     bool);
 }  // namespace g2b

@@ -44,14 +44,16 @@ int g2b_synth_fill_kv(g2b_ctx *ctx, void *kcache, void *vcache, int32_t ctx_cap,
 int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
 
 /* Tuning of the decode kernel; 0 keeps the automatic choice for each:
- * split_len = positions per split (automatic: a few workgroups per CU per
- * launch), unroll = wave-steps per loop trip (2 or 4), chunk = Q8_0
- * elements per lane (32 = a block, 16 = half a block), stage = how KV rows
- * reach the lanes: -1 per-lane loads straight from HBM, 1 chunks of rows
- * pulled into LDS by global_load_lds, 2 chunks loaded into registers one
- * chunk ahead and written to LDS (0: mode 2 wherever the row is a whole
- * number of 16-byte pieces, else -1). */
-int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t unroll, int32_t chunk, int32_t stage);
+ * split_len = positions per split of the static schedule (automatic: one
+ * round of workgroups per launch), chunk = Q8_0 elements per lane (32 = a
+ * block, 16 = half a block), stage = how KV rows reach the lanes (-1
+ * per-lane loads straight from HBM, 1 chunks of rows pulled into LDS by
+ * global_load_lds, 2 chunks loaded into registers one chunk ahead and written
+ * to LDS; automatic: 2 wherever the row is a whole number of 16-byte pieces,
+ * else -1), piece = the work-queue schedule (-1 static splits only, > 0
+ * positions per claimed piece; automatic: work queue when every (sequence,
+ * layer) of the call can have a resident workgroup). */
+int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t chunk, int32_t stage, int32_t piece);
 
 /* Kernel timing with HIP events on the context's stream: while enabled,
  * every decode-kernel launch is bracketed by two events.  _read waits for

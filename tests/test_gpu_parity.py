@@ -146,10 +146,25 @@ SHAPES = {
 }
 
 
+# Schedules of the decode call: (all layers in one call?, g2b_ctx_tune arguments
+# (split_len, chunk, stage, piece)).  "wq" forces the work queue (piece > 0),
+# "static" forces static splits, "dma" / "direct" the other KV row paths.
+MODES = {
+    "fused": (True, None),
+    "layers": (False, None),
+    "wq": (False, (0, 0, 2, 1)),
+    "wq_fused": (True, (0, 0, 2, 8)),
+    "static": (False, (0, 0, 2, -1)),
+    "dma": (True, (0, 0, 1, -1)),
+    "direct": (False, (0, 0, -1, -1)),
+}
+
+
 def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, norms=None,
-                   setup=None):
+                   setup=None, tune=None):
     """n_seq ragged sequences, all layers: device (one fused call or layer by
-    layer) against the oracle, sequence by sequence.  norms: None, or
+    layer) against the oracle, sequence by sequence.  tune: None or the
+    g2b_ctx_tune arguments for the context.  norms: None, or
     (q_norm, k_norm, eps) with q_norm/k_norm None or indexable by layer (an
     entry None: that layer has no such weights); the oracle side normalises
     its inputs with them, and they are set on the context unless setup(ctx)
@@ -166,6 +181,8 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
         return normed(x, None if kn is None else kn[L], o.n_kv_heads, hd, eps)
 
     with attn.Context(ashape(o)) as ctx:
+        if tune:
+            ctx.tune(*tune)
         if setup:
             setup(ctx)
         elif norms:
@@ -219,14 +236,15 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
 
 
 @pytest.mark.parametrize("name", sorted(SHAPES))
-@pytest.mark.parametrize("fused", [True, False])
-def test_batched_ragged_vs_oracle(gpu_device, name, fused):
+@pytest.mark.parametrize("mode", sorted(MODES))
+def test_batched_ragged_vs_oracle(gpu_device, name, mode):
     nh, nkv, hd, arch, q8 = SHAPES[name]
     o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
     caps = [1, 37, 300, 700, 129]
     poss = [0, 36, 211, 650, 64]  # pos 0 (attends to itself only), full, ragged
-    print(f"[batch] {name} fused={fused}", flush=True)
-    run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused)
+    fused, tune = MODES[mode]
+    print(f"[batch] {name} mode={mode}", flush=True)
+    run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused, tune=tune)
 
 
 QKN_SHAPES = {
@@ -281,12 +299,66 @@ def test_qk_norm_off_and_eps_rules(gpu_device):
 
 
 @pytest.mark.parametrize("q8", [True, False])
-def test_many_splits_single_sequence(gpu_device, q8):
-    """A long single sequence, layer by layer: hundreds of splits, every
-    split boundary crossed, partial last split."""
+@pytest.mark.parametrize("mode", ["layers", "wq"])
+def test_many_splits_single_sequence(gpu_device, q8, mode):
+    """A long single sequence, layer by layer: hundreds of splits (or
+    hundreds of work-queue pieces claimed by many workgroups), every boundary
+    crossed, partial last split or piece."""
     o = orc.Shape(1, 16, 8, 128, 1e6, orc.ARCH_QWEN3, q8)
-    print(f"[splits] q8={q8}", flush=True)
-    run_batch_case(o, [6000], [5999], seed=77, fused=False)
+    print(f"[splits] q8={q8} mode={mode}", flush=True)
+    run_batch_case(o, [6000], [5999], seed=77, fused=False,
+                   tune=(0, 0, 2, 12) if mode == "wq" else None)
+
+
+def test_work_queue_counters_across_calls(gpu_device):
+    """One context, work-queue calls with different unit counts in turn (one
+    layer, both layers, the other layer, a smaller batch, both layers
+    again): the per-launch counters are zeroed between calls over the extent
+    any earlier call used, so every call matches the oracle."""
+    o = orc.Shape(2, 16, 8, 128, 1e6, orc.ARCH_QWEN3, True)
+    caps, poss = [400, 90, 257], [399, 60, 256]
+    nL, n_seq = o.n_layers, len(caps)
+    with attn.Context(ashape(o)) as ctx:
+        ctx.tune(0, 0, 2, 4)
+        seqs = [DevSeq(ctx, o, c) for c in caps]
+        hosts = [orc.alloc_kv(o, c) for c in caps]
+        try:
+            for i, (c, p) in enumerate(zip(caps, poss)):
+                for L in range(nL):
+                    kp = orc.normal(900 + 10 * i + L, p * o.nkv).reshape(p, o.nkv)
+                    vp = orc.normal(950 + 10 * i + L, p * o.nkv).reshape(p, o.nkv)
+                    seqs[i].prefill(L, kp, vp)
+                    orc.kv_prefill(o, c, L, 0, hosts[i][0], hosts[i][1], kp, vp)
+            q = orc.normal(31, nL * n_seq * o.nq).reshape(nL, n_seq, o.nq)
+            k = orc.normal(32, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
+            v = orc.normal(33, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
+            refs = {}
+            for i, (c, p) in enumerate(zip(caps, poss)):
+                for L in range(nL):
+                    kc, vc = orc.alloc_kv(o, c)
+                    kc[:], vc[:] = hosts[i][0], hosts[i][1]
+                    ref, _ = orc.attn_layer(o, c, L, p, kc, vc, q[L, i], k[L, i], v[L, i])
+                    ex, _ = exact_attention(o, c, L, p, kc, vc, q[L, i])
+                    refs[(L, i)] = (ref, ex)
+            for step, (batch, layers) in enumerate([([0, 1, 2], [0]), ([0, 1, 2], [0, 1]),
+                                                    ([0, 1, 2], [1]), ([1], [0, 1]),
+                                                    ([2, 0], [1]), ([0, 1, 2], [0, 1])]):
+                ctx.batch_begin([(poss[i], caps[i], seqs[i].k, seqs[i].v) for i in batch])
+                L0, nl, nb = layers[0], len(layers), len(batch)
+                qs = np.ascontiguousarray(q[L0:L0 + nl][:, batch])
+                qd = hip.to_device(qs)
+                ks = hip.to_device(np.ascontiguousarray(k[L0:L0 + nl][:, batch]))
+                vs = hip.to_device(np.ascontiguousarray(v[L0:L0 + nl][:, batch]))
+                ctx.attn_layers(L0, nl, qd.ptr, ks.ptr, vs.ptr)
+                ctx.sync()
+                out = qd.download(np.float32, qs.size).reshape(qs.shape)
+                for a, L in enumerate(layers):
+                    for b, i in enumerate(batch):
+                        ref, ex = refs[(L, i)]
+                        check_out(out[a, b], ref, ex)
+        finally:
+            for s_ in seqs:
+                s_.free()
 
 
 def test_forward_host_matches_device_call(gpu_device):
