@@ -22,7 +22,9 @@ Bytes per step are algorithmic, as BASELINE states them:
 CPU baseline: the C99 oracle (a restatement of the reference path, built
 with the reference flags) on a bounded sample of the same units and the
 same KV bytes the GPU used, timed on the host cores; its outputs double as
-a full-size parity check.  rank 0 prints one JSON line.
+a full-size parity check.  After the headline, the other BASELINE configs
+(c1, c2, c3, c5) are measured the same way (layer-serial and all layers in
+one call) and reported under all_configs.  rank 0 prints one JSON line.
 """
 from __future__ import annotations
 
@@ -110,6 +112,106 @@ def load_traffic(workload: str):
         return json.load(f)
 
 
+class Workload:
+    """One config's KV caches (filled on the device), inputs and step functions."""
+
+    def __init__(self, name: str, args, n_seq_override: int = 0):
+        self.name = name
+        shape, n_seq, (lo, hi), p_scale, desc = CONFIGS[name]
+        if n_seq_override:
+            n_seq = n_seq_override
+        self.shape, self.n_seq, self.desc = shape, n_seq, desc
+        L, nq, nkv = shape.n_layers, shape.nq, shape.nkv
+        if lo == hi:
+            poss = [lo] * n_seq
+        else:
+            u = splitmix_uniform(args.seed ^ 0xC7C7, n_seq)
+            poss = [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]
+        self.poss, self.caps = poss, [p + 1 for p in poss]
+        thr = norm_ppf(1.0 - p_scale) if p_scale > 0 else float("inf")
+        kv_total = sum(2 * attn.kv_bytes(shape, c) for c in self.caps)
+        log(f"{name}: {desc}; n_seq={n_seq}, KV {kv_total / 1e9:.2f} GB")
+        self.ctx = ctx = attn.Context(shape)
+        ctx.tune(args.split, args.chunk, args.stage, args.piece)
+        t0 = time.perf_counter()
+        self.kvs = [ctx.kv_alloc(c) for c in self.caps]
+        for i, (p, c) in enumerate(zip(poss, self.caps)):
+            k, v = self.kvs[i]
+            ctx.synth_fill_kv(k, v, c, 0, L, 0, p, args.seed, i, thr)
+            if i % 32 == 31:
+                ctx.sync()
+                log(f"filled {i + 1}/{n_seq} sequences ({time.perf_counter() - t0:.1f}s)")
+        ctx.sync()
+        self.t_fill = time.perf_counter() - t0
+        log(f"KV fill done in {self.t_fill:.1f}s")
+        self.nQ, self.nK = L * n_seq * nq, L * n_seq * nkv
+        self.q0 = hip.DeviceBuffer(self.nQ * 4)
+        self.qw = hip.DeviceBuffer(self.nQ * 4)
+        self.kb = hip.DeviceBuffer(self.nK * 4)
+        self.vb = hip.DeviceBuffer(self.nK * 4)
+        ctx.synth_normal(self.q0.ptr, self.nQ, attn.stream_seed(args.seed, 0, 0, 2))
+        ctx.synth_normal(self.kb.ptr, self.nK, attn.stream_seed(args.seed, 0, 0, 3))
+        ctx.synth_normal(self.vb.ptr, self.nK, attn.stream_seed(args.seed, 0, 0, 4))
+        ctx.batch_begin([(p, c, k, v) for p, c, (k, v) in zip(poss, self.caps, self.kvs)])
+        ctx.sync()
+        self.bytes_per_step = step_bytes(shape, poss)
+
+    def step_layer_serial(self):
+        s, ctx, n = self.shape, self.ctx, self.n_seq
+        ctx.synth_copy(self.qw.ptr, self.q0.ptr, self.nQ * 4)
+        for layer in range(s.n_layers):
+            ctx.attn_layers(layer, 1, self.qw.ptr + layer * n * s.nq * 4,
+                            self.kb.ptr + layer * n * s.nkv * 4,
+                            self.vb.ptr + layer * n * s.nkv * 4)
+
+    def step_fused(self):
+        self.ctx.synth_copy(self.qw.ptr, self.q0.ptr, self.nQ * 4)
+        self.ctx.attn_layers(0, self.shape.n_layers, self.qw.ptr, self.kb.ptr, self.vb.ptr)
+
+    def timed(self, step, steps, warmup):
+        """(event ms per step, host ms per step, decode-kernel ms summed, launches)."""
+        ctx = self.ctx
+        for _ in range(warmup):
+            step()
+        ctx.sync()
+        ctx.profile(True)
+        ctx.profile_read()
+        e0, e1 = hip.Event(), hip.Event()
+        h0 = time.perf_counter()
+        e0.record(ctx.stream)
+        for _ in range(steps):
+            step()
+        e1.record(ctx.stream)
+        e1.synchronize()
+        wall = time.perf_counter() - h0
+        dms, nlaunch = ctx.profile_read()
+        ctx.profile(False)
+        return e0.elapsed_ms(e1) / steps, wall / steps * 1e3, dms, nlaunch
+
+    def summary(self, steps, warmup):
+        """Layer-serial and all-layers-in-one-call figures of this config."""
+        ms, _, dms, dn = self.timed(self.step_layer_serial, steps, warmup)
+        fms, _, fdms, fdn = self.timed(self.step_fused, steps, 1)
+        sb, L = self.bytes_per_step, self.shape.n_layers
+        per_launch = launch_bytes(self.shape, self.poss, 1)
+        return {"workload": self.desc, "n_seq": self.n_seq,
+                "ctx_min": min(self.poss), "ctx_max": max(self.poss),
+                "us_per_step": round(ms * 1e3, 2), "GBps": round(sb / (ms * 1e-3) / 1e9, 2),
+                "pct_hbm_peak": round(100 * sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+                "k_layer_avg_us": round(dms / max(dn, 1) * 1e3, 2),
+                "k_layer_GBps": round(per_launch / (dms / max(dn, 1) * 1e-3) / 1e9, 2),
+                "all_layers_one_call_us_per_step": round(fms * 1e3, 2),
+                "all_layers_one_call_GBps": round(sb / (fms * 1e-3) / 1e9, 2),
+                "bytes_per_step": sb}
+
+    def close(self):
+        for k, v in self.kvs:
+            self.ctx.kv_free(k, v)
+        for b in (self.q0, self.qw, self.kb, self.vb):
+            b.free()
+        self.ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,11 +222,13 @@ def main():
     ap.add_argument("--seed", type=int, default=20241201)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-fused", action="store_true", help="skip the all-layers-in-one-call run")
+    ap.add_argument("--no-others", action="store_true",
+                    help="skip the other BASELINE configs (reported under all_configs)")
     ap.add_argument("--cpu-seq-a", type=int, default=4, help="sequences in the 1-thread sample")
     ap.add_argument("--cpu-seq-b", type=int, default=32, help="sequences in the all-threads sample")
     ap.add_argument("--cpu-min-s", type=float, default=8.0,
                     help="repeat each CPU sample until it has run this long")
-    ap.add_argument("--split", type=int, default=0, help="decode split length (0 = automatic)")
+    ap.add_argument("--split", type=int, default=0, help="static split length (0 = automatic)")
     ap.add_argument("--chunk", type=int, default=0, help="Q8 elements per lane (0 = auto)")
     ap.add_argument("--stage", type=int, default=0, choices=(-1, 0, 1, 2),
                     help="KV row path: -1 per-lane HBM loads, 1 global_load_lds chunks, "
@@ -148,45 +252,9 @@ def main():
         sys.exit(1)
     hip.set_device(0)
 
-    shape, n_seq, (lo, hi), p_scale, desc = CONFIGS[args.config]
-    if args.n_seq:
-        n_seq = args.n_seq
-    L, nq, nkv, rb = shape.n_layers, shape.nq, shape.nkv, row_bytes(shape)
-    if lo == hi:
-        poss = [lo] * n_seq
-    else:
-        u = splitmix_uniform(args.seed ^ 0xC7C7, n_seq)
-        poss = [int(lo + min(int(x * (hi - lo + 1)), hi - lo)) for x in u]
-    caps = [p + 1 for p in poss]
-    thr = norm_ppf(1.0 - p_scale) if p_scale > 0 else float("inf")
-    kv_total = sum(2 * attn.kv_bytes(shape, c) for c in caps)
-    log(f"{args.config}: {desc}; n_seq={n_seq}, KV {kv_total / 1e9:.2f} GB")
-
-    ctx = attn.Context(shape)
-    ctx.tune(args.split, args.chunk, args.stage, args.piece)
-    stream = ctx.stream
-    t0 = time.perf_counter()
-    kvs = [ctx.kv_alloc(c) for c in caps]
-    for i, (p, c) in enumerate(zip(poss, caps)):
-        k, v = kvs[i]
-        ctx.synth_fill_kv(k, v, c, 0, L, 0, p, args.seed, i, thr)
-        if i % 32 == 31:
-            ctx.sync()
-            log(f"filled {i + 1}/{n_seq} sequences ({time.perf_counter() - t0:.1f}s)")
-    ctx.sync()
-    t_fill = time.perf_counter() - t0
-    log(f"KV fill done in {t_fill:.1f}s")
-
-    nQ, nK = L * n_seq * nq, L * n_seq * nkv
-    q0 = hip.DeviceBuffer(nQ * 4)
-    qw = hip.DeviceBuffer(nQ * 4)
-    kb = hip.DeviceBuffer(nK * 4)
-    vb = hip.DeviceBuffer(nK * 4)
-    ctx.synth_normal(q0.ptr, nQ, attn.stream_seed(args.seed, 0, 0, 2))
-    ctx.synth_normal(kb.ptr, nK, attn.stream_seed(args.seed, 0, 0, 3))
-    ctx.synth_normal(vb.ptr, nK, attn.stream_seed(args.seed, 0, 0, 4))
-    ctx.batch_begin([(p, c, k, v) for p, c, (k, v) in zip(poss, caps, kvs)])
-    ctx.sync()
+    w = Workload(args.config, args, args.n_seq)
+    ctx, shape, poss, caps, kvs = w.ctx, w.shape, w.poss, w.caps, w.kvs
+    L, n_seq = shape.n_layers, w.n_seq
     if args.calibrate_copy:
         nb = args.calibrate_copy << 20
         src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
@@ -196,54 +264,27 @@ def main():
         dst.free()
         log(f"calibration copy of {args.calibrate_copy} MiB done")
 
-    def step_layer_serial():
-        ctx.synth_copy(qw.ptr, q0.ptr, nQ * 4)
-        for layer in range(L):
-            ctx.attn_layers(layer, 1, qw.ptr + layer * n_seq * nq * 4,
-                            kb.ptr + layer * n_seq * nkv * 4, vb.ptr + layer * n_seq * nkv * 4)
-
-    def step_fused():
-        ctx.synth_copy(qw.ptr, q0.ptr, nQ * 4)
-        ctx.attn_layers(0, L, qw.ptr, kb.ptr, vb.ptr)
-
-    def timed(step, steps, warmup):
-        for _ in range(warmup):
-            step()
-        ctx.sync()
-        ctx.profile(True)
-        ctx.profile_read()
-        e0, e1 = hip.Event(), hip.Event()
-        h0 = time.perf_counter()
-        e0.record(stream)
-        for _ in range(steps):
-            step()
-        e1.record(stream)
-        e1.synchronize()
-        wall = time.perf_counter() - h0
-        dms, nlaunch = ctx.profile_read()
-        ctx.profile(False)
-        return e0.elapsed_ms(e1) / steps, wall / steps * 1e3, dms, nlaunch
-
+    sb = w.bytes_per_step
     if args.sweep_splits:
         for sl in [int(x) for x in args.sweep_splits.split(",")]:
-            ctx.tune(sl, args.chunk, args.stage, args.piece)
-            sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
-            log(f"split {sl}: {sms * 1e3:.1f} us/step, {step_bytes(shape, poss) / sms / 1e6:.1f} "
-                f"GB/s, k_layer avg {sd / max(sn, 1) * 1e3:.1f} us")
+            ctx.tune(sl, args.chunk, args.stage, -1)
+            sms, _, sd, sn = w.timed(w.step_layer_serial, max(3, args.steps // 2), 1)
+            log(f"split {sl}: {sms * 1e3:.1f} us/step, {sb / sms / 1e6:.1f} GB/s, "
+                f"k_layer avg {sd / max(sn, 1) * 1e3:.1f} us")
         ctx.tune(args.split, args.chunk, args.stage, args.piece)
     if args.sweep_variants:
         for v in args.sweep_variants.split(";"):
             sl, ch, st, pc = [int(x) for x in v.split(",")]
             ctx.tune(sl, ch, st, pc)
-            sms, _, sd, sn = timed(step_layer_serial, max(3, args.steps // 2), 1)
-            fms, _, fd, fn = timed(step_fused, max(3, args.steps // 2), 1)
-            log(f"variant split={sl} chunk={ch} stage={st} piece={pc}: layer-serial {sms * 1e3:.1f} us/step "
-                f"({step_bytes(shape, poss) / sms / 1e6:.1f} GB/s, k_layer {sd / max(sn, 1) * 1e3:.1f}"
-                f" us), fused {fms * 1e3:.1f} us/step ({step_bytes(shape, poss) / fms / 1e6:.1f} GB/s)")
+            sms, _, sd, sn = w.timed(w.step_layer_serial, max(3, args.steps // 2), 1)
+            fms, _, fd, fn = w.timed(w.step_fused, max(3, args.steps // 2), 1)
+            log(f"variant split={sl} chunk={ch} stage={st} piece={pc}: layer-serial "
+                f"{sms * 1e3:.1f} us/step ({sb / sms / 1e6:.1f} GB/s, k_layer "
+                f"{sd / max(sn, 1) * 1e3:.1f} us), fused {fms * 1e3:.1f} us/step "
+                f"({sb / fms / 1e6:.1f} GB/s)")
         ctx.tune(args.split, args.chunk, args.stage, args.piece)
 
-    ms, wall_ms, dec_ms, dec_n = timed(step_layer_serial, args.steps, args.warmup)
-    sb = step_bytes(shape, poss)
+    ms, wall_ms, dec_ms, dec_n = w.timed(w.step_layer_serial, args.steps, args.warmup)
     gbps = sb / (ms * 1e-3) / 1e9
     log(f"layer-serial: {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), {gbps:.1f} GB/s, "
         f"{100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak")
@@ -254,7 +295,7 @@ def main():
 
     fused = None
     if not args.no_fused:
-        fms, fwall, fdec, fn = timed(step_fused, args.steps, 1)
+        fms, fwall, fdec, fn = w.timed(w.step_fused, args.steps, 1)
         fused = {"us_per_step": round(fms * 1e3, 2),
                  "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
                  "k_layer_avg_us": round(fdec / max(fn, 1) * 1e3, 2),
@@ -263,13 +304,28 @@ def main():
         log(f"all layers in one call: {fms * 1e3:.1f} us/step, {fused['GBps']} GB/s")
 
     # Leave the layer-serial outputs in qw for the parity sample.
-    step_layer_serial()
+    w.step_layer_serial()
     ctx.sync()
 
     cpu = None
     parity = None
     if not args.no_cpu:
-        cpu, parity = cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb)
+        cpu, parity = cpu_leg(args, ctx, shape, poss, caps, kvs, w.q0, w.qw, w.kb, w.vb)
+    t_fill = w.t_fill
+    w.close()
+
+    others = None
+    if not args.no_others:
+        others = {}
+        for name in sorted(CONFIGS):
+            if name == args.config:
+                continue
+            o = Workload(name, args)
+            others[name] = o.summary(max(5, args.steps // 2), 2)
+            log(f"{name}: layer-serial {others[name]['us_per_step']} us/step "
+                f"({others[name]['GBps']} GB/s, {others[name]['pct_hbm_peak']}% of HBM peak), "
+                f"all layers in one call {others[name]['all_layers_one_call_us_per_step']} us/step")
+            o.close()
 
     traffic = load_traffic(args.config)
     roof = {"bound": "hbm", "kernel": "k_layer", "achieved": round(dec_gbps, 2),
@@ -284,7 +340,7 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"{args.config}: {desc}", "n_seq": n_seq,
+        "config": {"workload": f"{args.config}: {w.desc}", "n_seq": n_seq,
                    "ctx_min": min(poss), "ctx_max": max(poss), "layers": L,
                    "n_heads": shape.n_heads, "n_kv_heads": shape.n_kv_heads,
                    "head_dim": shape.head_dim, "kv": "q8_0" if shape.kv_q8 else "f32",
@@ -298,10 +354,8 @@ def main():
         "cpu_baseline": cpu,
         "all_layers_one_call": fused,
         "parity_full_size": parity,
+        "all_configs": others,
     }
-    for k, v in kvs:
-        ctx.kv_free(k, v)
-    ctx.close()
     print(json.dumps(line), flush=True)
 
 

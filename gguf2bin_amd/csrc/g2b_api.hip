@@ -103,6 +103,9 @@ size_t row_bytes_of(const g2b_shape *s) {
 // dwords around 34-byte blocks.
 constexpr size_t kKvSlack = 256;
 
+// The staged KV loads read 16-byte pieces from the cache bases.
+bool misaligned(const void *p) { return ((uintptr_t)p & 15u) != 0; }
+
 int set_device(g2b_ctx *c) {
   G2B_HIP(c, hipSetDevice(c->device));
   return G2B_OK;
@@ -183,11 +186,14 @@ int32_t slots_for(g2b_ctx *c, const DecodeParams &dp, bool wq) {
   return std::max(1, c->n_cu) * std::max(1, occ);
 }
 
+// min_len: the shortest split worth a workgroup (its waves get a few
+// wave-steps or chunks each; shorter splits cost more in setup and partials
+// than they gain in parallelism).
 int32_t choose_split(const g2b_ctx *c, int64_t slots, int64_t total_pos, int32_t max_pos,
-                     int32_t n_layers, bool fast) {
+                     int32_t n_layers, bool fast, int32_t min_len) {
   const int64_t work = total_pos * (int64_t)n_layers;
   int64_t sl = c->split_override > 0 ? c->split_override : (work + slots - 1) / slots;
-  if (c->split_override <= 0) sl = std::max<int64_t>(sl, 64);
+  if (c->split_override <= 0) sl = std::max<int64_t>(sl, min_len);
   const int64_t min_for_cap = ((int64_t)max_pos + 1 + 511) / 512;
   sl = std::max(sl, min_for_cap);
   if (!fast) sl = std::min<int64_t>(sl, kGenericMaxSplit);
@@ -229,7 +235,12 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
-  dp.stage_mode = c->tune_stage < 0 ? 0 : c->tune_stage > 0 ? c->tune_stage : kDefaultStageMode;
+  // Staging pays for Q8_0 rows, whose per-lane block windows overlap; F32
+  // rows are read by the lanes in whole, disjoint 64-byte runs already.
+  dp.stage_mode = c->tune_stage < 0   ? 0
+                  : c->tune_stage > 0 ? c->tune_stage
+                  : c->shape.kv_q8    ? kDefaultStageMode
+                                      : 0;
   dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
@@ -283,7 +294,12 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     dp.wq_grid = (int32_t)slots;
     dp.split_len = 0;
   } else {
-    const int32_t split_len = choose_split(c, slots, total_pos, max_pos, n_layers, fast);
+    // (measured: four staged chunks or eight per-lane wave-steps per wave)
+    const int32_t min_len = !fast                ? 64
+                            : dp.stage_rows > 0 ? kWavesPerSplit * 4 * dp.stage_rows
+                                                : kWavesPerSplit * 8 * decode_ppw(c->sh, dp.tune_chunk);
+    const int32_t split_len =
+        choose_split(c, slots, total_pos, max_pos, n_layers, fast, min_len);
     max_splits = (max_pos + 1 + split_len - 1) / split_len;
     if (max_splits > 512)
       return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
@@ -558,6 +574,8 @@ int g2b_batch_begin(g2b_ctx *c, int32_t n_seq, const g2b_seq *seqs) {
   for (int32_t i = 0; i < n_seq; i++) {
     const g2b_seq &s = seqs[i];
     if (!s.kcache || !s.vcache) return fail(c, G2B_ENOKV, "sequence %d has no KV", i);
+    if (misaligned(s.kcache) || misaligned(s.vcache))
+      return fail(c, G2B_EINVAL, "sequence %d: KV caches must be 16-byte aligned", i);
     if (s.ctx_cap < 1 || s.pos < 0 || s.pos >= s.ctx_cap)
       return fail(c, G2B_EPOS, "sequence %d: pos=%d outside [0,%d)", i, s.pos, s.ctx_cap);
     max_pos = std::max(max_pos, s.pos);
@@ -615,6 +633,8 @@ int g2b_attn_forward(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, vo
                      void *vc, float *q, const float *k, const float *v, float *att) {
   if (!c) return G2B_EINVAL;
   if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (misaligned(kc) || misaligned(vc))
+    return fail(c, G2B_EINVAL, "KV caches must be 16-byte aligned");
   if (ctx_cap < 1 || pos < 0 || pos >= ctx_cap)
     return fail(c, G2B_EPOS, "pos=%d outside [0,%d)", pos, ctx_cap);
   if (int rc = set_device(c)) return rc;
@@ -631,6 +651,8 @@ int g2b_attn_forward_host(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_ca
   if (!c) return G2B_EINVAL;
   if (!q || !k || !v) return fail(c, G2B_EINVAL, "q/k/v must be host pointers");
   if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (misaligned(kc) || misaligned(vc))
+    return fail(c, G2B_EINVAL, "KV caches must be 16-byte aligned");
   if (ctx_cap < 1 || pos < 0 || pos >= ctx_cap)
     return fail(c, G2B_EPOS, "pos=%d outside [0,%d)", pos, ctx_cap);
   if (int rc = set_device(c)) return rc;

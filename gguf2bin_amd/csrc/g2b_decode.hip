@@ -214,12 +214,16 @@ static int fast_chunk(const ShapeDev &sh) {
   return 16;
 }
 
-int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode) {
-  if (!decode_fast_available(sh)) return 0;
+int32_t decode_ppw(const ShapeDev &sh, int32_t tune_chunk) {
+  if (!decode_fast_available(sh)) return 1;
   const int cd = tune_chunk == 16 ? 16 : fast_chunk(sh);
   const int lpp = sh.n_kv_heads * (sh.head_dim / cd);
-  if (lpp < 1 || lpp > 64) return 0;
-  return stage_rows_of(sh.row_bytes, 64 / lpp, mode);
+  return lpp >= 1 && lpp <= 64 ? 64 / lpp : 1;
+}
+
+int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode) {
+  if (!decode_fast_available(sh)) return 0;
+  return stage_rows_of(sh.row_bytes, decode_ppw(sh, tune_chunk), mode);
 }
 
 template <int FMT, int HD>

@@ -163,6 +163,8 @@ int decode_blocks_per_cu(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_m
 // DecodeParams): 0 when k_layer must load straight from HBM (no specialised
 // kernel, or rows that are not whole 16-byte pieces).
 int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode);
+// Positions per wave-step of the specialised kernel (1 for other shapes).
+int32_t decode_ppw(const ShapeDev &sh, int32_t tune_chunk);
 // Staging mode k_layer uses unless tuned otherwise.
 constexpr int32_t kDefaultStageMode = 2;
 // k_layer for one (KV format 0 = F32 / 1 = Q8_0, head_dim, GQA group),

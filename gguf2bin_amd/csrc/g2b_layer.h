@@ -94,6 +94,9 @@ struct Codec<0, 16> {
     o.o1 = o.o2 = o.sel = o.sshift = 0;
     return o;
   }
+  // Default cache policy: each of the four loads touches every cache line of
+  // the lanes' 64-byte runs, and the later ones hit the lines the first one
+  // brought into the vector cache (non-temporal loads would fetch them again).
   static __device__ __forceinline__ void load(Raw &r, const uint8_t *row, const LaneOff &o) {
 #pragma unroll
     for (int i = 0; i < 4; i++) r.x[i] = gload<f32x4>(row + o.o0 + 16 * i);
@@ -390,6 +393,30 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     const int layer = P.layer0 + li;
     const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
     const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+    const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+    const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+    // Register staging (STG 2): the next chunk's 16-byte pieces, lane l
+    // taking pieces l, l + 64, ... of the chunk's K and V bytes (at most
+    // kStageLoads per lane and tensor).
+    [[maybe_unused]] u32x4 rk[kStageLoads], rv[kStageLoads];
+    [[maybe_unused]] auto issue = [&](int cs0) {
+      const uint32_t np = (uint32_t)min(P.stage_rows, tend - cs0) * (uint32_t)row / 16u;
+      const uint8_t *gk = kb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+      const uint8_t *gv = vb + (size_t)cs0 * row + 16u * (uint32_t)lane;
+#pragma unroll
+      for (int i = 0; i < kStageLoads; i++) {
+        if (64u * (uint32_t)i + (uint32_t)lane < np) {
+          rk[i] = __builtin_nontemporal_load(
+              (const __attribute__((address_space(1))) u32x4 *)(gk + 1024u * i));
+          rv[i] = __builtin_nontemporal_load(
+              (const __attribute__((address_space(1))) u32x4 *)(gv + 1024u * i));
+        }
+      }
+    };
+    // Static schedule: the wave's first chunk is in flight during the setup.
+    if constexpr (STG == 2 && !WQ) {
+      if (t0 + wave * P.stage_rows < tend) issue(t0 + wave * P.stage_rows);
+    }
     {
       // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by
       // pair as the append does (l3_math.c:74-101)
@@ -435,8 +462,6 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
     }
     if constexpr (STG != 0) __syncthreads();  // every wave has its q: staging may overwrite qrot
-    const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
-    const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
 
     float m[G], l[G], acc[G][CD];
 #pragma unroll
@@ -634,23 +659,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
           }
         }
       } else {
-        // Registers hold the next chunk (kStageLoads 16-byte pieces per lane
-        // and tensor at most) while the current one is consumed.
-        u32x4 rk[kStageLoads], rv[kStageLoads];
-        auto issue = [&](int cs0) {
-          const uint32_t np = (uint32_t)min(R, tend - cs0) * (uint32_t)row / 16u;
-          const uint8_t *gk = kb + (size_t)cs0 * row + 16u * (uint32_t)lane;
-          const uint8_t *gv = vb + (size_t)cs0 * row + 16u * (uint32_t)lane;
-#pragma unroll
-          for (int i = 0; i < kStageLoads; i++) {
-            if (64u * (uint32_t)i + (uint32_t)lane < np) {
-              rk[i] = __builtin_nontemporal_load(
-                  (const __attribute__((address_space(1))) u32x4 *)(gk + 1024u * i));
-              rv[i] = __builtin_nontemporal_load(
-                  (const __attribute__((address_space(1))) u32x4 *)(gv + 1024u * i));
-            }
-          }
-        };
+        // Registers hold the next chunk while the current one is consumed.
         auto stash = [&](int cs0) {
           const uint32_t np = (uint32_t)min(R, tend - cs0) * (uint32_t)row / 16u;
 #pragma unroll
@@ -663,8 +672,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
           }
         };
         if constexpr (!WQ) {
-          int cs0 = t0 + wave * R;
-          if (cs0 < tend) issue(cs0);
+          int cs0 = t0 + wave * R;  // (its loads were issued before the setup)
           for (; cs0 < tend; cs0 += cstride) {
             // (the previous chunk's LDS reads were all used before this point)
             stash(cs0);

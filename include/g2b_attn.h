@@ -18,6 +18,9 @@
  * nkv = n_kv_heads*head_dim.  The layer stride uses the effective context
  * ctx_cap (Model.ctx), not seq_len.
  *
+ * Caches are 16-byte aligned device buffers (g2b_kv_alloc's are; the decode
+ * kernels read them in 16-byte pieces): a misaligned cache is G2B_EINVAL.
+ *
  * Conventions: 0 on success, a negative G2B_E* code on error; nothing
  * aborts or exits (the reference's model_set_ctx/alloc_rt return -1,
  * model_forward returns early).  Device pointers are HIP device addresses on

@@ -402,6 +402,12 @@ def test_errors_map_to_reference_conditions(gpu_device):
             with pytest.raises(attn.G2BError) as e:
                 ctx.attn_forward(2, 3, 16, k, v, buf.ptr, buf.ptr, buf.ptr)
             assert e.value.code == attn.G2B_EINVAL
+            with pytest.raises(attn.G2BError) as e:  # caches are read in 16-byte pieces
+                ctx.attn_forward(0, 3, 16, k + 8, v, buf.ptr, buf.ptr, buf.ptr)
+            assert e.value.code == attn.G2B_EINVAL
+            with pytest.raises(attn.G2BError) as e:
+                ctx.batch_begin([(3, 16, k, v + 4)])
+            assert e.value.code == attn.G2B_EINVAL
             with pytest.raises(attn.G2BError) as e:
                 ctx.batch_begin([(3, 16, k, v), (16, 16, k, v)])
             assert e.value.code == attn.G2B_EPOS
