@@ -71,6 +71,9 @@ __device__ __forceinline__ T gload(const uint8_t *p) {
 constexpr int kAuxNT = 2;
 // s_waitcnt operand (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited.
 constexpr int kWaitVmcnt0 = 0x0F70;
+// Online softmax: how far (log2 units) a score may exceed the reference
+// before the accumulators are rescaled.
+constexpr float kRescaleSlack = 8.f;
 
 // Per-lane addressing of its chunk inside a row.
 struct LaneOff {
@@ -508,6 +511,12 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
           }
         }
       }
+      // m is a reference, not necessarily the running maximum: it is raised
+      // (rescaling l and acc) only when a score exceeds it by more than
+      // kRescaleSlack, so p = exp2(s - m) <= 2^kRescaleSlack and l, acc stay
+      // far from overflow; any reference gives the same softmax, and the
+      // merges scale each partial by its own m.  Rescales, which touch every
+      // accumulator of the wave, become rare.
       bool need = false;
       float mn[G];
 #pragma unroll
@@ -516,7 +525,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
 #pragma unroll
         for (int u = 0; u < UU; u++) mx = fmaxf(mx, sc[u][i]);
         mn[i] = mx;
-        need |= mx > m[i];
+        need |= mx > m[i] + kRescaleSlack;
       }
       if (__any(need)) {
 #pragma unroll
