@@ -35,6 +35,7 @@ struct g2b_ctx {
   int32_t n_seq = 0, max_pos = 0;
   int64_t total_pos = 0;
   SeqDev *d_seqs = nullptr, *h_seqs = nullptr;  // h_seqs: pinned staging
+  SeqDev seq0{};  // the batch's only sequence (n_seq == 1): passed by value
   int32_t seqs_cap = 0;
   hipEvent_t seqs_ev = nullptr;
   bool seqs_ev_live = false;
@@ -607,6 +608,7 @@ int g2b_batch_begin(g2b_ctx *c, int32_t n_seq, const g2b_seq *seqs) {
     d.k = (uint8_t *)seqs[i].kcache;
     d.v = (uint8_t *)seqs[i].vcache;
     c->h_seqs[i] = d;
+    if (i == 0) c->seq0 = d;
   }
   G2B_HIP(c, hipMemcpyAsync(c->d_seqs, c->h_seqs, n_seq * sizeof(SeqDev),
                             hipMemcpyHostToDevice, c->stream));
@@ -624,7 +626,12 @@ int g2b_attn_layers(g2b_ctx *c, int32_t layer0, int32_t n_layers, float *q, cons
   if (!c) return G2B_EINVAL;
   if (c->n_seq < 1) return fail(c, G2B_EINVAL, "no batch: call g2b_batch_begin first");
   if (int rc = set_device(c)) return rc;
+  // One sequence travels in the kernel arguments: no dependent load of its
+  // descriptor at the start of every workgroup.
   SeqDev none{};
+  if (c->n_seq == 1)
+    return run_layers(c, nullptr, c->seq0, 1, c->max_pos, c->total_pos, layer0, n_layers, q, k,
+                      v, att, att_stride);
   return run_layers(c, c->d_seqs, none, c->n_seq, c->max_pos, c->total_pos, layer0, n_layers,
                     q, k, v, att, att_stride);
 }

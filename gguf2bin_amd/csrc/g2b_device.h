@@ -144,6 +144,46 @@ __device__ __forceinline__ void q8_quant_block(const float *x, int cnt, uint8_t 
   }
 }
 
+// The same block quantised by four consecutive lanes of a wave, eight
+// elements each (part = 0..3, all four lanes call together): each lane's
+// maximum of |x| over its elements (NaN skipped by '>', as in the serial
+// loop), combined across the four with the same '>' - an exact maximum, so
+// amax, d, the scale bits and every byte equal q8_quant_block's.  x may be
+// LDS or global memory; elements at or past cnt are padding (byte 0).
+__device__ __forceinline__ void q8_quant_block_x4(const float *x, int cnt, uint8_t *dst,
+                                                  int part) {
+  float v[8];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int e = 8 * part + j;
+    v[j] = e < cnt ? x[e] : 0.f;
+    const float a = fabsf(v[j]);
+    if (a > amax) amax = a;
+  }
+  float o = __shfl_xor(amax, 1);
+  if (o > amax) amax = o;
+  o = __shfl_xor(amax, 2);
+  if (o > amax) amax = o;
+  float d = __fdiv_rn(amax, 127.f);
+  if (!(d > 0.f)) d = 1e-10f;
+  uint16_t *out16 = reinterpret_cast<uint16_t *>(dst);
+  if (part == 0) out16[0] = (uint16_t)f32_to_half_trunc(d);
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    int32_t qa = 0, qb = 0;
+    if (8 * part + j < cnt) {
+      qa = lround_i32_like_host(__fdiv_rn(v[j], d));
+      qa = qa > 127 ? 127 : (qa < -127 ? -127 : qa);
+    }
+    if (8 * part + j + 1 < cnt) {
+      qb = lround_i32_like_host(__fdiv_rn(v[j + 1], d));
+      qb = qb > 127 ? 127 : (qb < -127 ? -127 : qb);
+    }
+    out16[1 + 4 * part + j / 2] = (uint16_t)((uint32_t)(qa & 0xff) | ((uint32_t)(qb & 0xff) << 8));
+  }
+}
+
 // RoPE pair rotation of /root/reference/src/l3_math.c:79 and :98-99:
 // a' = a*c - b*s, b' = a*s + b*c, each product rounded (no contraction).
 __device__ __forceinline__ void rope_pair(float &a, float &b, float c, float s) {

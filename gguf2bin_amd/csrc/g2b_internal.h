@@ -37,8 +37,9 @@ __host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
   return (int32_t)steps * positions_per_wave_step;
 }
 
-// k_layer's dynamic LDS: [0, rows) holds the rotated q and new k before the
-// stream starts and the waves' staging regions (stage_rows > 0) during it;
+// k_layer's dynamic LDS: [0, rows) holds the rotated q and the new k and v
+// (floats) before the stream starts and the waves' staging regions
+// (stage_rows > 0) during it;
 // then the new K and V rows (row_pad bytes each) and n_heads floats of
 // QK-RMSNorm scratch.  After the stream, the wave merge of the partials
 // ([wave][head][kPartHead + head_dim] floats) reuses everything from 0.
@@ -48,7 +49,7 @@ struct LdsLayout {
 __host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
   const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
-  const uint32_t pre = nq * 4u + ((nkv * 4u + 15u) & ~15u);
+  const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u);
   const uint32_t stage = (uint32_t)kWavesPerSplit * 2u * (uint32_t)stage_rows * sh.row_bytes;
   const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)sh.n_heads *
                          (uint32_t)(kPartHead + sh.head_dim) * 4u;

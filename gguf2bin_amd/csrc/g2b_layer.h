@@ -274,12 +274,15 @@ __device__ __forceinline__ float fast_exp2(float x) {
 // workgroup and no cache level is involved.  Every thread calls it.
 __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int layer, int pos,
                                       const float *k, const float *v, const float *rope,
-                                      const NormDev &norm, float *kr, uint8_t *rowk,
+                                      const NormDev &norm, float *kr, float *vr, uint8_t *rowk,
                                       uint8_t *rowv, float *inv) {
   const int hd = sh.head_dim, half = hd / 2;
   const int nkv = sh.n_kv_heads * hd;
   const float *cs = (sh.rope_on && rope) ? rope + (size_t)pos * hd : nullptr;
-  for (int e = threadIdx.x; e < nkv; e += blockDim.x) kr[e] = k[e];
+  for (int e = threadIdx.x; e < nkv; e += blockDim.x) {
+    kr[e] = k[e];
+    vr[e] = v[e];
+  }
   __syncthreads();
   if (const float *wk = norm_weights(norm, layer, 1, hd))
     qk_rmsnorm_block(kr, sh.n_kv_heads, hd, wk, norm.eps, inv);
@@ -293,18 +296,21 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
   }
   __syncthreads();
   if (sh.kv_q8) {
+    // four lanes per block (a multiple of 4 items, so a block's four lanes
+    // are active together)
     const int nb = (nkv + 31) / 32;
-    for (int b = threadIdx.x; b < 2 * nb; b += blockDim.x) {
+    for (int it = threadIdx.x; it < 8 * nb; it += blockDim.x) {
+      const int b = it >> 2, part = it & 3;
       const bool is_k = b < nb;
       const int bb = is_k ? b : b - nb;
       const int cnt = min(32, nkv - 32 * bb);
-      q8_quant_block(is_k ? kr + 32 * bb : v + 32 * bb, cnt, (is_k ? rowk : rowv) + 34 * bb);
+      q8_quant_block_x4((is_k ? kr : vr) + 32 * bb, cnt, (is_k ? rowk : rowv) + 34 * bb, part);
     }
   } else {
     float *fk = reinterpret_cast<float *>(rowk), *fv = reinterpret_cast<float *>(rowv);
     for (int e = threadIdx.x; e < nkv; e += blockDim.x) {
       fk[e] = kr[e];
-      fv[e] = v[e];
+      fv[e] = vr[e];
     }
   }
   __syncthreads();
@@ -376,12 +382,13 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
   const size_t ustep = (size_t)stride * row;  // bytes between them
 
-  // LDS: rotated q (nq floats) and rotated new k (nkv floats) at 0 - with
+  // LDS: rotated q (nq floats), rotated new k and new v (nkv floats each) at 0 - with
   // STG, the waves' staging regions overlap them once q is in registers -
   // then the new K and V rows and the QK-RMSNorm scratch (n_heads floats).
   const LdsLayout ll = layer_lds_layout(P.sh, STG ? P.stage_rows : 0);
   float *qrot = reinterpret_cast<float *>(lds);
   float *kr = reinterpret_cast<float *>(lds + nq * 4);
+  float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
   uint8_t *rowk = lds + ll.rows;
   uint8_t *rowv = rowk + ll.row_pad;
   float *inv = reinterpret_cast<float *>(rowv + ll.row_pad);
@@ -416,9 +423,31 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         }
       }
     };
-    // Static schedule: the wave's first chunk is in flight during the setup.
+    // Per-lane loads (STG 0): trip tb is UP wave-steps at positions
+    // tb + u*stride + slot; positions past tend (and idle lanes) load row t0
+    // and are masked out of the softmax.  Two register sets: the next trip
+    // loads while the current one is consumed.  (F32 rows with 3 or 4 heads
+    // per group: one wave-step per trip, to stay within 256 VGPRs.)
+    constexpr int UP = (FMT == 0 && G >= 3) ? 1 : U;
+    [[maybe_unused]] typename C::Raw ka[UP], va[UP], kn[UP], vn[UP];
+    [[maybe_unused]] auto fetch = [&](int tb, typename C::Raw(&kk)[UP],
+                                      typename C::Raw(&vv)[UP]) {
+      const size_t base = (size_t)(tb + slot_ld) * row;
+#pragma unroll
+      for (int u = 0; u < UP; u++) {
+        size_t off = base + (size_t)u * ustep;
+        if (!(lane_on && tb + u * stride + slot < tend)) off = (size_t)t0 * row;
+        C::load(kk[u], kb + off, lo);
+        C::load(vv[u], vb + off, lo);
+      }
+    };
+    // Static schedule: the wave's first chunk or trip is in flight during
+    // the setup.
     if constexpr (STG == 2 && !WQ) {
       if (t0 + wave * P.stage_rows < tend) issue(t0 + wave * P.stage_rows);
+    }
+    if constexpr (STG == 0) {
+      if (t0 + wave * PPW < tend) fetch(t0 + wave * PPW, ka, va);
     }
     {
       // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by
@@ -443,7 +472,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     }
     if (owns_new)  // (its barriers also publish qrot)
       append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
-                     P.norm, kr, rowk, rowv, inv);
+                     P.norm, kr, vr, rowk, rowv, inv);
     else
       __syncthreads();
 
@@ -716,33 +745,24 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         }
       }
     } else {
-      // Per-lane loads: positions tb = t0 + wave*PPW + k*stride + slot.
-      auto trip = [&](int tb, auto check) {
-        constexpr bool CHECK = decltype(check)::value;
-        typename C::Raw krr[U], vrr[U];
-        bool valid[U];
-        int tpos[U];
-        const size_t base = (size_t)(tb + slot_ld) * row;
+      // Per-lane loads, one trip ahead (the first was issued before the setup).
+      auto pipe_step = [&](int tb, typename C::Raw(&kc)[UP], typename C::Raw(&vc)[UP],
+                           typename C::Raw(&kx)[UP], typename C::Raw(&vx)[UP]) {
+        if (tb + stride * UP < tend) fetch(tb + stride * UP, kx, vx);
+        bool valid[UP];
+        int tpos[UP];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-          size_t off = base + (size_t)u * ustep;
+        for (int u = 0; u < UP; u++) {
           tpos[u] = tb + u * stride + slot;
-          if constexpr (CHECK) {
-            valid[u] = lane_on && tpos[u] < tend;
-            if (!valid[u]) off = (size_t)t0 * row;
-          } else {
-            valid[u] = lane_on;
-          }
-          C::load(krr[u], kb + off, lo);
-          C::load(vrr[u], vb + off, lo);
+          valid[u] = lane_on && tpos[u] < tend;
         }
-        consume(krr, vrr, valid, tpos, std::integral_constant<int, U>{}, check);
+        consume(kc, vc, valid, tpos, std::integral_constant<int, UP>{}, std::true_type{});
       };
-      const int trip_span = (U - 1) * stride + PPW;  // positions one trip reaches past tb
-      int tb = t0 + wave * PPW;
-      if (tend > t0) {  // (a split of one position may hold only pos)
-        for (; tb + trip_span <= tend; tb += stride * U) trip(tb, std::false_type{});
-        for (; tb < tend; tb += stride * U) trip(tb, std::true_type{});
+      // (two steps per loop trip, so the register sets swap roles without copies)
+      for (int tb = t0 + wave * PPW; tb < tend; tb += 2 * stride * UP) {
+        pipe_step(tb, ka, va, kn, vn);
+        if (tb + stride * UP >= tend) break;
+        pipe_step(tb + stride * UP, kn, vn, ka, va);
       }
     }
     if (owns_new) {
