@@ -246,23 +246,25 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
 
-  // Work queue when every unit (sequence, layer) can have a resident
-  // workgroup and few enough waves share each unit's counters; otherwise
-  // static splits, sized so the launch's workgroups form whole rounds.
+  // Work queue (staged streaming) when few enough waves share each unit's
+  // counters - with more units (sequence, layer) than resident workgroups,
+  // the workgroups take the units in turn; otherwise static splits, sized
+  // so the launch's workgroups form whole rounds.
   const int64_t n_units = (int64_t)n_seq * n_layers;
   const int64_t wq_slots = fast && dp.stage_mode != 0 ? slots_for(c, dp, true) : 0;
-  const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 && n_units <= wq_slots &&
+  const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
                        wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
   const int64_t slots = use_wq ? wq_slots : slots_for(c, dp, false);
   int32_t max_splits;
   if (use_wq) {
-    if (n_units > c->wq_cap) {
+    const int64_t wq_lines = n_units + 1;  // the units and the next-unit counter
+    if (wq_lines > c->wq_cap) {
       G2B_HIP(c, hipStreamSynchronize(c->stream));
       if (c->wq) G2B_HIP(c, hipFree(c->wq));
       c->wq = nullptr;
       c->wq_cap = 0;
-      const int32_t cap = (int32_t)std::max<int64_t>(n_units, 256);
+      const int32_t cap = (int32_t)std::max<int64_t>(wq_lines, 256);
       const size_t bytes = (size_t)2 * cap * kWqStride * sizeof(int32_t);
       if (hipMalloc((void **)&c->wq, bytes) != hipSuccess) {
         c->wq = nullptr;
@@ -283,8 +285,13 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
         std::max<int64_t>(kWqMinParts, (slots + n_units - 1) / n_units + 8), 2048);
     const int32_t R = dp.stage_rows;
     const int64_t streamed = (total_pos - n_seq) * (int64_t)n_layers;  // positions [0, pos)
-    int64_t pl = c->tune_piece > 0 ? c->tune_piece
-                                   : streamed / (slots * kWavesPerSplit * kWqClaimsPerWave);
+    // (automatic: about kWqClaimsPerWave claims per wave of the grid; with
+    // more units than workgroups also at most 1/kWqUnitPieces of an average
+    // unit, so that a workgroup that has a unit to itself keeps its four
+    // waves evenly loaded)
+    int64_t pl = streamed / (slots * kWavesPerSplit * kWqClaimsPerWave);
+    if (n_units > slots) pl = std::min<int64_t>(pl, streamed / (n_units * kWqUnitPieces));
+    if (c->tune_piece > 0) pl = c->tune_piece;
     pl = std::min<int64_t>(std::max<int64_t>(pl, R), (int64_t)64 * R);
     dp.piece_len = (int32_t)(pl - pl % R);
     dp.piece_big = dp.piece_len * kWqBigFactor;
@@ -353,7 +360,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {
     // this launch dirtied its set; the combine zeroed the other one
-    c->wq_dirty[c->wq_set] = std::max<int32_t>(c->wq_dirty[c->wq_set], (int32_t)n_units);
+    c->wq_dirty[c->wq_set] = std::max<int32_t>(c->wq_dirty[c->wq_set], (int32_t)n_units + 1);
     c->wq_dirty[c->wq_set ^ 1] = 0;
     c->wq_set ^= 1;
     c->wq_reset = false;

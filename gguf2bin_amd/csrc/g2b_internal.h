@@ -99,8 +99,10 @@ struct DecodeParams {
   // Work-queue mode of k_layer (wq != nullptr; stage_mode 2 only): units are
   // (seq, layer) pairs, u = li*n_seq + seq.  wq holds two counter sets of
   // wq_cap units x kWqStride int32 each: [0] = pieces claimed, [1] = partial
-  // slots reserved.  The launch uses set wq_set; k_combine reads it and
-  // zeroes units [0, wq_zero_units) of the other set.
+  // slots reserved; line n_units holds the next never-assigned unit (used
+  // when the grid has fewer workgroups than units).  The launch uses set
+  // wq_set; k_combine reads it and zeroes lines [0, wq_zero_units) of the
+  // other set.
   int32_t *wq;
   int32_t wq_set, wq_cap, wq_zero_units;
   int32_t wq_grid;      // workgroups of the launch
@@ -112,6 +114,7 @@ constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte li
 constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit
 constexpr int kWqMinParts = 16;  // partial slots per unit at least
 constexpr int kWqClaimsPerWave = 64;   // automatic small piece: about this many per wave
+constexpr int kWqUnitPieces = 1024;    // automatic small piece: at most 1/this of a unit
 constexpr int kWqMaxWavesPerUnit = 64; // more waves per unit than this: static splits instead
 constexpr int kWqBigFactor = 8;        // big piece = this many small pieces
 constexpr int kWqTailDiv = 8;          // the last 1/kWqTailDiv of a unit goes in small pieces

@@ -340,10 +340,12 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
 // P.piece_len positions that the waves of every workgroup visiting the unit
 // claim one by one from the unit's counter (relaxed device-scope atomics,
 // one claim ahead), so workgroups on busier parts of the memory system take
-// fewer pieces.  A workgroup whose unit has no pieces left moves to another
-// unit with pieces left.  Each visit first reserves a partial slot from the
+// fewer pieces.  With more units than workgroups, a workgroup done with its
+// unit first takes the next never-assigned unit from a counter; after that,
+// a workgroup whose unit has no pieces left moves to another unit with
+// pieces left.  Each visit first reserves a partial slot from the
 // unit's slot counter; the visit that gets slot 0 appends and consumes pos.
-// At most P.max_splits visits per unit are admitted, and both counters only
+// At most P.max_splits visits per unit are admitted, and all counters only
 // grow, so every workgroup finishes.  k_combine reads the slot count and
 // zeroes the counter set of the next launch.
 // A merge of the partials inside this kernel (last workgroup of a unit by
@@ -856,6 +858,10 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     int32_t *const wq = P.wq + (size_t)P.wq_set * (size_t)P.wq_cap * kWqStride;
     int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)n_units));
     uint32_t probe = blockIdx.x * 2654435761u;  // where the next search starts
+    // More units than workgroups: units [gridDim.x, n_units) are handed out
+    // in order from the counter in line n_units before any search.
+    int32_t *const fresh = wq + (size_t)n_units * kWqStride;
+    bool fresh_left = (int)gridDim.x < n_units;
     for (;;) {
       int32_t *ctr = wq + (size_t)unit * kWqStride;
       if (threadIdx.x == 0)
@@ -867,6 +873,19 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         const int seq = unit % P.n_seq, li = unit / P.n_seq;
         const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
         visit(sd, seq, li, 0, sd.pos, pslot == 0, pslot, ctr);
+      }
+      if (fresh_left) {
+        if (threadIdx.x == 0)
+          s_bcast = (int)gridDim.x +
+                    __hip_atomic_fetch_add(fresh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int nu = __builtin_amdgcn_readfirstlane(s_bcast);
+        __syncthreads();
+        if (nu < n_units) {
+          unit = nu;
+          continue;
+        }
+        fresh_left = false;
       }
       // Next unit: one with at least kWqStealMin unclaimed pieces and a free
       // partial slot, searched by wave 0 from a per-workgroup offset.

@@ -126,6 +126,37 @@ def test_codec_special_rows_on_device(gpu_device):
     assert np.array_equal(kv_rows(o, kc, n, n), kv_rows(o, okc, n, n))
 
 
+@pytest.mark.parametrize("heads", [(2, 1, 64), (16, 8, 128)])
+def test_codec_special_rows_through_decode(gpu_device, heads):
+    """The same quantiser branches through the append of a decode step (the
+    new row that the attention kernel itself quantises, four lanes per
+    block): row t of the special rows, tiled (and rolled) across nkv, is the
+    new k and v at pos t.  K and V bytes must equal the oracle's (reference
+    quantiser; K after RoPE at t)."""
+    rows = q8_special_rows()
+    nh, nkvh, hd = heads
+    o = orc.Shape(1, nh, nkvh, hd, 1e4, orc.ARCH_QWEN3, True)
+    n, nkv = rows.shape[0], o.nkv
+    tiled = np.stack([np.roll(np.tile(rows[t], nkv // 64), 7 * t) for t in range(n)])
+    tiled = tiled.astype(np.float32)
+    rng = np.random.default_rng(11)
+    print(f"[codec-decode] shape={o} rows={n}", flush=True)
+    with attn.Context(ashape(o)) as ctx:
+        seq = DevSeq(ctx, o, n)
+        try:
+            for t in range(n):
+                q = rng.standard_normal(o.nq).astype(np.float32)
+                ctx.attn_forward_host(0, t, n, seq.k, seq.v, q, tiled[t], tiled[t])
+            kc, vc = seq.download()
+        finally:
+            seq.free()
+    okc, ovc = orc.alloc_kv(o, n)
+    for t in range(n):
+        orc.kv_prefill(o, n, 0, t, okc, ovc, tiled[t:t + 1], tiled[t:t + 1])
+    assert np.array_equal(kv_rows(o, vc, n, n), kv_rows(o, ovc, n, n))
+    assert np.array_equal(kv_rows(o, kc, n, n), kv_rows(o, okc, n, n))
+
+
 # ---------------------------------------------------------------- oracle comparisons
 
 SHAPES = {
@@ -308,6 +339,19 @@ def test_many_splits_single_sequence(gpu_device, q8, mode):
     print(f"[splits] q8={q8} mode={mode}", flush=True)
     run_batch_case(o, [6000], [5999], seed=77, fused=False,
                    tune=(0, 0, 2, 12) if mode == "wq" else None)
+
+
+@pytest.mark.parametrize("piece", [0, 8])
+def test_work_queue_more_units_than_workgroups(gpu_device, piece):
+    """One call over 24 layers x 32 ragged sequences (768 units, more than
+    the resident workgroups of the work-queue grid): workgroups take the
+    never-assigned units from the counter in turn, then steal pieces."""
+    o = orc.Shape(24, 16, 8, 128, 1e6, orc.ARCH_QWEN3, True)
+    rng = np.random.default_rng(41 + piece)
+    poss = [int(x) for x in rng.integers(40, 200, 32)]
+    caps = [p + 1 + int(x) for p, x in zip(poss, rng.integers(0, 5, 32))]
+    print(f"[wq-units] piece={piece} units={o.n_layers * len(poss)}", flush=True)
+    run_batch_case(o, caps, poss, 2600 + piece, fused=True, tune=(0, 0, 2, piece))
 
 
 def test_work_queue_counters_across_calls(gpu_device):
