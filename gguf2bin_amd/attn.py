@@ -29,6 +29,7 @@ EXPORTS = [
     "g2b_ctx_create", "g2b_ctx_destroy", "g2b_ctx_set_stream", "g2b_ctx_stream",
     "g2b_strerror", "g2b_ctx_last_error", "g2b_kv_row_bytes", "g2b_kv_bytes",
     "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows", "g2b_set_qk_norm",
+    "g2b_model_kv_bytes", "g2b_clamp_ctx", "g2b_hbm_bytes", "g2b_auto_budget", "g2b_hbm_info",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
@@ -100,6 +101,12 @@ def lib() -> C.CDLL:
             "g2b_kv_row_bytes": ([C.POINTER(_Shape)], C.c_size_t),
             "g2b_kv_bytes": ([C.POINTER(_Shape), i32], u64),
             "g2b_kv_offset": ([C.POINTER(_Shape), i32, i32, i32], u64),
+            "g2b_model_kv_bytes": ([C.POINTER(_Shape), i32, i32], u64),
+            "g2b_clamp_ctx": ([i32, i32], i32),
+            "g2b_hbm_bytes": ([C.POINTER(_Shape), i32, i32, i32], u64),
+            "g2b_auto_budget": ([C.POINTER(_Shape), i32, i32, u64, C.POINTER(i32),
+                                 C.POINTER(i32)], C.c_int),
+            "g2b_hbm_info": ([vp, C.POINTER(u64), C.POINTER(u64)], C.c_int),
             "g2b_kv_alloc": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], C.c_int),
             "g2b_kv_free": ([vp, vp, vp], C.c_int),
             "g2b_kv_append_rows": ([vp, vp, vp, i32, i32, i32, i32, fp, fp], C.c_int),
@@ -142,6 +149,32 @@ def kv_bytes(shape: Shape, ctx_cap: int) -> int:
 
 def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
     return int(lib().g2b_kv_offset(C.byref(shape.c()), ctx_cap, layer, pos))
+
+
+def model_kv_bytes(shape: Shape, seq_len: int, kv_q8: bool) -> int:
+    """model_kv_bytes (l5_model.c:195-203): K+V bytes at the full seq_len."""
+    return int(lib().g2b_model_kv_bytes(C.byref(shape.c()), seq_len, 1 if kv_q8 else 0))
+
+
+def clamp_ctx(ctx: int, seq_len: int) -> int:
+    """model_set_ctx's clamp (l5_model.c:166-169)."""
+    return int(lib().g2b_clamp_ctx(ctx, seq_len))
+
+
+def hbm_bytes(shape: Shape, ctx: int, kv_q8: bool, n_seq: int) -> int:
+    """HBM of n_seq sequences at context ctx: KV, RoPE table, partial scratch."""
+    return int(lib().g2b_hbm_bytes(C.byref(shape.c()), ctx, 1 if kv_q8 else 0, n_seq))
+
+
+def auto_budget(shape: Shape, seq_len: int, n_seq: int, budget: int):
+    """model_auto_budget (l5_model.c:218-230) against an HBM budget.
+    Returns (kv_q8, ctx, fits); raises G2BError for invalid arguments."""
+    q8, ctx = C.c_int32(), C.c_int32()
+    rc = lib().g2b_auto_budget(C.byref(shape.c()), seq_len, n_seq, budget, C.byref(q8),
+                               C.byref(ctx))
+    if rc not in (G2B_OK, G2B_ENOMEM):
+        raise G2BError(rc, f"g2b_auto_budget: {strerror(rc)}")
+    return bool(q8.value), int(ctx.value), rc == G2B_OK
 
 
 def rope_table(pos0: int, n_pos: int, head_dim: int, theta: float) -> np.ndarray:
@@ -198,6 +231,12 @@ class Context:
 
     def sync(self):
         self._check(lib().g2b_sync(self.h), "g2b_sync")
+
+    def hbm_info(self):
+        """(free, total) HBM bytes of the context's device."""
+        fr, tot = C.c_uint64(), C.c_uint64()
+        self._check(lib().g2b_hbm_info(self.h, C.byref(fr), C.byref(tot)), "g2b_hbm_info")
+        return int(fr.value), int(tot.value)
 
     # ---- KV (alloc_rt / free_rt) ----
     def kv_alloc(self, ctx_cap: int):

@@ -693,6 +693,16 @@ int g2b_sync(g2b_ctx *c) {
   return G2B_OK;
 }
 
+int g2b_hbm_info(g2b_ctx *c, uint64_t *free_bytes, uint64_t *total_bytes) {
+  if (!c || !free_bytes || !total_bytes) return fail(c, G2B_EINVAL, "bad hbm_info arguments");
+  if (int rc = set_device(c)) return rc;
+  size_t fr = 0, tot = 0;
+  G2B_HIP(c, hipMemGetInfo(&fr, &tot));
+  *free_bytes = fr;
+  *total_bytes = tot;
+  return G2B_OK;
+}
+
 int g2b_synth_normal(g2b_ctx *c, float *out, uint64_t n, uint64_t seed) {
   if (!c || (!out && n)) return fail(c, G2B_EINVAL, "bad synth_normal arguments");
   if (int rc = set_device(c)) return rc;

@@ -1,0 +1,69 @@
+/*
+ * g2b_budget.c - HBM budgeting of the KV caches, C99, host only.
+ *
+ * The reference sizes its runtime for a RAM budget:
+ *   - model_kv_bytes (/root/reference/src/l5_model.c:195-203): K+V bytes at
+ *     the model's full seq_len in a given KV mode;
+ *   - est_for (:174-187): the resident runtime, KV plus host buffers and the
+ *     tokenizer;
+ *   - model_auto_budget (:218-230): first switch the KV to Q8_0 if F32 at the
+ *     starting context does not fit, then halve ctx (integer halving, not
+ *     below 256) while the estimate exceeds the budget, then model_set_ctx,
+ *     whose clamp (:166-169) maps ctx <= 0 to 256 and caps it at seq_len.
+ * Here the same decision is taken against an HBM budget for n_seq sequences
+ * of one shape (one Model each).  What lives in HBM is their KV caches and
+ * the decode path's scratch (g2b_hbm_bytes); the reference's host buffers,
+ * tokenizer and weights are not part of it.
+ */
+#include "g2b_attn.h"
+
+/* kv_q8_rowsize (l5_model.c:47) or nkv*4, for the given mode. */
+static uint64_t row_bytes_mode(const g2b_shape *s, int32_t kv_q8) {
+  const uint64_t nkv = (uint64_t)s->n_kv_heads * (uint64_t)s->head_dim;
+  return kv_q8 ? (nkv + 31u) / 32u * 34u : nkv * 4u;
+}
+
+static int shape_ok(const g2b_shape *s) {
+  return s && s->n_layers > 0 && s->n_heads > 0 && s->n_kv_heads > 0 && s->head_dim > 0;
+}
+
+uint64_t g2b_model_kv_bytes(const g2b_shape *s, int32_t seq_len, int32_t kv_q8) {
+  if (!shape_ok(s) || seq_len <= 0) return 0;
+  return 2u * (uint64_t)s->n_layers * (uint64_t)seq_len * row_bytes_mode(s, kv_q8);
+}
+
+int32_t g2b_clamp_ctx(int32_t ctx, int32_t seq_len) {
+  if (ctx <= 0) ctx = 256;
+  if (seq_len > 0 && ctx > seq_len) ctx = seq_len;
+  return ctx;
+}
+
+/* Upper bound of the split partials a one-layer call allocates: partial
+ * slots for max(2048, 64 * n_seq) splits, each (4 + head_dim) floats per q
+ * head (running max, sum, two pad floats, accumulator). */
+static uint64_t scratch_bytes(const g2b_shape *s, int32_t n_seq) {
+  uint64_t splits = 64u * (uint64_t)n_seq;
+  if (splits < 2048u) splits = 2048u;
+  return splits * (uint64_t)s->n_heads * (4u + (uint64_t)s->head_dim) * 4u;
+}
+
+uint64_t g2b_hbm_bytes(const g2b_shape *s, int32_t ctx, int32_t kv_q8, int32_t n_seq) {
+  if (!shape_ok(s) || ctx <= 0 || n_seq < 1) return 0;
+  const uint64_t kv = (uint64_t)n_seq * 2u * (uint64_t)s->n_layers * (uint64_t)ctx *
+                      row_bytes_mode(s, kv_q8);
+  const uint64_t rope = (uint64_t)ctx * (uint64_t)s->head_dim * 4u;
+  return kv + rope + scratch_bytes(s, n_seq);
+}
+
+int g2b_auto_budget(const g2b_shape *s, int32_t seq_len, int32_t n_seq, uint64_t budget,
+                    int32_t *kv_q8, int32_t *ctx_out) {
+  if (!shape_ok(s) || !budget || n_seq < 1 || !kv_q8 || !ctx_out) return G2B_EINVAL;
+  int32_t q8 = s->kv_q8 ? 1 : 0;
+  int32_t ctx = seq_len > 0 ? seq_len : 2048;
+  if (!q8 && g2b_hbm_bytes(s, ctx, 0, n_seq) > budget) q8 = 1;
+  while (ctx > 256 && g2b_hbm_bytes(s, ctx, q8, n_seq) > budget) ctx /= 2;
+  const int fits = g2b_hbm_bytes(s, ctx, q8, n_seq) <= budget;
+  *kv_q8 = q8;
+  *ctx_out = g2b_clamp_ctx(ctx, seq_len);
+  return fits ? G2B_OK : G2B_ENOMEM;
+}

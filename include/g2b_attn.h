@@ -95,6 +95,35 @@ uint64_t g2b_kv_bytes(const g2b_shape *shape, int32_t ctx_cap);
 /* Byte offset of (layer, pos) inside one cache (l5_model.c:232-234,239-240). */
 uint64_t g2b_kv_offset(const g2b_shape *shape, int32_t ctx_cap, int32_t layer, int32_t pos);
 
+/* HBM budgeting (host arithmetic; no device needed).
+ * g2b_model_kv_bytes: model_kv_bytes (l5_model.c:195-203), K+V bytes of one
+ *   sequence at the full seq_len in the given mode (0 when seq_len <= 0).
+ * g2b_clamp_ctx: model_set_ctx's clamp (l5_model.c:166-169): ctx <= 0 -> 256,
+ *   then at most seq_len when seq_len > 0.
+ * g2b_hbm_bytes: HBM that n_seq sequences of the shape at context ctx take on
+ *   the device - their K and V caches, the RoPE table (ctx*head_dim floats)
+ *   and an upper bound of the split partials of a one-layer call
+ *   (max(2048, 64*n_seq) splits x n_heads x (4+head_dim) floats).  Takes the
+ *   place of est_for (l5_model.c:174-187), whose host buffers and tokenizer
+ *   are not in HBM.  0 for a bad shape, ctx <= 0 or n_seq < 1.
+ * g2b_auto_budget: model_auto_budget (l5_model.c:218-230) against an HBM
+ *   budget for n_seq sequences: starting from kv_q8 = shape->kv_q8 and
+ *   ctx = seq_len (2048 when seq_len <= 0), switch to Q8_0 if F32 does not
+ *   fit, halve ctx (integer halving) while ctx > 256 and it does not fit, and
+ *   clamp as g2b_clamp_ctx.  Writes the chosen mode and context; returns
+ *   G2B_OK when g2b_hbm_bytes fits the budget, G2B_ENOMEM when even the
+ *   smallest context tried does not (where the reference prints a warning and
+ *   goes on), G2B_EINVAL for a bad shape, budget 0, n_seq < 1 or null outputs
+ *   (the reference returns -1 for budget 0 or no layers). */
+uint64_t g2b_model_kv_bytes(const g2b_shape *shape, int32_t seq_len, int32_t kv_q8);
+int32_t g2b_clamp_ctx(int32_t ctx, int32_t seq_len);
+uint64_t g2b_hbm_bytes(const g2b_shape *shape, int32_t ctx, int32_t kv_q8, int32_t n_seq);
+int g2b_auto_budget(const g2b_shape *shape, int32_t seq_len, int32_t n_seq, uint64_t budget,
+                    int32_t *kv_q8, int32_t *ctx);
+/* Free and total HBM of the context's device (hipMemGetInfo), e.g. as the
+ * budget of g2b_auto_budget. */
+int g2b_hbm_info(g2b_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes);
+
 /* alloc_rt's KV half (l5_model.c:141-147) in HBM: two zeroed device buffers
  * of g2b_kv_bytes(ctx_cap) each.  Also extends the context's RoPE table to
  * ctx_cap positions.  ctx_cap must be >= 1 (model_set_ctx clamps before

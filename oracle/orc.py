@@ -256,6 +256,44 @@ def attn_batch(shape: Shape, layer0: int, n_layers: int, pos: np.ndarray,
     return qo
 
 
+# ---------------------------------------------------------------- budgeting
+# Pure-Python restatements (small integer arithmetic).
+
+
+def est_for_ram(dim: int, hid: int, n_layers: int, n_heads: int, n_kv_heads: int, vocab: int,
+                head_dim: int, ctx: int, q8: int) -> int:
+    """est_for (l5_model.c:174-187) of a Model without tokenizer: K and V at
+    ctx positions (kv_q8_rowsize or nkv*4 per row) plus the f32 runtime
+    buffer of alloc_rt (:124-125)."""
+    nkv = n_kv_heads * head_dim
+    row = (nkv + 31) // 32 * 34 if q8 else nkv * 4
+    kv = 2 * n_layers * ctx * row
+    maxn = dim if dim > hid else hid
+    if vocab > maxn:
+        maxn = vocab
+    nbuf = dim * 3 + hid * 2 + n_heads * head_dim + nkv * 2 + n_heads * ctx + maxn
+    return kv + nbuf * 4
+
+
+def auto_budget(est, seq_len: int, q8: int, budget: int):
+    """model_auto_budget (l5_model.c:218-230) followed by model_set_ctx's
+    clamp (:166-169), for an estimator est(ctx, q8).  Returns (ctx, q8,
+    fits): Q8_0 first if F32 at the starting context does not fit, then
+    integer halving while ctx > 256 and the estimate exceeds the budget."""
+    q8 = 1 if q8 else 0
+    ctx = seq_len if seq_len > 0 else 2048
+    if not q8 and est(ctx, 0) > budget:
+        q8 = 1
+    while ctx > 256 and est(ctx, q8) > budget:
+        ctx //= 2
+    fits = est(ctx, q8) <= budget
+    if ctx <= 0:
+        ctx = 256
+    if seq_len > 0 and ctx > seq_len:
+        ctx = seq_len
+    return ctx, q8, fits
+
+
 def now() -> float:
     return lib().orc_now_sec()
 
@@ -297,6 +335,11 @@ def ref_lib(variant: str = "avx2"):
                                        _vp, _vp, C.c_float,
                                        _f32p, _f32p, _f32p, _u8p, _u8p]
     L.ref_forward_case_qkn.restype = C.c_int
+    L.ref_est_for.argtypes = [C.c_int32] * 9 + [C.c_int]
+    L.ref_est_for.restype = C.c_uint64
+    L.ref_auto_budget.argtypes = ([C.c_int32] * 8 + [C.c_int, C.c_uint64,
+                                  C.POINTER(C.c_int32), C.POINTER(C.c_int32)])
+    L.ref_auto_budget.restype = C.c_int
     _ref[variant] = L
     return L
 

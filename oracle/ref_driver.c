@@ -184,3 +184,42 @@ int ref_forward_case(i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 head_dim, f3
                               ctx_cap, n_pre, k_pre, v_pre, n_fwd, x_rows, NULL, NULL, 1e-6f,
                               xb_out, out_per_step, att_out, kc_out, vc_out);
 }
+
+/* The reference's RAM budgeting on an in-memory Model with the given config
+ * (no tokenizer, no weights): est_for (l5_model.c:174-187) and
+ * model_auto_budget (:218-230), which allocates the runtime through
+ * model_set_ctx; the chosen context and KV mode are read back and the
+ * runtime is freed. */
+static void budget_model(Model *m, i32 dim, i32 hid, i32 n_layers, i32 n_heads, i32 n_kv_heads,
+                         i32 vocab, i32 seq_len, i32 head_dim, int q8) {
+  memset(m, 0, sizeof *m);
+  m->c.dim = dim;
+  m->c.hidden_dim = hid;
+  m->c.n_layers = n_layers;
+  m->c.n_heads = n_heads;
+  m->c.n_kv_heads = n_kv_heads;
+  m->c.vocab = vocab;
+  m->c.seq_len = seq_len;
+  m->c.head_dim = head_dim;
+  m->flags = q8 ? F_KV_Q8 : 0;
+#if !defined(_WIN32)
+  m->fd = -1;
+  m->swap_fd = -1;
+#endif
+}
+u64 ref_est_for(i32 dim, i32 hid, i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 vocab,
+                i32 seq_len, i32 head_dim, i32 ctx, int q8) {
+  Model m;
+  budget_model(&m, dim, hid, n_layers, n_heads, n_kv_heads, vocab, seq_len, head_dim, q8);
+  return est_for(&m, ctx, q8);
+}
+int ref_auto_budget(i32 dim, i32 hid, i32 n_layers, i32 n_heads, i32 n_kv_heads, i32 vocab,
+                    i32 seq_len, i32 head_dim, int q8, u64 max_ram, i32 *ctx_out, i32 *q8_out) {
+  Model m;
+  budget_model(&m, dim, hid, n_layers, n_heads, n_kv_heads, vocab, seq_len, head_dim, q8);
+  const int rc = model_auto_budget(&m, max_ram);
+  *ctx_out = m.ctx;
+  *q8_out = (m.flags & F_KV_Q8) ? 1 : 0;
+  free_rt(&m);
+  return rc;
+}

@@ -492,3 +492,19 @@ def test_synth_fill_matches_host_stream(gpu_device):
     # double-precision log/cos/sin on the device may differ from glibc in the
     # last bit; after rounding to float that flips a value at most rarely
     assert mism <= 4, f"{mism} bytes differ"
+
+
+def test_hbm_info_as_budget(gpu_device):
+    """g2b_hbm_info reports the device's HBM, and g2b_auto_budget against the
+    free HBM picks a plan whose KV then allocates (one sequence, c4 shape)."""
+    s = attn.Shape(28, 16, 8, 128, 1e6, attn.ARCH_QWEN3, False)
+    with attn.Context(s) as ctx:
+        free, total = ctx.hbm_info()
+        print(f"[hbm] free={free} total={total}", flush=True)
+        assert 0 < free <= total
+        q8, c, fits = attn.auto_budget(s, 40960, 1, free // 4)
+        assert fits and c == 40960 and not q8  # 9.4 GB of F32 KV fits a quarter of HBM
+        q8, c, fits = attn.auto_budget(s, 40960, 256, free // 4)
+        assert fits and q8 and c < 40960  # 256 sequences need Q8_0 and a shorter context
+        k, v = ctx.kv_alloc(c)
+        ctx.kv_free(k, v)
