@@ -222,6 +222,7 @@ def main():
     ap.add_argument("--seed", type=int, default=20241201)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-fused", action="store_true", help="skip the all-layers-in-one-call run")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the weight-GEMV measurement")
     ap.add_argument("--no-others", action="store_true",
                     help="skip the other BASELINE configs (reported under all_configs)")
     ap.add_argument("--cpu-seq-a", type=int, default=4, help="sequences in the 1-thread sample")
@@ -327,6 +328,8 @@ def main():
                 f"all layers in one call {others[name]['all_layers_one_call_us_per_step']} us/step")
             o.close()
 
+    gemv = None if args.no_gemv else gemv_leg(args)
+
     traffic = load_traffic(args.config)
     roof = {"bound": "hbm", "kernel": "k_layer", "achieved": round(dec_gbps, 2),
             "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
@@ -355,8 +358,74 @@ def main():
         "all_layers_one_call": fused,
         "parity_full_size": parity,
         "all_configs": others,
+        "gemv": gemv,
     }
     print(json.dumps(line), flush=True)
+
+
+def gemv_leg(args):
+    """Device weight GEMVs (g2b_matmul, matmul_q of l2_codec.c:342-360) on
+    Qwen3-0.6B's output projection (vocab 151936 x dim 1024), the largest
+    single matmul_q call of a decode step: weight GB/s of each fused type,
+    with the reference's own AVX2+OpenMP matmul (compiled reference, when it
+    was built; else the oracle's scalar restatement on one thread) timed on
+    the host cores as the CPU baseline, and a row sample checked against the
+    float64 product."""
+    from oracle import orc  # CPU baseline and checker only
+
+    n, d = 1024, 151936
+    rng = np.random.default_rng(args.seed + 7)
+    ctx = attn.Context(attn.Shape(1, 2, 1, 64, 1e4, attn.ARCH_QWEN3, False))
+    x = rng.standard_normal(n).astype(np.float32)
+    xd = hip.to_device(x)
+    od = hip.DeviceBuffer(d * 4)
+    res = {"workload": f"Qwen3-0.6B output projection: d={d} rows x n={n}, x ~ N(0,1)",
+           "unit": "GB/s of weight bytes"}
+    ref = orc.ref_lib("avx2")
+    for t, name in ((attn.T_Q8_0, "q8_0"), (attn.T_Q4_0, "q4_0"), (attn.T_F32, "f32")):
+        w = orc.random_weights(rng, t, n, d)
+        wd = ctx.weights_upload(w)
+        for _ in range(3):
+            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+        ctx.sync()
+        e0, e1 = hip.Event(), hip.Event()
+        K = max(20, args.steps * 5)
+        e0.record(ctx.stream)
+        for _ in range(K):
+            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+        e1.record(ctx.stream)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) / K * 1e3
+        out = od.download(np.float32, d)
+        ctx.weights_free(wd)
+        rows = np.sort(rng.choice(d, 4096, replace=False))
+        wr = w.reshape(d, -1)[rows].reshape(-1)
+        ex, ab = orc.matmul_exact(x, wr, t, n, len(rows))
+        rel = float(np.max(np.abs(out[rows] - ex) / ab))
+        # CPU baseline: whole matrix, repeated for about a second
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            if ref is not None:
+                orc.ref_matmul(x, w, t, n, d, "avx2")
+            else:
+                orc.matmul_scalar(x, w, t, n, d)
+            reps += 1
+            if time.perf_counter() - t0 >= 1.0:
+                break
+        cpu_s = (time.perf_counter() - t0) / reps
+        res[name] = {"us": round(us, 2), "GBps": round(w.nbytes / us / 1e3, 1),
+                     "pct_hbm_peak": round(100 * w.nbytes / us / 1e3 / HBM_PEAK_GBPS, 1),
+                     "weight_bytes": int(w.nbytes),
+                     "max_err_over_sum_abs": rel,
+                     "cpu_GBps": round(w.nbytes / cpu_s / 1e9, 2),
+                     "cpu_kind": ("reference matmul (AVX2, OpenMP)" if ref is not None
+                                  else "oracle scalar restatement, 1 thread"),
+                     "cpu_threads": orc.max_threads() if ref is not None else 1}
+        log(f"gemv {name}: {us:.1f} us, {res[name]['GBps']} GB/s "
+            f"({res[name]['pct_hbm_peak']}% of HBM peak), err/sum|wx| {rel:.1e}, "
+            f"cpu {res[name]['cpu_GBps']} GB/s")
+    ctx.close()
+    return res
 
 
 def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):

@@ -30,6 +30,8 @@ EXPORTS = [
     "g2b_strerror", "g2b_ctx_last_error", "g2b_kv_row_bytes", "g2b_kv_bytes",
     "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows", "g2b_set_qk_norm",
     "g2b_model_kv_bytes", "g2b_clamp_ctx", "g2b_hbm_bytes", "g2b_auto_budget", "g2b_hbm_info",
+    "g2b_matmul_row_bytes", "g2b_matmul", "g2b_matmul_host", "g2b_weights_upload",
+    "g2b_weights_free",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
@@ -107,6 +109,11 @@ def lib() -> C.CDLL:
             "g2b_auto_budget": ([C.POINTER(_Shape), i32, i32, u64, C.POINTER(i32),
                                  C.POINTER(i32)], C.c_int),
             "g2b_hbm_info": ([vp, C.POINTER(u64), C.POINTER(u64)], C.c_int),
+            "g2b_matmul_row_bytes": ([i32, i32], C.c_size_t),
+            "g2b_matmul": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
+            "g2b_matmul_host": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
+            "g2b_weights_upload": ([vp, vp, u64, C.POINTER(vp)], C.c_int),
+            "g2b_weights_free": ([vp, vp], C.c_int),
             "g2b_kv_alloc": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], C.c_int),
             "g2b_kv_free": ([vp, vp, vp], C.c_int),
             "g2b_kv_append_rows": ([vp, vp, vp, i32, i32, i32, i32, fp, fp], C.c_int),
@@ -149,6 +156,14 @@ def kv_bytes(shape: Shape, ctx_cap: int) -> int:
 
 def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
     return int(lib().g2b_kv_offset(C.byref(shape.c()), ctx_cap, layer, pos))
+
+
+T_F32, T_Q4_0, T_Q8_0 = 0, 2, 8  # GGML type ids of the device GEMVs
+
+
+def matmul_row_bytes(t: int, n: int) -> int:
+    """Bytes of one weight row (row_stride, l2_codec.c:340)."""
+    return int(lib().g2b_matmul_row_bytes(t, n))
 
 
 def model_kv_bytes(shape: Shape, seq_len: int, kv_q8: bool) -> int:
@@ -231,6 +246,30 @@ class Context:
 
     def sync(self):
         self._check(lib().g2b_sync(self.h), "g2b_sync")
+
+    # ---- weight GEMVs (matmul_q, l2_codec.c:342-360) ----
+    def weights_upload(self, host: np.ndarray) -> int:
+        """Copy a host byte array into HBM; returns the device pointer."""
+        h = np.ascontiguousarray(host).view(np.uint8)
+        dev = C.c_void_p()
+        self._check(lib().g2b_weights_upload(self.h, h.ctypes.data, h.nbytes, C.byref(dev)),
+                     "g2b_weights_upload")
+        return int(dev.value)
+
+    def weights_free(self, dev: int):
+        self._check(lib().g2b_weights_free(self.h, dev), "g2b_weights_free")
+
+    def matmul(self, out: int, x: int, w: int, t: int, n: int, d: int):
+        """Device pointers; asynchronous on the context's stream."""
+        self._check(lib().g2b_matmul(self.h, out, x, w, t, n, d), "g2b_matmul")
+
+    def matmul_host(self, x: np.ndarray, w: int, t: int, n: int, d: int) -> np.ndarray:
+        """x in host memory, w a device pointer; returns out (host)."""
+        out = np.zeros(max(d, 1), np.float32)
+        xx = np.ascontiguousarray(x, np.float32)
+        self._check(lib().g2b_matmul_host(self.h, out.ctypes.data, xx.ctypes.data, w, t, n, d),
+                     "g2b_matmul_host")
+        return out[:d]
 
     def hbm_info(self):
         """(free, total) HBM bytes of the context's device."""

@@ -17,6 +17,7 @@
 
 #include "g2b_attn.h"
 #include "g2b_internal.h"
+#include "g2b_matmul.h"
 #include "g2b_synth.h"
 
 using namespace g2b;
@@ -690,6 +691,86 @@ int g2b_sync(g2b_ctx *c) {
   if (!c) return G2B_EINVAL;
   if (int rc = set_device(c)) return rc;
   G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
+size_t g2b_matmul_row_bytes(int32_t type, int32_t n) {
+  if (n < 0) return 0;
+  switch (type) {
+    case G2B_T_F32: return (size_t)n * 4u;
+    case G2B_T_Q8_0: return (size_t)(n / 32) * 34u;
+    case G2B_T_Q4_0: return (size_t)(n / 32) * 18u;
+    default: return 0;
+  }
+}
+
+int g2b_matmul(g2b_ctx *c, float *out, const float *x, const void *w, int32_t type, int32_t n,
+               int32_t d) {
+  if (!c) return G2B_EINVAL;
+  if (type != G2B_T_F32 && type != G2B_T_Q8_0 && type != G2B_T_Q4_0)
+    return fail(c, G2B_EUNSUP, "weight type %d has no device GEMV", type);
+  if (int rc = set_device(c)) return rc;
+  if (!out || !x || !w || n <= 0 || d <= 0) {  // matmul_q's guard (l2_codec.c:343-346)
+    if (out && d > 0) G2B_HIP(c, launch_fill_zero(out, d, c->stream));
+    return G2B_OK;
+  }
+  if (((uintptr_t)w & 1u) && type != G2B_T_F32)
+    return fail(c, G2B_EINVAL, "quantised weights must be 2-byte aligned");
+  if (((uintptr_t)w & 3u) && type == G2B_T_F32)
+    return fail(c, G2B_EINVAL, "F32 weights must be 4-byte aligned");
+  GemvParams p{};
+  p.out = out;
+  p.x = x;
+  p.w = (const uint8_t *)w;
+  p.n = n;
+  p.d = d;
+  p.x_vec4 = ((uintptr_t)x & 15u) == 0;
+  G2B_HIP(c, launch_gemv(p, type, c->n_cu, c->stream));
+  return G2B_OK;
+}
+
+int g2b_matmul_host(g2b_ctx *c, float *out, const float *x, const void *w, int32_t type,
+                    int32_t n, int32_t d) {
+  if (!c) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  if (!out || d <= 0) return g2b_matmul(c, nullptr, nullptr, nullptr, type, 0, 0);
+  const size_t nx = (x && w && n > 0) ? (size_t)n : 0;
+  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nx + (size_t)d + 4)) return rc;
+  float *dx = c->hstage, *dout = dx + ((nx + 3) & ~(size_t)3);
+  if (nx) G2B_HIP(c, hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, c->stream));
+  if (int rc = g2b_matmul(c, dout, nx ? dx : nullptr, w, type, n, d)) return rc;
+  G2B_HIP(c, hipMemcpyAsync(out, dout, (size_t)d * 4, hipMemcpyDeviceToHost, c->stream));
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
+int g2b_weights_upload(g2b_ctx *c, const void *host, uint64_t bytes, void **dev) {
+  if (!c || !dev || bytes == 0) return fail(c, G2B_EINVAL, "bad weights_upload arguments");
+  *dev = nullptr;
+  if (int rc = set_device(c)) return rc;
+  void *p = nullptr;
+  if (hipMalloc(&p, (size_t)bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(c, G2B_ENOMEM, "hipMalloc of %llu weight bytes failed",
+                (unsigned long long)bytes);
+  }
+  if (host) {
+    const hipError_t e = hipMemcpy(p, host, (size_t)bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return fail(c, G2B_EDEVICE, "weight upload: %s", hipGetErrorString(e));
+    }
+  }
+  *dev = p;
+  return G2B_OK;
+}
+
+int g2b_weights_free(g2b_ctx *c, void *dev) {
+  if (!c) return G2B_EINVAL;
+  if (!dev) return G2B_OK;
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  G2B_HIP(c, hipFree(dev));
   return G2B_OK;
 }
 

@@ -180,6 +180,24 @@ template <int FMT, int HD, int G>
 int layer_occupancy(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
                     int32_t stage_rows, bool wq);
 
+// Device GEMVs (g2b_matmul.hip) for matmul_q's fused types (GGML type ids,
+// /root/reference/include/g2b.h:13-14).
+constexpr int32_t kTypeF32 = 0, kTypeQ4_0 = 2, kTypeQ8_0 = 8;
+struct GemvParams {
+  float *out;          // [d]
+  const float *x;      // [n]
+  const uint8_t *w;    // d rows of row_bytes
+  int32_t n, d;
+  int32_t nb;          // blocks per row (Q8_0 / Q4_0: n/32)
+  uint32_t row_bytes;
+  int32_t steps;       // wave-steps over the rows
+  int32_t n_waves;     // waves of the launch
+  int32_t vec4;        // F32: 16-byte loads allowed
+  int32_t x_vec4;      // Q8_0 / Q4_0: x 16-byte aligned (x kept in registers)
+};
+hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s);
+hipError_t launch_fill_zero(float *out, int32_t n, hipStream_t s);
+
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {
   ShapeDev sh;

@@ -1,0 +1,441 @@
+// g2b_matmul.hip - device GEMVs of gguf2bin2's fused weight types:
+// matmul_q8_0 / matmul_q4_0 (/root/reference/src/l2_codec.c:203-340) and
+// the F32 matmul (src/l3_math.c:17-20), dispatched as matmul_q does
+// (l2_codec.c:342-349): out[i] = sum_j W[i][j] * x[j], i < d.
+//
+// Weight rows are streamed once per call (HBM-bound: 1.0625 B per weight for
+// Q8_0, 0.5625 B for Q4_0, 4 B for F32).  Q8_0 / Q4_0: a row of nb = n/32
+// blocks is spread over LPR lanes (LPR = nb rounded up to a power of two, at
+// most 64), lane c taking blocks c, c + LPR, ...; a wave covers 64/LPR rows
+// per step, so one step reads a contiguous run of whole rows.  Each lane
+// keeps the x values of its blocks in registers (up to two blocks; more are
+// read through the cache) and loads its blocks as dwords from the dword
+// boundary at or before the block (blocks are 2-byte aligned), extracting
+// the bytes with v_perm.  Arithmetic is fp32 like the reference: per block
+// sum_j q_j x_j by FMA, times the fp16 scale, summed over the lane's blocks
+// and then across the row's lanes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "g2b_internal.h"
+
+namespace g2b {
+
+namespace {
+
+typedef float gemv_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGemvThreads = 256;
+constexpr int kGemvUnroll = 4;  // steps whose loads are in flight together
+constexpr int kGemvGroup = 8;   // blocks per lane in flight (x in LDS or the cache)
+constexpr int kGemvMinSteps = 8;            // wave-steps per wave, where there are enough
+constexpr int kGemvMaxXLds = 64 * 1024;     // x staged in LDS up to this many bytes
+
+template <typename T>
+__device__ __forceinline__ T nt_load(const void *p) {
+  return __builtin_nontemporal_load((const __attribute__((address_space(1))) T *)p);
+}
+
+// Dwords [B, B + 4N) where B is the dword boundary at or before p, and the
+// byte offset of p inside the first one (0 or 2 for 2-byte aligned blocks).
+// Default cache policy: neighbouring lanes' windows share their edge dwords,
+// which non-temporal loads would fetch twice.
+template <int N>
+__device__ __forceinline__ void load_dwords(const uint8_t *p, uint32_t (&d)[N], uint32_t &sh) {
+  const uintptr_t a = (uintptr_t)p;
+  const __attribute__((address_space(1))) uint32_t *base =
+      (const __attribute__((address_space(1))) uint32_t *)(a & ~(uintptr_t)3);
+  sh = (uint32_t)(a & 3u);
+#pragma unroll
+  for (int i = 0; i < N; i++) d[i] = base[i];
+}
+
+// Quant words j of a block whose payload starts 2 bytes after its first
+// byte: bytes 2..5 (sh 0) or 4..7 (sh 2) of the dword pair (d[j], d[j+1]).
+__device__ __forceinline__ uint32_t payload_word(const uint32_t *d, int j, uint32_t sh) {
+  return __builtin_amdgcn_perm(d[j + 1], d[j], sh ? 0x07060504u : 0x05040302u);
+}
+
+__device__ __forceinline__ float scale_of(uint32_t d0, uint32_t sh) {
+  return half_bits_to_f32_hw((d0 >> (8u * sh)) & 0xFFFFu);
+}
+
+// Raw block bytes: Q8_0 34 bytes -> 9 dwords, Q4_0 18 bytes -> 5 dwords.
+template <int FMT>
+struct BlockRaw {
+  static constexpr int N = FMT == 1 ? 9 : 5;
+  uint32_t d[N];
+  uint32_t sh;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_block(BlockRaw<FMT> &r, const uint8_t *p) {
+  load_dwords<BlockRaw<FMT>::N>(p, r.d, r.sh);
+}
+
+template <int FMT>
+__device__ __forceinline__ void zero_block(BlockRaw<FMT> &r) {
+#pragma unroll
+  for (int i = 0; i < BlockRaw<FMT>::N; i++) r.d[i] = 0u;
+  r.sh = 0u;
+}
+
+// v_cvt_off_f32_i4 of the low nibble of byte B of t (SDWA byte select, so
+// no shift is needed to bring the nibble down).
+template <int B>
+__device__ __forceinline__ float nib_f(uint32_t t) {
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+        : "=v"(r) : "v"(t));
+  else if constexpr (B == 1)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+        : "=v"(r) : "v"(t));
+  else if constexpr (B == 2)
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+        : "=v"(r) : "v"(t));
+  else
+    asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+        : "=v"(r) : "v"(t));
+  return r;
+}
+
+// sum_j w_j x_j of one block in fp32 (x: the block's 32 values).
+template <int FMT>
+__device__ __forceinline__ float block_dot(const BlockRaw<FMT> &r, const float *x) {
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  if constexpr (FMT == 1) {
+    // Q8_0 (l2_codec.c:306-320): d * (int8) q_j, element j = byte j
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t w = payload_word(r.d, j, r.sh);
+      a0 = fmaf((float)(int8_t)(w & 0xFFu), x[4 * j + 0], a0);
+      a1 = fmaf((float)(int8_t)((w >> 8) & 0xFFu), x[4 * j + 1], a1);
+      a2 = fmaf((float)(int8_t)((w >> 16) & 0xFFu), x[4 * j + 2], a2);
+      a3 = fmaf((float)(int8_t)(w >> 24), x[4 * j + 3], a3);
+    }
+    return ((a0 + a1) + (a2 + a3)) * scale_of(r.d[0], r.sh);
+  } else {
+    // Q4_0 (l2_codec.c:321-337): byte j holds element j (low nibble) and
+    // element j + 16 (high nibble), each (nibble - 8) * d.  v_cvt_off_f32_i4
+    // turns a signed nibble s into s / 16; nibble ^ 8 read as signed is
+    // nibble - 8, so the block's value is 16 * d * sum(...).
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t t = payload_word(r.d, j, r.sh) ^ 0x88888888u;
+      const uint32_t h = t >> 4;
+      a0 = fmaf(nib_f<0>(t), x[4 * j + 0], a0);
+      a1 = fmaf(nib_f<1>(t), x[4 * j + 1], a1);
+      a0 = fmaf(nib_f<2>(t), x[4 * j + 2], a0);
+      a1 = fmaf(nib_f<3>(t), x[4 * j + 3], a1);
+      a2 = fmaf(nib_f<0>(h), x[16 + 4 * j + 0], a2);
+      a3 = fmaf(nib_f<1>(h), x[16 + 4 * j + 1], a3);
+      a2 = fmaf(nib_f<2>(h), x[16 + 4 * j + 2], a2);
+      a3 = fmaf(nib_f<3>(h), x[16 + 4 * j + 3], a3);
+    }
+    return ((a0 + a1) + (a2 + a3)) * (16.f * scale_of(r.d[0], r.sh));
+  }
+}
+
+template <int LPR>
+__device__ __forceinline__ float lanes_sum(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Q8_0 / Q4_0.  KB > 0: the lane's x blocks (KB of them) live in registers;
+// KB == -1: any nb, x staged once per workgroup in LDS; KB == 0: any nb, x
+// read per block through the cache.
+template <int FMT, int LPR, int KB>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
+  extern __shared__ float xs[];
+  constexpr int RPS = 64 / LPR;  // rows per wave-step
+  constexpr int BB = FMT == 1 ? 34 : 18;
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+  const int rr = lane / LPR, c = lane % LPR;
+  const int nb = P.nb;
+  [[maybe_unused]] float xr[KB > 0 ? KB : 1][32];
+  if constexpr (KB < 0) {
+    const int n4 = nb * 8;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * kGemvThreads) {
+      float4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (i0 + k * kGemvThreads < n4)
+          v[k] = reinterpret_cast<const float4 *>(P.x)[i0 + k * kGemvThreads];
+#pragma unroll
+      for (int k = 0; k < 8; k++)
+        if (i0 + k * kGemvThreads < n4) reinterpret_cast<float4 *>(xs)[i0 + k * kGemvThreads] = v[k];
+    }
+    __syncthreads();
+  }
+  if constexpr (KB > 0) {
+#pragma unroll
+    for (int k = 0; k < KB; k++) {
+      const int b = c + LPR * k;
+#pragma unroll
+      for (int j = 0; j < 32; j += 4) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (b < nb) v = *reinterpret_cast<const float4 *>(P.x + 32 * b + j);
+        xr[k][j] = v.x;
+        xr[k][j + 1] = v.y;
+        xr[k][j + 2] = v.z;
+        xr[k][j + 3] = v.w;
+      }
+    }
+  }
+  const int stride = P.n_waves;
+  for (int s0 = gw; s0 < P.steps; s0 += stride * kGemvUnroll) {
+    if constexpr (KB > 0) {
+      BlockRaw<FMT> raw[kGemvUnroll][KB];
+      int row[kGemvUnroll];
+      bool ok[kGemvUnroll];
+#pragma unroll
+      for (int u = 0; u < kGemvUnroll; u++) {
+        const int s = s0 + u * stride;
+        row[u] = s * RPS + rr;
+        ok[u] = s < P.steps && row[u] < P.d;
+#pragma unroll
+        for (int k = 0; k < KB; k++) {
+          const int b = c + LPR * k;
+          if (ok[u] && b < nb)
+            load_block<FMT>(raw[u][k], P.w + (size_t)row[u] * P.row_bytes + (size_t)b * BB);
+          else
+            zero_block<FMT>(raw[u][k]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kGemvUnroll; u++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < KB; k++) acc += block_dot<FMT>(raw[u][k], xr[k]);
+        acc = lanes_sum<LPR>(acc);
+        if (ok[u] && c == 0) P.out[row[u]] = acc;
+      }
+    } else {
+      // any number of blocks: kGemvGroup of the lane's blocks in flight at a time
+#pragma unroll 1
+      for (int u = 0; u < kGemvUnroll; u++) {
+        const int s = s0 + u * stride;
+        const int row = s * RPS + rr;
+        const bool ok = s < P.steps && row < P.d;  // (uniform per row group)
+        const uint8_t *wr = P.w + (size_t)row * P.row_bytes;
+        float acc = 0.f;
+        for (int b0 = c; ok && b0 < nb; b0 += kGemvGroup * LPR) {
+          BlockRaw<FMT> r[kGemvGroup];
+#pragma unroll
+          for (int g = 0; g < kGemvGroup; g++) {
+            const int b = b0 + g * LPR;
+            if (b < nb)
+              load_block<FMT>(r[g], wr + (size_t)b * BB);
+            else
+              zero_block<FMT>(r[g]);
+          }
+#pragma unroll
+          for (int g = 0; g < kGemvGroup; g++) {
+            const int b = b0 + g * LPR;
+            if (b < nb) acc += block_dot<FMT>(r[g], (KB < 0 ? xs : P.x) + 32 * b);
+          }
+        }
+        acc = lanes_sum<LPR>(acc);
+        if (ok && c == 0) P.out[row] = acc;
+      }
+    }
+  }
+}
+
+// Q8_0 / Q4_0 rows of more than 128 blocks: the workgroup's four waves
+// split each row's blocks in quarters (a quarter of at most 128 blocks, so
+// every lane keeps the x of its KB <= 2 blocks in registers) and add their
+// partial sums in LDS.  Workgroups stride over steps of RPS rows.
+template <int FMT, int LPR, int KB>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
+  constexpr int RPS = 64 / LPR;
+  constexpr int BB = FMT == 1 ? 34 : 18;
+  constexpr int NW = kGemvThreads / 64;
+  __shared__ float part[kGemvUnroll][NW][RPS];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rr = lane / LPR, c = lane % LPR;
+  const int nb = P.nb, nbw = (nb + NW - 1) / NW;
+  const int b_lo = wave * nbw, b_hi = min(nb, b_lo + nbw);
+  float xr[KB][32];
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const int b = b_lo + c + LPR * k;
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (b < b_hi) v = *reinterpret_cast<const float4 *>(P.x + 32 * b + j);
+      xr[k][j] = v.x;
+      xr[k][j + 1] = v.y;
+      xr[k][j + 2] = v.z;
+      xr[k][j + 3] = v.w;
+    }
+  }
+  const int stride = gridDim.x;
+  for (int s0 = blockIdx.x; s0 < P.steps; s0 += stride * kGemvUnroll) {
+    BlockRaw<FMT> raw[kGemvUnroll][KB];
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; u++) {
+      const int s = s0 + u * stride;
+      const int row = s * RPS + rr;
+      const bool ok = s < P.steps && row < P.d;
+#pragma unroll
+      for (int k = 0; k < KB; k++) {
+        const int b = b_lo + c + LPR * k;
+        if (ok && b < b_hi)
+          load_block<FMT>(raw[u][k], P.w + (size_t)row * P.row_bytes + (size_t)b * BB);
+        else
+          zero_block<FMT>(raw[u][k]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kGemvUnroll; u++) {
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < KB; k++) acc += block_dot<FMT>(raw[u][k], xr[k]);
+      acc = lanes_sum<LPR>(acc);
+      if (c == 0) part[u][wave][rr] = acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < kGemvUnroll * RPS) {
+      const int u = threadIdx.x / RPS, r = threadIdx.x % RPS;
+      const int s = s0 + u * stride;
+      const int row = s * RPS + r;
+      if (s < P.steps && row < P.d)
+        P.out[row] = (part[u][0][r] + part[u][1][r]) + (part[u][2][r] + part[u][3][r]);
+    }
+    __syncthreads();
+  }
+}
+
+// F32 (l3_math.c:17-20): a wave per row, lanes over float4 pieces.
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_f32(GemvParams P) {
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+  const int n = P.n, n4 = n / 4;
+  for (int row = gw; row < P.d; row += P.n_waves) {
+    const float *wr = reinterpret_cast<const float *>(P.w + (size_t)row * P.row_bytes);
+    float a0 = 0.f, a1 = 0.f;
+    if (P.vec4) {
+      for (int j = lane; j < n4; j += 64) {
+        const gemv_f32x4 w4 = nt_load<gemv_f32x4>(wr + 4 * j);
+        const float4 x4 = *reinterpret_cast<const float4 *>(P.x + 4 * j);
+        a0 = fmaf(w4.x, x4.x, a0);
+        a1 = fmaf(w4.y, x4.y, a1);
+        a0 = fmaf(w4.z, x4.z, a0);
+        a1 = fmaf(w4.w, x4.w, a1);
+      }
+      for (int j = 4 * n4 + lane; j < n; j += 64) a0 = fmaf(wr[j], P.x[j], a0);
+    } else {
+      for (int j = lane; j < n; j += 64) a0 = fmaf(wr[j], P.x[j], a0);
+    }
+    const float acc = lanes_sum<64>(a0 + a1);
+    if (lane == 0) P.out[row] = acc;
+  }
+}
+
+__global__ void k_fill_zero(float *out, int32_t n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = 0.f;
+}
+
+template <int FMT, int LPR>
+hipError_t launch_q_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
+  const dim3 blk(kGemvThreads);
+  switch (kb) {
+    case 1: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 1>), grid, blk, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 2>), grid, blk, 0, s, p); break;
+    case -1:
+      hipLaunchKernelGGL((k_gemv_q<FMT, LPR, -1>), grid, blk, (size_t)p.nb * 128u, s, p);
+      break;
+    default: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 0>), grid, blk, 0, s, p); break;
+  }
+  return hipGetLastError();
+}
+
+template <int FMT, int LPR>
+hipError_t launch_split_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
+  if (kb == 1)
+    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 1>), grid, dim3(kGemvThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 2>), grid, dim3(kGemvThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_split(const GemvParams &p, int lpr, int kb, dim3 grid, hipStream_t s) {
+  // a quarter of more than 128 blocks is more than 32: LPR is 64
+  (void)lpr;
+  return launch_split_lpr<FMT, 64>(p, kb, grid, s);
+}
+
+template <int FMT>
+hipError_t launch_q(const GemvParams &p, int lpr, int kb, dim3 grid, hipStream_t s) {
+  switch (lpr) {
+    case 1: return launch_q_lpr<FMT, 1>(p, kb, grid, s);
+    case 2: return launch_q_lpr<FMT, 2>(p, kb, grid, s);
+    case 4: return launch_q_lpr<FMT, 4>(p, kb, grid, s);
+    case 8: return launch_q_lpr<FMT, 8>(p, kb, grid, s);
+    case 16: return launch_q_lpr<FMT, 16>(p, kb, grid, s);
+    case 32: return launch_q_lpr<FMT, 32>(p, kb, grid, s);
+    default: return launch_q_lpr<FMT, 64>(p, kb, grid, s);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_fill_zero(float *out, int32_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_zero, dim3((n + 255) / 256), dim3(256), 0, s, out, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
+  const int waves_per_wg = kGemvThreads / 64;
+  if (type == kTypeF32) {
+    p.row_bytes = (uint32_t)p.n * 4u;
+    p.vec4 = ((uintptr_t)p.w % 16 == 0 && (uintptr_t)p.x % 16 == 0 && p.n % 4 == 0) ? 1 : 0;
+    const int wgs = std::max(1, std::min((p.d + waves_per_wg - 1) / waves_per_wg, n_cu * 8));
+    p.n_waves = wgs * waves_per_wg;
+    hipLaunchKernelGGL(k_gemv_f32, dim3(wgs), dim3(kGemvThreads), 0, s, p);
+    return hipGetLastError();
+  }
+  const int fmt = type == kTypeQ8_0 ? 1 : 2;
+  p.nb = p.n / 32;
+  p.row_bytes = (uint32_t)p.nb * (fmt == 1 ? 34u : 18u);
+  if (p.nb > 128 && p.nb <= 4 * 128 && p.x_vec4) {
+    // rows split over the workgroup's four waves (x in registers)
+    const int nbw = (p.nb + 3) / 4;  // > 32, so 64 lanes per row
+    const int kb = (nbw + 63) / 64;
+    p.steps = p.d;
+    const int wgs = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
+                                      std::min(p.steps, n_cu)),
+                             n_cu * 4);
+    p.n_waves = wgs * waves_per_wg;
+    return fmt == 1 ? launch_split<1>(p, 64, kb, dim3(wgs), s)
+                    : launch_split<2>(p, 64, kb, dim3(wgs), s);
+  }
+  int lpr = 1;
+  while (lpr < p.nb && lpr < 64) lpr *= 2;
+  const int kb = (p.nb + lpr - 1) / lpr;
+  const int rps = 64 / lpr;
+  p.steps = (p.d + rps - 1) / rps;
+  // every wave loads the x of its blocks once: at least kGemvMinSteps steps
+  // per wave where there are enough, at least 4 waves per CU, at most 16
+  const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
+                                      std::min(p.steps, n_cu * 4)),
+                             n_cu * 16);
+  const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
+  p.n_waves = wgs * waves_per_wg;
+  const int kbv = !p.x_vec4                     ? 0
+                  : kb <= 2                     ? kb
+                  : p.nb * 128 <= kGemvMaxXLds ? -1
+                                                : 0;
+  return fmt == 1 ? launch_q<1>(p, lpr, kbv, dim3(wgs), s) : launch_q<2>(p, lpr, kbv, dim3(wgs), s);
+}
+
+}  // namespace g2b

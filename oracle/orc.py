@@ -256,6 +256,103 @@ def attn_batch(shape: Shape, layer0: int, n_layers: int, pos: np.ndarray,
     return qo
 
 
+# ---------------------------------------------------------------- weight GEMVs
+# numpy restatements of the scalar matmul kernels (the reference's build
+# without AVX2, kvtest flags: no FMA contraction), vectorised over rows but
+# in the reference's per-row operation order, so they are bit-exact with it.
+
+T_F32, T_Q4_0, T_Q8_0 = 0, 2, 8
+
+
+def matmul_row_bytes(t: int, n: int) -> int:
+    """row_stride (l2_codec.c:340) of the fused types."""
+    return {T_F32: n * 4, T_Q8_0: (n // 32) * 34, T_Q4_0: (n // 32) * 18}[t]
+
+
+def _blocks(w: np.ndarray, t: int, n: int, d: int):
+    nb, bb = n // 32, (34 if t == T_Q8_0 else 18)
+    blk = np.ascontiguousarray(w[:d * nb * bb]).reshape(d, nb, bb)
+    scale = half_to_float(blk[:, :, :2].copy().view(np.uint16)).reshape(d, nb)
+    return nb, blk, scale
+
+
+def matmul_scalar(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int) -> np.ndarray:
+    """matmul_q8_0 (l2_codec.c:306-320): sum += s*(f32)q*x[j] serially;
+    matmul_q4_0 (:321-340): sum += s*((f32)(lo-8)*x[j] + (f32)(hi-8)*x[j+16]);
+    matmul (l3_math.c:17-20): s += w*x serially.  float32, no contraction."""
+    x = np.ascontiguousarray(x, np.float32)
+    f = np.float32
+    acc = np.zeros(d, np.float32)
+    if t == T_F32:
+        wf = np.ascontiguousarray(w[:d * n * 4]).view(np.float32).reshape(d, n)
+        for j in range(n):
+            acc = acc + wf[:, j] * x[j]
+        return acc
+    nb, blk, scale = _blocks(w, t, n, d)
+    for b in range(nb):
+        s = scale[:, b]
+        xb = x[32 * b:32 * b + 32]
+        if t == T_Q8_0:
+            q = blk[:, b, 2:].view(np.int8).astype(np.float32)
+            for j in range(32):
+                acc = acc + (s * q[:, j]) * xb[j]
+        else:
+            qs = blk[:, b, 2:]
+            lo = ((qs & 0x0F).astype(np.int32) - 8).astype(np.float32)
+            hi = ((qs >> 4).astype(np.int32) - 8).astype(np.float32)
+            for j in range(16):
+                acc = acc + s * (lo[:, j] * xb[j] + hi[:, j] * xb[j + 16])
+    assert acc.dtype == f
+    return acc
+
+
+def matmul_exact(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int):
+    """float64 W x of the same weights (dequantisation is exact: fp16 scale
+    times a small integer), and sum_j |w_ij x_j| (for error bounds)."""
+    x64 = np.asarray(x, np.float64)
+    if t == T_F32:
+        wf = np.ascontiguousarray(w[:d * n * 4]).view(np.float32).reshape(d, n).astype(np.float64)
+    else:
+        nb, blk, scale = _blocks(w, t, n, d)
+        if t == T_Q8_0:
+            q = blk[:, :, 2:].view(np.int8).astype(np.float64)
+        else:
+            qs = blk[:, :, 2:]
+            q = np.concatenate([(qs & 0x0F).astype(np.float64) - 8,
+                                (qs >> 4).astype(np.float64) - 8], axis=2)
+        wf = (q * scale.astype(np.float64)[:, :, None]).reshape(d, nb * 32)
+        x64 = x64[:nb * 32]
+    return wf @ x64, np.abs(wf) @ np.abs(x64)
+
+
+def ref_matmul(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int,
+               variant: str = "avx2") -> np.ndarray:
+    """The compiled reference's matmul_q8_0 / matmul_q4_0 / matmul."""
+    L = ref_lib(variant)
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    out = np.zeros(d, np.float32)
+    xx = np.ascontiguousarray(x, np.float32).copy()
+    ww = np.ascontiguousarray(w, np.uint8)
+    fn = {T_Q8_0: L.matmul_q8_0, T_Q4_0: L.matmul_q4_0, T_F32: L.matmul}[t]
+    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32]
+    fn.restype = None
+    fn(out.ctypes.data, xx.ctypes.data, ww.ctypes.data, n, d)
+    return out
+
+
+def random_weights(rng: np.random.Generator, t: int, n: int, d: int) -> np.ndarray:
+    """d rows of random blocks: fp16 scales in [2^-10, 2^-4), int8 quants in
+    [-128, 127] (Q8_0) or nibbles (Q4_0); N(0,1) floats for F32."""
+    if t == T_F32:
+        return rng.standard_normal(d * n).astype(np.float32).view(np.uint8).copy()
+    nb, bb = n // 32, (34 if t == T_Q8_0 else 18)
+    blk = rng.integers(0, 256, (d, nb, bb), dtype=np.uint8)
+    sc = np.exp2(rng.uniform(-10, -4, (d, nb))).astype(np.float16)
+    blk[:, :, :2] = sc.view(np.uint8).reshape(d, nb, 2)
+    return blk.reshape(-1).copy()
+
+
 # ---------------------------------------------------------------- budgeting
 # Pure-Python restatements (small integer arithmetic).
 

@@ -1,0 +1,95 @@
+"""The weight-GEMV oracle (oracle/orc.py: matmul_scalar, matmul_exact) pinned
+without a GPU:
+  * bit-exact with the compiled reference's scalar matmul_q8_0 / matmul_q4_0 /
+    matmul (l2_codec.c:306-340, l3_math.c:17-20; oracle/_ref scalar build);
+  * within the serial-summation error bound of a float64 evaluation of the
+    same (exactly dequantised) weights, as is the AVX2 reference;
+  * the float64 evaluation itself against closed forms (one-hot x picks a
+    column; constant nibble 8 gives zero weights; a block scale of 2^k scales
+    the output by 2^k exactly).
+"""
+import numpy as np
+import pytest
+
+from oracle import orc
+from gguf2bin_amd import attn
+
+U = 2.0 ** -24
+TYPES = [orc.T_Q8_0, orc.T_Q4_0, orc.T_F32]
+SHAPES = [(32, 1), (64, 5), (100, 9), (576, 33), (1024, 64), (3072, 17)]
+
+
+def ref_or_skip(variant):
+    if orc.ref_lib(variant) is None:
+        pytest.skip("compiled reference not built (make -C oracle ref)")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n,d", SHAPES)
+def test_scalar_restatement_bit_exact_with_reference(t, n, d):
+    ref_or_skip("scalar")
+    rng = np.random.default_rng(n * 7 + d + t)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    a = orc.matmul_scalar(x, w, t, n, d)
+    r = orc.ref_matmul(x, w, t, n, d, "scalar")
+    assert np.array_equal(a.view(np.uint32), r.view(np.uint32))
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n,d", SHAPES)
+def test_oracle_and_avx2_reference_within_fp32_bound(t, n, d):
+    rng = np.random.default_rng(n * 11 + d + t)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    ex, ab = orc.matmul_exact(x, w, t, n, d)
+    terms = n if t == orc.T_F32 else (n // 32) * 32
+    bound = (terms + 2) * U * ab  # serial summation of terms products
+    assert np.all(np.abs(orc.matmul_scalar(x, w, t, n, d) - ex) <= bound)
+    if orc.ref_lib("avx2") is not None:
+        assert np.all(np.abs(orc.ref_matmul(x, w, t, n, d, "avx2") - ex) <= bound)
+
+
+@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0])
+def test_exact_evaluation_closed_forms(t):
+    n, d = 96, 4
+    rng = np.random.default_rng(5)
+    w = orc.random_weights(rng, t, n, d)
+    bb = 34 if t == orc.T_Q8_0 else 18
+    blk = w.reshape(d, n // 32, bb)
+    # one-hot x at column j: the output is that column's dequantised weight
+    for j in (0, 17, 31, 32, 95):
+        x = np.zeros(n, np.float32)
+        x[j] = 1.0
+        ex, _ = orc.matmul_exact(x, w, t, n, d)
+        b, e = divmod(j, 32)
+        s = blk[:, b, :2].copy().view(np.float16).astype(np.float64).ravel()
+        if t == orc.T_Q8_0:
+            q = blk[:, b, 2 + e].view(np.int8).astype(np.float64)
+        else:
+            byte = blk[:, b, 2 + (e % 16)]
+            q = ((byte & 0x0F) if e < 16 else (byte >> 4)).astype(np.float64) - 8
+        assert np.array_equal(ex, s * q)
+    # Q4_0 nibble 8 everywhere is the zero matrix
+    if t == orc.T_Q4_0:
+        z = blk.copy()
+        z[:, :, 2:] = 0x88
+        ex, ab = orc.matmul_exact(rng.standard_normal(n), z.ravel(), t, n, d)
+        assert not ex.any() and not ab.any()
+    # scale 2^k -> output x 2^k exactly
+    x = rng.standard_normal(n).astype(np.float32)
+    one = blk.copy()
+    one[:, :, :2] = np.array([1.0], np.float16).view(np.uint8)
+    four = blk.copy()
+    four[:, :, :2] = np.array([4.0], np.float16).view(np.uint8)
+    e1, _ = orc.matmul_exact(x, one.ravel(), t, n, d)
+    e4, _ = orc.matmul_exact(x, four.ravel(), t, n, d)
+    assert np.array_equal(e4, 4 * e1)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_row_bytes(t):
+    for n in (0, 31, 32, 100, 1024, 14336):
+        assert attn.matmul_row_bytes(t, n) == orc.matmul_row_bytes(t, n)
+    assert attn.matmul_row_bytes(t, -1) == 0
+    assert attn.matmul_row_bytes(1, 64) == 0  # F16: no device GEMV
