@@ -104,6 +104,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
 // drifts by ~1e-5 relative once one partial dominates.
 constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 2048;
+constexpr int kCombineFewParts = 32;  // up to this many partials: 64-thread workgroups
 
 __device__ inline float block_max_f(float x, float *red) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -296,7 +297,12 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s) {
   if (p.max_splits > kCombineMaxParts) return hipErrorInvalidValue;
   dim3 grid(p.sh.n_heads, p.n_seq, n_layers);
-  hipLaunchKernelGGL(k_combine, grid, dim3(kCombineThreads), 0, s, p, p.q_out);
+  // Few partials per head: one wave per workgroup.  With thousands of heads
+  // in the grid (c4: 4096) the launch is bound by dispatching waves (~7 us
+  // to start 4096 x 4 waves), not by the merge; many partials (a single
+  // long sequence) need the four waves.
+  const int threads = p.max_splits <= kCombineFewParts ? 64 : kCombineThreads;
+  hipLaunchKernelGGL(k_combine, grid, dim3(threads), 0, s, p, p.q_out);
   return hipGetLastError();
 }
 
