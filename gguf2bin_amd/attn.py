@@ -31,7 +31,9 @@ EXPORTS = [
     "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows", "g2b_set_qk_norm",
     "g2b_model_kv_bytes", "g2b_clamp_ctx", "g2b_hbm_bytes", "g2b_auto_budget", "g2b_hbm_info",
     "g2b_matmul_row_bytes", "g2b_matmul", "g2b_matmul_host", "g2b_weights_upload",
-    "g2b_weights_free",
+    "g2b_weights_free", "g2b_g2bx_open", "g2b_g2bx_close", "g2b_g2bx_slot",
+    "g2b_model_load_g2bx", "g2b_model_free", "g2b_model_info", "g2b_model_ctx",
+    "g2b_model_forward",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
@@ -54,6 +56,24 @@ class _Shape(C.Structure):
 class _Seq(C.Structure):
     _fields_ = [("pos", C.c_int32), ("ctx_cap", C.c_int32), ("kcache", C.c_void_p),
                 ("vcache", C.c_void_p)]
+
+
+class _ModelCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden_dim", C.c_int32), ("n_layers", C.c_int32),
+                ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32), ("vocab", C.c_int32),
+                ("seq_len", C.c_int32), ("head_dim", C.c_int32), ("eps", C.c_float),
+                ("rope_theta", C.c_float)]
+
+
+class _Slot(C.Structure):
+    _fields_ = [("role", C.c_uint8), ("layer", C.c_uint16), ("type", C.c_uint8),
+                ("nbytes", C.c_uint32), ("off", C.c_uint64)]
+
+
+class _G2bx(C.Structure):
+    _fields_ = [("version", C.c_uint16), ("arch", C.c_uint8), ("flags", C.c_uint8),
+                ("cfg", _ModelCfg), ("n_slots", C.c_uint32), ("slots", C.POINTER(_Slot)),
+                ("data", C.POINTER(C.c_uint8)), ("data_size", C.c_uint64)]
 
 
 @dataclass(frozen=True)
@@ -109,6 +129,15 @@ def lib() -> C.CDLL:
             "g2b_auto_budget": ([C.POINTER(_Shape), i32, i32, u64, C.POINTER(i32),
                                  C.POINTER(i32)], C.c_int),
             "g2b_hbm_info": ([vp, C.POINTER(u64), C.POINTER(u64)], C.c_int),
+            "g2b_g2bx_open": ([C.c_char_p, C.POINTER(_G2bx)], C.c_int),
+            "g2b_g2bx_close": ([C.POINTER(_G2bx)], None),
+            "g2b_g2bx_slot": ([C.POINTER(_G2bx), i32, i32], C.POINTER(_Slot)),
+            "g2b_model_load_g2bx": ([C.POINTER(vp), i32, C.c_char_p, i32, i32], C.c_int),
+            "g2b_model_free": ([vp], C.c_int),
+            "g2b_model_info": ([vp, C.POINTER(_ModelCfg), C.POINTER(i32), C.POINTER(i32),
+                                C.POINTER(i32)], C.c_int),
+            "g2b_model_ctx": ([vp], vp),
+            "g2b_model_forward": ([vp, i32, i32, fp], C.c_int),
             "g2b_matmul_row_bytes": ([i32, i32], C.c_size_t),
             "g2b_matmul": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
             "g2b_matmul_host": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
@@ -159,6 +188,67 @@ def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
 
 
 T_F32, T_Q4_0, T_Q8_0 = 0, 2, 8  # GGML type ids of the device GEMVs
+T_F16 = 1
+CFG_FIELDS = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab", "seq_len",
+              "head_dim", "eps", "rope_theta")
+
+
+def g2bx_open(path: str) -> dict:
+    """Parse a G2BX container on the host (g2b_g2bx_open): header, config,
+    slots (role, layer, type, nbytes, off) and the weight blob (bytes)."""
+    g = _G2bx()
+    rc = lib().g2b_g2bx_open(path.encode(), C.byref(g))
+    if rc:
+        raise G2BError(rc, f"g2b_g2bx_open({path}): {strerror(rc)}")
+    try:
+        cfg = {f: getattr(g.cfg, f) for f in CFG_FIELDS}
+        slots = [(g.slots[i].role, g.slots[i].layer, g.slots[i].type, g.slots[i].nbytes,
+                  g.slots[i].off) for i in range(g.n_slots)]
+        data = C.string_at(g.data, g.data_size)
+        return {"version": g.version, "arch": g.arch, "flags": g.flags, "cfg": cfg,
+                "slots": slots, "data": data}
+    finally:
+        lib().g2b_g2bx_close(C.byref(g))
+
+
+class Model:
+    """A G2BX model on the device (g2b_model_*): weights in HBM, the decode
+    step (model_forward, l5_model.c:461-606) as device kernels."""
+
+    def __init__(self, path: str, device: int = 0, kv_q8: bool = False, ctx: int = 0):
+        self.h = C.c_void_p()
+        rc = lib().g2b_model_load_g2bx(C.byref(self.h), device, path.encode(),
+                                       1 if kv_q8 else 0, ctx)
+        if rc:
+            raise G2BError(rc, f"g2b_model_load_g2bx({path}): {strerror(rc)}")
+        c, arch, flags, cc = _ModelCfg(), C.c_int32(), C.c_int32(), C.c_int32()
+        lib().g2b_model_info(self.h, C.byref(c), C.byref(arch), C.byref(flags), C.byref(cc))
+        self.cfg = {f: getattr(c, f) for f in CFG_FIELDS}
+        self.arch, self.flags, self.ctx_cap = arch.value, flags.value, cc.value
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        out = np.zeros(self.cfg["vocab"], np.float32)
+        rc = lib().g2b_model_forward(self.h, token, pos, out.ctypes.data)
+        if rc:
+            raise G2BError(rc, f"g2b_model_forward: {strerror(rc)}")
+        return out
+
+    def forward_rc(self, token: int, pos: int):
+        """(return code, logits) without raising."""
+        out = np.full(self.cfg["vocab"], 7.0, np.float32)
+        rc = lib().g2b_model_forward(self.h, token, pos, out.ctypes.data)
+        return rc, out
+
+    def close(self):
+        if self.h:
+            lib().g2b_model_free(self.h)
+            self.h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
 
 
 def matmul_row_bytes(t: int, n: int) -> int:

@@ -341,6 +341,48 @@ def ref_matmul(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int,
     return out
 
 
+def ref_g2bx_info(path: str):
+    """The compiled reference's model_load_g2bx on a file: (cfg40 bytes,
+    arch, flags, slots as (role, layer, type, nbytes, off))."""
+    L = ref_lib("avx2")
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    fn = L.ref_g2bx_info
+    fn.argtypes = [C.c_char_p, C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                   C.POINTER(C.c_uint32), C.c_void_p, C.c_uint32]
+    fn.restype = C.c_int
+    cfg = np.zeros(40, np.uint8)
+    slots = np.zeros(16 * 4096, np.uint8)
+    arch, flags, ns = C.c_int(), C.c_int(), C.c_uint32()
+    if fn(path.encode(), cfg.ctypes.data, C.byref(arch), C.byref(flags), C.byref(ns),
+          slots.ctypes.data, 4096):
+        raise RuntimeError(f"reference loader rejected {path}")
+    out = []
+    for i in range(min(ns.value, 4096)):
+        b = slots[16 * i:16 * i + 16].tobytes()
+        out.append((b[0], int.from_bytes(b[1:3], "little"), b[3],
+                    int.from_bytes(b[4:8], "little"), int.from_bytes(b[8:16], "little")))
+    return cfg.tobytes(), arch.value, flags.value, out
+
+
+def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
+                      ctx: int = 0) -> np.ndarray:
+    """The compiled reference's model_forward over tokens at positions
+    0..n-1 of a G2BX file: logits [n][vocab]."""
+    L = ref_lib("avx2")
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    fn = L.ref_model_forward_g2bx
+    fn.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    fn.restype = C.c_int
+    tok = np.ascontiguousarray(tokens, np.int32)
+    out = np.zeros((len(tok), vocab), np.float32)
+    rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, tok.ctypes.data, len(tok), out.ctypes.data)
+    if rc:
+        raise RuntimeError(f"reference forward failed ({rc})")
+    return out
+
+
 def random_weights(rng: np.random.Generator, t: int, n: int, d: int) -> np.ndarray:
     """d rows of random blocks: fp16 scales in [2^-10, 2^-4), int8 quants in
     [-128, 127] (Q8_0) or nibbles (Q4_0); N(0,1) floats for F32."""

@@ -223,3 +223,36 @@ int ref_auto_budget(i32 dim, i32 hid, i32 n_layers, i32 n_heads, i32 n_kv_heads,
   free_rt(&m);
   return rc;
 }
+
+/* The reference's G2BX loader (model_load_g2bx, l5_model.c:393-408) on a file:
+ * its parsed ModelCfg (40 packed bytes), arch, flags, slot count and packed
+ * 16-byte slots (at most max_slots copied).  0 on success. */
+int ref_g2bx_info(const char *path, u8 *cfg40, int *arch, int *flags, u32 *n_slots,
+                  u8 *slots16, u32 max_slots) {
+  Model m;
+  if (model_load_g2bx(path, &m)) return -1;
+  memcpy(cfg40, &m.c, sizeof m.c);
+  *arch = m.arch;
+  *flags = m.flags;
+  *n_slots = m.n_slots;
+  for (u32 i = 0; i < m.n_slots && i < max_slots; i++) memcpy(slots16 + 16 * i, &m.slots[i], 16);
+  model_free(&m);
+  return 0;
+}
+
+/* model_forward (l5_model.c:461-606) over tokens[0..n) at positions 0..n-1
+ * of a G2BX file, KV in Q8_0 when kv_q8, context ctx (<= 0: seq_len):
+ * logits of every step into out[n][vocab].  0 on success. */
+int ref_model_forward_g2bx(const char *path, int kv_q8, int ctx, const i32 *tokens, int n,
+                           f32 *out) {
+  Model m;
+  if (model_load_g2bx(path, &m)) return -1;
+  if (kv_q8) m.flags |= F_KV_Q8;
+  if (model_set_ctx(&m, ctx > 0 ? ctx : m.c.seq_len)) {
+    model_free(&m);
+    return -2;
+  }
+  for (int i = 0; i < n; i++) model_forward(&m, tokens[i], i, out + (size_t)i * m.c.vocab);
+  model_free(&m);
+  return 0;
+}

@@ -207,3 +207,89 @@ def check_weights(got, ref, exact, rtol: float = W_RTOL):
         assert r_ex <= rtol, f"max rel |w - float64| = {r_ex:.3g} > {rtol}"
         assert r_ref <= rtol + own, f"max rel |w - ref| = {r_ref:.3g} > {rtol} + own {own:.3g}"
     assert np.all(np.abs(got[~big] - exact[~big]) <= 1e-35)
+
+
+# ---------------------------------------------------------------- G2BX files
+# Roles and flags of the container (include/g2b.h:18-24).
+R_TOK_EMBD, R_OUT_NORM, R_OUTPUT = 0, 1, 2
+(R_ATTN_NORM, R_ATTN_Q, R_ATTN_K, R_ATTN_V, R_ATTN_O, R_ATTN_Q_NORM, R_ATTN_K_NORM,
+ R_FFN_NORM, R_FFN_GATE, R_FFN_UP, R_FFN_DOWN) = range(3, 14)
+F_TIE_EMBD, F_QK_NORM = 1, 2
+G2BX_CFG = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab", "seq_len",
+            "head_dim", "eps", "rope_theta")
+
+
+def write_g2bx(path, cfg: dict, arch: int, flags: int, slots, version: int = 1):
+    """A G2BX container laid out as the reference's writer lays it out
+    (exp_synth_qwen_tiny, /root/reference/src/l5_model.c:666-676): header,
+    packed 40-byte ModelCfg, slot table, then each slot's bytes at a 64-byte
+    aligned offset, zero padding to the aligned end.  slots: (role, layer,
+    type, bytes) with layer 0xFFFF for global slots."""
+    import struct
+    offs, cur = [], 0
+    for s in slots:
+        offs.append(cur)
+        cur = (cur + len(s[3]) + 63) & ~63
+    head = b"G2BX" + struct.pack("<HBB", version, arch, flags)
+    head += struct.pack("<8i2f", *[cfg[k] for k in G2BX_CFG])
+    head += struct.pack("<I", len(slots))
+    for (role, layer, typ, data), off in zip(slots, offs):
+        head += struct.pack("<BHBIQ", role, layer, typ, len(data), off)
+    blob = bytearray(cur)
+    for (_, _, _, data), off in zip(slots, offs):
+        blob[off:off + len(data)] = data
+    with open(path, "wb") as f:
+        f.write(head + bytes(blob))
+
+
+def random_matrix_bytes(rng, t: int, rows: int, n: int, gain: float = 1.0) -> bytes:
+    """rows x n weights of type t with values ~ gain * U(-1, 1) / sqrt(n) (Q8_0,
+    Q4_0: random quants with one fp16 scale per block; F32: normal / sqrt(n))."""
+    if t == 0:
+        return (rng.standard_normal((rows, n)) * gain / np.sqrt(n)).astype(np.float32).tobytes()
+    if t == 1:
+        return (rng.standard_normal((rows, n)) * gain / np.sqrt(n)).astype(np.float16).tobytes()
+    nb = n // 32
+    if t == 8:
+        blk = np.zeros((rows, nb, 34), np.uint8)
+        blk[:, :, 2:] = rng.integers(-127, 128, (rows, nb, 32)).astype(np.int8).view(np.uint8)
+        sc = np.full((rows, nb), gain / (127 * np.sqrt(n)) * 1.7, np.float32)
+    else:
+        blk = np.zeros((rows, nb, 18), np.uint8)
+        blk[:, :, 2:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)
+        sc = np.full((rows, nb), gain / (8 * np.sqrt(n)) * 1.7, np.float32)
+    sc *= rng.uniform(0.5, 1.5, (rows, nb)).astype(np.float32)
+    blk[:, :, :2] = sc.astype(np.float16).view(np.uint8).reshape(rows, nb, 2)
+    return blk.tobytes()
+
+
+def random_model_slots(rng, cfg: dict, flags: int, mat_type: int, emb_type: int,
+                       out_type=None):
+    """Every slot model_forward reads, random: norms near 1 (F32), matrices
+    of mat_type, embeddings of emb_type, an untied output of out_type (None:
+    tied to the embeddings, F_TIE_EMBD)."""
+    d, h, nl = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"]
+    nq, nkv, hd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["head_dim"]
+    G = 0xFFFF
+
+    def norm(n):
+        return (1.0 + 0.2 * rng.standard_normal(n)).astype(np.float32).tobytes()
+
+    slots = [(R_TOK_EMBD, G, emb_type, random_matrix_bytes(rng, emb_type, cfg["vocab"], d,
+                                                           gain=np.sqrt(d))),
+             (R_OUT_NORM, G, 0, norm(d))]
+    if out_type is not None:
+        slots.append((R_OUTPUT, G, out_type, random_matrix_bytes(rng, out_type, cfg["vocab"], d)))
+    for L in range(nl):
+        slots += [(R_ATTN_NORM, L, 0, norm(d)),
+                  (R_ATTN_Q, L, mat_type, random_matrix_bytes(rng, mat_type, nq, d)),
+                  (R_ATTN_K, L, mat_type, random_matrix_bytes(rng, mat_type, nkv, d)),
+                  (R_ATTN_V, L, mat_type, random_matrix_bytes(rng, mat_type, nkv, d)),
+                  (R_ATTN_O, L, mat_type, random_matrix_bytes(rng, mat_type, d, nq))]
+        if flags & F_QK_NORM:
+            slots += [(R_ATTN_Q_NORM, L, 0, norm(hd)), (R_ATTN_K_NORM, L, 0, norm(hd))]
+        slots += [(R_FFN_NORM, L, 0, norm(d)),
+                  (R_FFN_GATE, L, mat_type, random_matrix_bytes(rng, mat_type, h, d)),
+                  (R_FFN_UP, L, mat_type, random_matrix_bytes(rng, mat_type, h, d)),
+                  (R_FFN_DOWN, L, mat_type, random_matrix_bytes(rng, mat_type, d, h))]
+    return slots
