@@ -223,6 +223,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-fused", action="store_true", help="skip the all-layers-in-one-call run")
     ap.add_argument("--no-gemv", action="store_true", help="skip the weight-GEMV measurement")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the whole-decode-step (model_forward) measurement")
     ap.add_argument("--no-others", action="store_true",
                     help="skip the other BASELINE configs (reported under all_configs)")
     ap.add_argument("--cpu-seq-a", type=int, default=4, help="sequences in the 1-thread sample")
@@ -329,6 +331,7 @@ def main():
             o.close()
 
     gemv = None if args.no_gemv else gemv_leg(args)
+    model = None if args.no_model else model_leg(args)
 
     traffic = load_traffic(args.config)
     roof = {"bound": "hbm", "kernel": "k_layer", "achieved": round(dec_gbps, 2),
@@ -359,6 +362,7 @@ def main():
         "parity_full_size": parity,
         "all_configs": others,
         "gemv": gemv,
+        "model_forward": model,
     }
     print(json.dumps(line), flush=True)
 
@@ -426,6 +430,76 @@ def gemv_leg(args):
             f"cpu {res[name]['cpu_GBps']} GB/s")
     ctx.close()
     return res
+
+
+def model_leg(args):
+    """A whole decode step on the device (g2b_model_forward, model_forward of
+    l5_model.c:461-606) for a Qwen3-0.6B-shape model with random Q8_0 weights
+    (28 layers, dim 1024, hidden 3072, 16/8 heads of 128, vocab 151936, tied
+    embeddings, QK-RMSNorm; 0.63 GB) written as a G2BX file, Q8_0 KV: decode
+    tokens per second at positions 8..8+K, next to the reference's own
+    model_forward (compiled reference, AVX2+OpenMP) on the same file, whose
+    first steps also check the device's logits."""
+    import tempfile
+    from oracle import orc  # CPU baseline and checker only
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from helpers import F_QK_NORM, F_TIE_EMBD, random_model_slots, write_g2bx
+
+    cfg = dict(dim=1024, hidden_dim=3072, n_layers=28, n_heads=16, n_kv_heads=8, vocab=151936,
+               seq_len=4096, head_dim=128, eps=1e-6, rope_theta=1e6)
+    flags = F_QK_NORM | F_TIE_EMBD
+    rng = np.random.default_rng(args.seed + 11)
+    fd, path = tempfile.mkstemp(suffix=".g2bx")
+    os.close(fd)
+    try:
+        slots = random_model_slots(rng, cfg, flags, attn.T_Q8_0, attn.T_Q8_0, None)
+        wbytes = sum(len(s[3]) for s in slots)
+        write_g2bx(path, cfg, attn.ARCH_QWEN3, flags, slots)
+        del slots
+        K = max(16, args.steps * 2)
+        toks = [int(t) for t in rng.integers(0, cfg["vocab"], 8 + K)]
+        with attn.Model(path, kv_q8=True) as m:
+            first = [m.forward(toks[i], i) for i in range(8)]
+            t0 = time.perf_counter()
+            for i in range(8, 8 + K):
+                m.forward(toks[i], i)
+            dt = (time.perf_counter() - t0) / K
+        res = {"workload": "Qwen3-0.6B shape, random Q8_0 weights (tied embeddings, QK-RMSNorm), "
+                           "Q8_0 KV, batch 1, positions 8.." + str(8 + K - 1),
+               "ms_per_token": round(dt * 1e3, 3), "tokens_per_s": round(1 / dt, 1),
+               "weight_bytes": int(wbytes),
+               "weight_GBps": round(wbytes / dt / 1e9, 1),
+               "launches_per_token": cfg["n_layers"] * 14 + 4}
+        if orc.ref_lib("avx2") is not None:
+            def rel_diff(dev, ref):
+                return max(float(np.abs(dev[i] - ref[i]).max() / max(1.0, np.abs(ref[i]).max()))
+                           for i in range(len(ref)))
+            # per-token time of the reference without its load: 1 vs 5 tokens
+            t0 = time.perf_counter()
+            orc.ref_model_forward(path, toks[:1], cfg["vocab"], True, 0)
+            t1 = time.perf_counter()
+            ref_q8 = orc.ref_model_forward(path, toks[:5], cfg["vocab"], True, 0)
+            t2 = time.perf_counter()
+            cdt = max((t2 - t1) - (t1 - t0), 1e-9) / 4
+            # parity with an F32 KV (no quantisation of the appended rows: fp32
+            # summation order only), and the Q8_0-KV figure beside it
+            ref_f32 = orc.ref_model_forward(path, toks[:5], cfg["vocab"], False, 0)
+            with attn.Model(path, kv_q8=False) as m32:
+                dev_f32 = [m32.forward(toks[i], i) for i in range(5)]
+            res.update({"cpu_tokens_per_s": round(1 / cdt, 2),
+                        "cpu_kind": "reference model_forward (AVX2, OpenMP)",
+                        "cpu_threads": orc.max_threads(),
+                        "max_rel_logit_diff_vs_reference_f32_kv": rel_diff(dev_f32, ref_f32),
+                        "max_rel_logit_diff_vs_reference_q8_kv": rel_diff(first[:5], ref_q8),
+                        "note": "Q8_0 KV: appended rows can quantise one step apart where the "
+                                "two fp32 k/v differ in their last bits; the difference compounds "
+                                "over 28 layers (argmax unchanged)"})
+        log(f"model_forward: {res['ms_per_token']} ms/token ({res['tokens_per_s']} tokens/s, "
+            f"{res['weight_GBps']} GB/s of weights), cpu {res.get('cpu_tokens_per_s')} tokens/s, "
+            f"logits vs reference (F32 KV) {res.get('max_rel_logit_diff_vs_reference_f32_kv')}")
+        return res
+    finally:
+        os.unlink(path)
 
 
 def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):

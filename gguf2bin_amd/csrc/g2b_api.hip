@@ -371,6 +371,18 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
 
 }  // namespace
 
+// Decode attention of one sequence whose descriptor lives in device memory
+// (the kernels read pos from it), scheduled for any pos <= max_pos: the
+// launches stay valid from step to step, as a captured step graph needs.
+int g2b::attn_forward_device_seq(g2b_ctx *c, int32_t layer, const SeqDev *d_seq,
+                                 int32_t max_pos, float *q, const float *k, const float *v) {
+  if (!c || !d_seq) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  SeqDev none{};
+  return run_layers(c, d_seq, none, 1, max_pos, (int64_t)max_pos + 1, layer, 1, q, k, v, nullptr,
+                    0);
+}
+
 extern "C" {
 
 const char *g2b_strerror(int32_t code) {

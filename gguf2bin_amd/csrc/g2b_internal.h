@@ -198,6 +198,16 @@ struct GemvParams {
 hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s);
 hipError_t launch_fill_zero(float *out, int32_t n, hipStream_t s);
 
+}  // namespace g2b
+struct g2b_ctx;
+namespace g2b {
+// Decode attention (RoPE, append, attention, combine) of one sequence whose
+// descriptor lives in device memory - the kernels read pos from it - with
+// the schedule sized for any pos <= max_pos, so the same launches serve
+// every step (a captured step graph); the output overwrites q.
+int attn_forward_device_seq(g2b_ctx *c, int32_t layer, const SeqDev *d_seq, int32_t max_pos,
+                            float *q, const float *k, const float *v);
+
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {
   ShapeDev sh;

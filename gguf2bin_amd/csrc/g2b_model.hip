@@ -27,8 +27,11 @@ namespace {
 constexpr int kEwThreads = 256;
 
 // gguf_dequant of one embedding row (l2_codec.c:186-199) for the types the
-// device supports; the products are exact in fp32.
-__global__ void k_embed_row(float *out, const uint8_t *row, int32_t type, int32_t n) {
+// device supports; the products are exact in fp32.  The token comes from
+// device memory (checked against vocab on the host before it is written).
+__global__ void k_embed_row(float *out, const uint8_t *emb, const int32_t *tok, uint64_t stride,
+                            int32_t type, int32_t n) {
+  const uint8_t *row = emb + (size_t)(*tok) * stride;
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     float v;
     if (type == kTypeF32) {
@@ -113,6 +116,13 @@ struct g2b_model {
   void *kc = nullptr, *vc = nullptr;
   int32_t ctx_cap = 0;
   float *act = nullptr;  // x, xb, hb, hb2, q, k, v, logits (device)
+  // step inputs: the sequence descriptor (pos) and the token, in device
+  // memory so that a captured step graph reads them; pinned staging
+  uint8_t *d_step = nullptr, *h_step = nullptr;
+  SeqDev *d_seq = nullptr;
+  int32_t *d_tok = nullptr;
+  bool use_graph = true, graph_tried = false;
+  hipGraphExec_t exec = nullptr;
   float *x = nullptr, *xb = nullptr, *hb = nullptr, *hb2 = nullptr, *q = nullptr,
         *k = nullptr, *v = nullptr, *logits = nullptr;
   // slot_get's index (l5_model.c:34-45): per layer and role, and global
@@ -132,6 +142,9 @@ int g2b_model_free(g2b_model *m) {
   if (!m) return G2B_EINVAL;
   if (m->ctx) {
     (void)g2b_sync(m->ctx);
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->h_step) (void)hipHostFree(m->h_step);
+    if (m->d_step) (void)g2b_weights_free(m->ctx, m->d_step);
     if (m->kc || m->vc) (void)g2b_kv_free(m->ctx, m->kc, m->vc);
     if (m->dblob) (void)g2b_weights_free(m->ctx, m->dblob);
     if (m->act) (void)g2b_weights_free(m->ctx, m->act);
@@ -255,6 +268,14 @@ int g2b_model_load_g2bx(g2b_model **out, int32_t device, const char *path, int32
   m->k = p; p += up4(nkv);
   m->v = p; p += up4(nkv);
   m->logits = p;
+  if (int rc = g2b_weights_upload(m->ctx, nullptr, 64, (void **)&m->d_step)) return bail(rc, m);
+  if (hipHostMalloc((void **)&m->h_step, 64, hipHostMallocDefault) != hipSuccess) {
+    m->h_step = nullptr;
+    (void)hipGetLastError();
+    return bail(G2B_ENOMEM, m);
+  }
+  m->d_seq = reinterpret_cast<SeqDev *>(m->d_step);
+  m->d_tok = reinterpret_cast<int32_t *>(m->d_step + 32);
   g2b_g2bx_close(&g);
   *out = m;
   return G2B_OK;
@@ -272,19 +293,24 @@ int g2b_model_info(const g2b_model *m, g2b_model_cfg *cfg, int32_t *arch, int32_
 
 g2b_ctx *g2b_model_ctx(g2b_model *m) { return m ? m->ctx : nullptr; }
 
-int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
-  if (!m || !logits) return G2B_EINVAL;
+int g2b_model_use_graph(g2b_model *m, int32_t on) {
+  if (!m) return G2B_EINVAL;
+  m->use_graph = on != 0;
+  return G2B_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Every launch of one decode step, reading the token and pos from the step
+// inputs in device memory: the same sequence runs eagerly and is captured.
+int enqueue_step(g2b_model *m) {
   const g2b_model_cfg &c = m->cfg;
-  // the forward's own checks (l5_model.c:469-483)
-  if (pos < 0 || pos >= m->ctx_cap || token < 0 || token >= c.vocab) {
-    memset(logits, 0, (size_t)c.vocab * sizeof(float));
-    return pos < 0 || pos >= m->ctx_cap ? G2B_EPOS : G2B_EINVAL;
-  }
   const int32_t dim = c.dim, hid = c.hidden_dim;
   const int32_t nq = c.n_heads * c.head_dim, nkv = c.n_kv_heads * c.head_dim;
   g2b_ctx *cx = m->ctx;
   hipStream_t st = (hipStream_t)g2b_ctx_stream(cx);
-  if (hipSetDevice(m->device) != hipSuccess) return G2B_EDEVICE;
 #define G2B_MODEL_HIP(call)                        \
   do {                                             \
     if ((call) != hipSuccess) return G2B_EDEVICE; \
@@ -294,15 +320,12 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
     const int rc_ = (call);     \
     if (rc_) return rc_;        \
   } while (0)
-
   const g2b_slot *emb = m->get(G2B_R_TOK_EMBD, -1);
   if (!emb) return G2B_EINVAL;  // require_slot("tok_embd")
-  const uint64_t es = row_stride_of(emb->type, dim);
-  if ((uint64_t)(token + 1) * es > emb->nbytes) return G2B_EINVAL;
   hipLaunchKernelGGL(k_embed_row, dim3(ew_blocks(dim)), dim3(kEwThreads), 0, st, m->x,
-                     m->ptr(emb) + (size_t)token * es, (int32_t)emb->type, dim);
+                     m->ptr(emb), m->d_tok, row_stride_of(emb->type, dim), (int32_t)emb->type,
+                     dim);
   G2B_MODEL_HIP(hipGetLastError());
-
   for (int32_t L = 0; L < c.n_layers; L++) {
     const g2b_slot *an = m->get(G2B_R_ATTN_NORM, L);
     const g2b_slot *wq = m->get(G2B_R_ATTN_Q, L), *wk = m->get(G2B_R_ATTN_K, L),
@@ -317,9 +340,9 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
     G2B_MODEL_RC(g2b_matmul(cx, m->q, m->xb, m->ptr(wq), wq->type, dim, nq));
     G2B_MODEL_RC(g2b_matmul(cx, m->k, m->xb, m->ptr(wk), wk->type, dim, nkv));
     G2B_MODEL_RC(g2b_matmul(cx, m->v, m->xb, m->ptr(wv), wv->type, dim, nkv));
-    // QK-RMSNorm, RoPE, KV append, attention; the output over q
-    G2B_MODEL_RC(g2b_attn_forward(cx, L, pos, m->ctx_cap, m->kc, m->vc, m->q, m->k, m->v,
-                                  nullptr));
+    // QK-RMSNorm, RoPE, KV append, attention over the positions up to pos
+    // (scheduled for the whole context); the output over q
+    G2B_MODEL_RC(attn_forward_device_seq(cx, L, m->d_seq, m->ctx_cap - 1, m->q, m->k, m->v));
     G2B_MODEL_RC(g2b_matmul(cx, m->xb, m->q, m->ptr(wo), wo->type, nq, dim));
     hipLaunchKernelGGL(k_add, dim3(ew_blocks(dim)), dim3(kEwThreads), 0, st, m->x, m->xb, dim);
     G2B_MODEL_HIP(hipGetLastError());
@@ -344,10 +367,60 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
   if (!out) out = emb;  // tied embeddings (l5_model.c:602)
   if (out->type == 1) return G2B_EUNSUP;  // F16 logits matrix: no device GEMV
   G2B_MODEL_RC(g2b_matmul(cx, m->logits, m->x, m->ptr(out), out->type, dim, c.vocab));
-  G2B_MODEL_HIP(hipMemcpyAsync(logits, m->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost, st));
-  G2B_MODEL_HIP(hipStreamSynchronize(st));
 #undef G2B_MODEL_HIP
 #undef G2B_MODEL_RC
+  return G2B_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
+  if (!m || !logits) return G2B_EINVAL;
+  const g2b_model_cfg &c = m->cfg;
+  // the forward's own checks (l5_model.c:469-483)
+  if (pos < 0 || pos >= m->ctx_cap || token < 0 || token >= c.vocab) {
+    memset(logits, 0, (size_t)c.vocab * sizeof(float));
+    return pos < 0 || pos >= m->ctx_cap ? G2B_EPOS : G2B_EINVAL;
+  }
+  hipStream_t st = (hipStream_t)g2b_ctx_stream(m->ctx);
+  if (hipSetDevice(m->device) != hipSuccess) return G2B_EDEVICE;
+  // step inputs (the previous step's copies have completed: every forward
+  // ends with a stream synchronisation)
+  SeqDev sd{};
+  sd.pos = pos;
+  sd.ctx_cap = m->ctx_cap;
+  sd.k = (uint8_t *)m->kc;
+  sd.v = (uint8_t *)m->vc;
+  memcpy(m->h_step, &sd, sizeof sd);
+  memcpy(m->h_step + 32, &token, sizeof token);
+  if (hipMemcpyAsync(m->d_step, m->h_step, 64, hipMemcpyHostToDevice, st) != hipSuccess)
+    return G2B_EDEVICE;
+  if (m->exec && m->use_graph) {
+    if (hipGraphLaunch(m->exec, st) != hipSuccess) return G2B_EDEVICE;
+  } else {
+    if (int rc = enqueue_step(m)) return rc;
+    if (m->use_graph && !m->graph_tried) {
+      // capture the step once (every buffer it touches exists by now); on any
+      // failure the model keeps running eagerly
+      m->graph_tried = true;
+      hipGraph_t graph = nullptr;
+      if (hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) == hipSuccess) {
+        const int rc = enqueue_step(m);
+        const hipError_t e = hipStreamEndCapture(st, &graph);
+        if (rc == G2B_OK && e == hipSuccess && graph &&
+            hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0) != hipSuccess)
+          m->exec = nullptr;
+        if (graph) (void)hipGraphDestroy(graph);
+      }
+      (void)hipGetLastError();
+    }
+  }
+  if (hipMemcpyAsync(logits, m->logits, (size_t)c.vocab * 4, hipMemcpyDeviceToHost, st) !=
+      hipSuccess)
+    return G2B_EDEVICE;
+  if (hipStreamSynchronize(st) != hipSuccess) return G2B_EDEVICE;
   return G2B_OK;
 }
 

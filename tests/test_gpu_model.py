@@ -97,6 +97,21 @@ def test_forward_long_context(gpu_device, tmp_path):
     check(dev, ref, "long", True)
 
 
+@pytest.mark.parametrize("kv_q8", [False, True])
+def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
+    """Every forward after the first replays the captured step; stepped in
+    turn with an eager model of the same file (its launches one by one, with
+    the synchronisation that ends every forward between the replays), each
+    replay must give the eager step's logits bit for bit."""
+    p, cfg, rng = make(tmp_path, "qwen3_hd128_q8", seed=5)
+    toks = [int(t) for t in rng.integers(0, cfg["vocab"], 20)]
+    with attn.Model(p, kv_q8=kv_q8) as g, attn.Model(p, kv_q8=kv_q8) as e:
+        e.use_graph(False)
+        for i, t in enumerate(toks):
+            a, b = g.forward(t, i), e.forward(t, i)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+
+
 def test_tiny_g2bx(gpu_device):
     """The reference's own tiny model (all-zero Q4_0 weights: logits 0)."""
     ref_or_skip()
