@@ -33,7 +33,7 @@ EXPORTS = [
     "g2b_matmul_row_bytes", "g2b_matmul", "g2b_matmul_host", "g2b_weights_upload",
     "g2b_weights_free", "g2b_g2bx_open", "g2b_g2bx_close", "g2b_g2bx_slot",
     "g2b_model_load_g2bx", "g2b_model_free", "g2b_model_info", "g2b_model_ctx",
-    "g2b_model_forward", "g2b_model_use_graph",
+    "g2b_model_forward", "g2b_model_use_graph", "g2b_model_set_fused",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
@@ -139,6 +139,7 @@ def lib() -> C.CDLL:
             "g2b_model_ctx": ([vp], vp),
             "g2b_model_forward": ([vp, i32, i32, fp], C.c_int),
             "g2b_model_use_graph": ([vp, i32], C.c_int),
+            "g2b_model_set_fused": ([vp, i32], C.c_int),
             "g2b_matmul_row_bytes": ([i32, i32], C.c_size_t),
             "g2b_matmul": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
             "g2b_matmul_host": ([vp, fp, fp, vp, i32, i32, i32], C.c_int),
@@ -237,6 +238,11 @@ class Model:
     def use_graph(self, on: bool):
         """Replay the captured step graph (default) or keep every step eager."""
         lib().g2b_model_use_graph(self.h, 1 if on else 0)
+
+    def set_fused(self, on: bool):
+        """Fused GEMV launches (rmsnorm, SiLU x up and the residual inside
+        them; default) or every step as separate launches."""
+        lib().g2b_model_set_fused(self.h, 1 if on else 0)
 
     def forward_rc(self, token: int, pos: int):
         """(return code, logits) without raising."""

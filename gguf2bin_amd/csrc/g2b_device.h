@@ -110,6 +110,55 @@ __device__ __forceinline__ float half_bits_to_f32_hw(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// sum(x[i]^2), i < n, over a workgroup of 256 threads (x 16-byte aligned;
+// red: 4 floats of LDS), returned to every thread: thread t accumulates the
+// float4 pieces t, t + 256, ... in element order (eight loads in flight),
+// then, if t < n % 4, element 4 * (n / 4) + t; a tree per wave;
+// (w0 + w1) + (w2 + w3).  rmsnorm's sum (l3_math.c:21-37) in another fp32
+// order; one order for every kernel that normalises, so they agree bitwise.
+// STAGE: also xw[i] = x[i] * w[i] for i < 4 * (n / 4) (xw: LDS).
+template <bool STAGE>
+__device__ inline float wg256_sumsq_t(const float *x, int n, float *red, const float *w,
+                                      float *xw) {
+  const int t = threadIdx.x, n4 = n >> 2;
+  const float4 *x4 = reinterpret_cast<const float4 *>(x);
+  float s = 0.f;
+  for (int i0 = t; i0 < n4; i0 += 8 * 256) {
+    float4 v[8];
+    [[maybe_unused]] float4 g[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const bool in = i0 + 256 * k < n4;
+      v[k] = in ? x4[i0 + 256 * k] : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (STAGE) {
+        const int e = 4 * (i0 + 256 * k);
+        g[k] = in ? make_float4(w[e], w[e + 1], w[e + 2], w[e + 3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      s = fmaf(v[k].x, v[k].x, s);
+      s = fmaf(v[k].y, v[k].y, s);
+      s = fmaf(v[k].z, v[k].z, s);
+      s = fmaf(v[k].w, v[k].w, s);
+      if constexpr (STAGE) {
+        if (i0 + 256 * k < n4)
+          reinterpret_cast<float4 *>(xw)[i0 + 256 * k] =
+              make_float4(v[k].x * g[k].x, v[k].y * g[k].y, v[k].z * g[k].z, v[k].w * g[k].w);
+      }
+    }
+  }
+  if (t < (n & 3)) s = fmaf(x[4 * n4 + t], x[4 * n4 + t], s);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if ((t & 63) == 0) red[t >> 6] = s;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ inline float wg256_sumsq(const float *x, int n, float *red) {
+  return wg256_sumsq_t<false>(x, n, red, nullptr, nullptr);
+}
+
 // (int32)lroundf(r) as glibc on x86-64 gives it: round half away from zero,
 // out-of-range and NaN produce LONG_MIN, whose low 32 bits are 0.
 __device__ __forceinline__ int32_t lround_i32_like_host(float r) {

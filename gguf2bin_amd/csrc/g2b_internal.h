@@ -194,7 +194,31 @@ struct GemvParams {
   int32_t n_waves;     // waves of the launch
   int32_t vec4;        // F32: 16-byte loads allowed
   int32_t x_vec4;      // Q8_0 / Q4_0: x 16-byte aligned (x kept in registers)
+  // Fused forms (Q8_0 / Q4_0 with x in registers only: gemv_fusable).
+  // Segments: rows [0, d0) use w / out, [d0, d01) w1 / out1, [d01, d) w2 /
+  // out2 - matrices of one type and one n sharing x (Q/K/V, gate/up).  A
+  // plain launch has d0 = d01 = d.
+  const uint8_t *w1, *w2;
+  float *out1, *out2;
+  int32_t d0, d01;
+  // x as the rows read it: kProNone x; kProRmsnorm (x * nw) * (1 / sqrtf(
+  // sum(x^2) / n + eps)); kProSiluMul silu(x) * x2.
+  int32_t pro;
+  const float *nw, *x2;
+  float eps;
+  const float *res;    // segment 0: out = res + W x (res may be out itself)
 };
+constexpr int32_t kProNone = 0, kProRmsnorm = 1, kProSiluMul = 2;
+// Whether launch_gemv takes the fused forms for this type and row length.
+inline bool gemv_fusable(int32_t type, int32_t n) {
+  return (type == kTypeQ8_0 || type == kTypeQ4_0) && n > 0 && n % 32 == 0 && n / 32 <= 512;
+}
+// The prologues keep x * w or SiLU x up of all of x in LDS: n floats within
+// 60 KiB.
+constexpr int32_t kGemvProMaxN = 15360;
+inline bool gemv_fusable_pro(int32_t type, int32_t n) {
+  return gemv_fusable(type, n) && n <= kGemvProMaxN;
+}
 hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s);
 hipError_t launch_fill_zero(float *out, int32_t n, hipStream_t s);
 

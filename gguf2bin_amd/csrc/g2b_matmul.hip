@@ -138,6 +138,101 @@ __device__ __forceinline__ float block_dot(const BlockRaw<FMT> &r, const float *
   }
 }
 
+// Fused forms (GemvParams): rmsnorm (l3_math.c:21-50) as (x * w) * inv with
+// inv = 1 / sqrtf(sum(x^2) / n + eps), computed by every workgroup from the
+// whole of x in wg256_sumsq's order (the model's own rmsnorm kernel's);
+// x * w goes to LDS (xs: n floats, n a multiple of 32) in the same pass.
+__device__ __forceinline__ float wg_rms_stage(const GemvParams &P, float *xs) {
+  static_assert(kGemvThreads == 256, "wg256_sumsq");
+  __shared__ float red[kGemvThreads / 64];
+  const float sum = wg256_sumsq_t<true>(P.x, P.n, red, P.nw, xs);
+  return 1.f / sqrtf(sum / (float)P.n + P.eps);
+}
+
+// silu(x) * x2 (silu, l3_math.c:57-62, then the product of l5_model.c:595)
+// for the whole of x, once per workgroup, into LDS (xs: n floats; n is a
+// multiple of 32, x and x2 16-byte aligned): eight float4 pieces of each in
+// flight per thread.
+__device__ __forceinline__ void wg_silu_mul(const GemvParams &P, float *xs) {
+  const int n4 = P.n >> 2;
+  const float4 *g4 = reinterpret_cast<const float4 *>(P.x);
+  const float4 *u4 = reinterpret_cast<const float4 *>(P.x2);
+  for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * kGemvThreads) {
+    float4 g[8], u[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if (i0 + kGemvThreads * k < n4) {
+        g[k] = g4[i0 + kGemvThreads * k];
+        u[k] = u4[i0 + kGemvThreads * k];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      if (i0 + kGemvThreads * k < n4) {
+        float4 r;
+        r.x = (g[k].x / (1.f + expf(-g[k].x))) * u[k].x;
+        r.y = (g[k].y / (1.f + expf(-g[k].y))) * u[k].y;
+        r.z = (g[k].z / (1.f + expf(-g[k].z))) * u[k].z;
+        r.w = (g[k].w / (1.f + expf(-g[k].w))) * u[k].w;
+        reinterpret_cast<float4 *>(xs)[i0 + kGemvThreads * k] = r;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// x[i..i+4) as the rows read it: plain, rmsnorm'd (x * w from LDS, times
+// inv, as rmsnorm's AVX2 loop) or SiLU x up from LDS.  i is a multiple of 4,
+// x 16-byte aligned.
+__device__ __forceinline__ float4 pro_x4(const GemvParams &P, const float *xs, int i, float inv) {
+  if (P.pro == kProNone) return *reinterpret_cast<const float4 *>(P.x + i);
+  float4 v = *reinterpret_cast<const float4 *>(xs + i);
+  if (P.pro == kProRmsnorm) {
+    v.x *= inv;
+    v.y *= inv;
+    v.z *= inv;
+    v.w *= inv;
+  }
+  return v;
+}
+
+// A lane's x blocks (KB of them, blocks b0 + LPR * k below b_hi) in
+// registers, through the prologue.
+template <int LPR, int KB>
+__device__ __forceinline__ void lane_x(const GemvParams &P, const float *xs, int b0, int b_hi,
+                                       float inv, float (&xr)[KB][32]) {
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const int b = b0 + LPR * k;
+#pragma unroll
+    for (int j = 0; j < 32; j += 4) {
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (b < b_hi) v = pro_x4(P, xs, 32 * b + j, inv);
+      xr[k][j] = v.x;
+      xr[k][j + 1] = v.y;
+      xr[k][j + 2] = v.z;
+      xr[k][j + 3] = v.w;
+    }
+  }
+}
+
+// Row `row` of the launch's concatenated segments: its weights, and the
+// store of its result (segment 0 adds the residual res when given:
+// x[i] += xb[i], l5_model.c:583, :597).
+__device__ __forceinline__ const uint8_t *seg_row(const GemvParams &P, int row) {
+  if (row < P.d0) return P.w + (size_t)row * P.row_bytes;
+  if (row < P.d01) return P.w1 + (size_t)(row - P.d0) * P.row_bytes;
+  return P.w2 + (size_t)(row - P.d01) * P.row_bytes;
+}
+__device__ __forceinline__ void seg_store(const GemvParams &P, int row, float acc) {
+  if (row < P.d0)
+    P.out[row] = P.res ? P.res[row] + acc : acc;
+  else if (row < P.d01)
+    P.out1[row - P.d0] = acc;
+  else
+    P.out2[row - P.d01] = acc;
+}
+
 template <int LPR>
 __device__ __forceinline__ float lanes_sum(float v) {
 #pragma unroll
@@ -145,9 +240,10 @@ __device__ __forceinline__ float lanes_sum(float v) {
   return v;
 }
 
-// Q8_0 / Q4_0.  KB > 0: the lane's x blocks (KB of them) live in registers;
-// KB == -1: any nb, x staged once per workgroup in LDS; KB == 0: any nb, x
-// read per block through the cache.
+// Q8_0 / Q4_0.  KB > 0: the lane's x blocks (KB of them) live in registers,
+// prepared while the first weights are in flight (the fused forms: LDS of n
+// floats for SiLU x up); KB == -1: any nb, x staged once per workgroup in
+// LDS; KB == 0: any nb, x read per block through the cache.
 template <int FMT, int LPR, int KB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
   extern __shared__ float xs[];
@@ -172,24 +268,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
     }
     __syncthreads();
   }
-  if constexpr (KB > 0) {
-#pragma unroll
-    for (int k = 0; k < KB; k++) {
-      const int b = c + LPR * k;
-#pragma unroll
-      for (int j = 0; j < 32; j += 4) {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (b < nb) v = *reinterpret_cast<const float4 *>(P.x + 32 * b + j);
-        xr[k][j] = v.x;
-        xr[k][j + 1] = v.y;
-        xr[k][j + 2] = v.z;
-        xr[k][j + 3] = v.w;
-      }
-    }
-  }
   const int stride = P.n_waves;
-  for (int s0 = gw; s0 < P.steps; s0 += stride * kGemvUnroll) {
-    if constexpr (KB > 0) {
+  if constexpr (KB > 0) {
+    // Every wave runs the first trip (rows or not): its weights are issued,
+    // then the workgroup prepares x (barriers) while they are in flight.
+    for (int s0 = gw, trip = 0;; s0 += stride * kGemvUnroll, trip++) {
       BlockRaw<FMT> raw[kGemvUnroll][KB];
       int row[kGemvUnroll];
       bool ok[kGemvUnroll];
@@ -202,10 +285,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
         for (int k = 0; k < KB; k++) {
           const int b = c + LPR * k;
           if (ok[u] && b < nb)
-            load_block<FMT>(raw[u][k], P.w + (size_t)row[u] * P.row_bytes + (size_t)b * BB);
+            load_block<FMT>(raw[u][k], seg_row(P, row[u]) + (size_t)b * BB);
           else
             zero_block<FMT>(raw[u][k]);
         }
+      }
+      if (trip == 0) {
+        float inv = 1.f;
+        if (P.pro == kProSiluMul) wg_silu_mul(P, xs);
+        if (P.pro == kProRmsnorm) inv = wg_rms_stage(P, xs);
+        lane_x<LPR, KB>(P, xs, c, nb, inv, xr);
       }
 #pragma unroll
       for (int u = 0; u < kGemvUnroll; u++) {
@@ -213,9 +302,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
 #pragma unroll
         for (int k = 0; k < KB; k++) acc += block_dot<FMT>(raw[u][k], xr[k]);
         acc = lanes_sum<LPR>(acc);
-        if (ok[u] && c == 0) P.out[row[u]] = acc;
+        if (ok[u] && c == 0) seg_store(P, row[u], acc);
       }
-    } else {
+      if (s0 + stride * kGemvUnroll >= P.steps) break;
+    }
+  } else {
+    for (int s0 = gw; s0 < P.steps; s0 += stride * kGemvUnroll) {
       // any number of blocks: kGemvGroup of the lane's blocks in flight at a time
 #pragma unroll 1
       for (int u = 0; u < kGemvUnroll; u++) {
@@ -253,6 +345,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
 // partial sums in LDS.  Workgroups stride over steps of RPS rows.
 template <int FMT, int LPR, int KB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
+  extern __shared__ float xs[];  // the fused SiLU x up: n floats
   constexpr int RPS = 64 / LPR;
   constexpr int BB = FMT == 1 ? 34 : 18;
   constexpr int NW = kGemvThreads / 64;
@@ -261,22 +354,11 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
   const int rr = lane / LPR, c = lane % LPR;
   const int nb = P.nb, nbw = (nb + NW - 1) / NW;
   const int b_lo = wave * nbw, b_hi = min(nb, b_lo + nbw);
-  float xr[KB][32];
-#pragma unroll
-  for (int k = 0; k < KB; k++) {
-    const int b = b_lo + c + LPR * k;
-#pragma unroll
-    for (int j = 0; j < 32; j += 4) {
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (b < b_hi) v = *reinterpret_cast<const float4 *>(P.x + 32 * b + j);
-      xr[k][j] = v.x;
-      xr[k][j + 1] = v.y;
-      xr[k][j + 2] = v.z;
-      xr[k][j + 3] = v.w;
-    }
-  }
   const int stride = gridDim.x;
-  for (int s0 = blockIdx.x; s0 < P.steps; s0 += stride * kGemvUnroll) {
+  float xr[KB][32];
+  // Every workgroup runs the first trip: its weights are issued, then x is
+  // prepared (barriers) while they are in flight.
+  for (int s0 = blockIdx.x, trip = 0;; s0 += stride * kGemvUnroll, trip++) {
     BlockRaw<FMT> raw[kGemvUnroll][KB];
 #pragma unroll
     for (int u = 0; u < kGemvUnroll; u++) {
@@ -287,10 +369,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
       for (int k = 0; k < KB; k++) {
         const int b = b_lo + c + LPR * k;
         if (ok && b < b_hi)
-          load_block<FMT>(raw[u][k], P.w + (size_t)row * P.row_bytes + (size_t)b * BB);
+          load_block<FMT>(raw[u][k], seg_row(P, row) + (size_t)b * BB);
         else
           zero_block<FMT>(raw[u][k]);
       }
+    }
+    if (trip == 0) {
+      float inv = 1.f;
+      if (P.pro == kProSiluMul) wg_silu_mul(P, xs);
+      if (P.pro == kProRmsnorm) inv = wg_rms_stage(P, xs);
+      lane_x<LPR, KB>(P, xs, b_lo + c, b_hi, inv, xr);
     }
 #pragma unroll
     for (int u = 0; u < kGemvUnroll; u++) {
@@ -306,9 +394,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
       const int s = s0 + u * stride;
       const int row = s * RPS + r;
       if (s < P.steps && row < P.d)
-        P.out[row] = (part[u][0][r] + part[u][1][r]) + (part[u][2][r] + part[u][3][r]);
+        seg_store(P, row, (part[u][0][r] + part[u][1][r]) + (part[u][2][r] + part[u][3][r]));
     }
     __syncthreads();
+    if (s0 + stride * kGemvUnroll >= P.steps) break;
   }
 }
 
@@ -343,12 +432,17 @@ __global__ void k_fill_zero(float *out, int32_t n) {
   if (i < n) out[i] = 0.f;
 }
 
+// LDS of the register-x forms: x * w or SiLU x up of the whole of x
+inline size_t pro_lds(const GemvParams &p) {
+  return p.pro != kProNone ? (size_t)p.n * sizeof(float) : 0;
+}
+
 template <int FMT, int LPR>
 hipError_t launch_q_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
   const dim3 blk(kGemvThreads);
   switch (kb) {
-    case 1: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 1>), grid, blk, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 2>), grid, blk, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 1>), grid, blk, pro_lds(p), s, p); break;
+    case 2: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 2>), grid, blk, pro_lds(p), s, p); break;
     case -1:
       hipLaunchKernelGGL((k_gemv_q<FMT, LPR, -1>), grid, blk, (size_t)p.nb * 128u, s, p);
       break;
@@ -360,9 +454,9 @@ hipError_t launch_q_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
 template <int FMT, int LPR>
 hipError_t launch_split_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
   if (kb == 1)
-    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 1>), grid, dim3(kGemvThreads), 0, s, p);
+    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 1>), grid, dim3(kGemvThreads), pro_lds(p), s, p);
   else
-    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 2>), grid, dim3(kGemvThreads), 0, s, p);
+    hipLaunchKernelGGL((k_gemv_q_split<FMT, LPR, 2>), grid, dim3(kGemvThreads), pro_lds(p), s, p);
   return hipGetLastError();
 }
 
@@ -396,6 +490,15 @@ hipError_t launch_fill_zero(float *out, int32_t n, hipStream_t s) {
 
 hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   const int waves_per_wg = kGemvThreads / 64;
+  if (p.d0 == 0 && p.d01 == 0) p.d0 = p.d01 = p.d;  // one segment
+  const bool fused = p.pro != kProNone || p.res || p.d0 != p.d || p.d01 != p.d;
+  // the fused forms exist where x lives in registers (gemv_fusable, x aligned)
+  if (fused && (!gemv_fusable(type, p.n) || ((uintptr_t)p.x & 15u) || p.d0 > p.d01 ||
+                p.d01 > p.d || (p.pro == kProRmsnorm && !p.nw) ||
+                (p.pro != kProNone && p.n > kGemvProMaxN) ||
+                (p.pro == kProSiluMul && (!p.x2 || ((uintptr_t)p.x2 & 15u)))))
+    return hipErrorInvalidValue;
+  if (fused) p.x_vec4 = 1;
   if (type == kTypeF32) {
     p.row_bytes = (uint32_t)p.n * 4u;
     p.vec4 = ((uintptr_t)p.w % 16 == 0 && (uintptr_t)p.x % 16 == 0 && p.n % 4 == 0) ? 1 : 0;

@@ -53,19 +53,15 @@ __global__ void k_embed_row(float *out, const uint8_t *emb, const int32_t *tok, 
   }
 }
 
-// rmsnorm (l3_math.c:21-50) by one workgroup: o may alias x (the final norm
-// runs in place): every read of x happens before the barrier that precedes
-// the writes.
+// rmsnorm (l3_math.c:21-50) by one workgroup of kEwThreads: o may alias x
+// (the final norm runs in place): every read of x happens before the barrier
+// that precedes the writes.
 __global__ __launch_bounds__(kEwThreads) void k_rmsnorm(float *o, const float *x, const float *w,
                                                         int32_t n, float eps) {
   __shared__ float red[kEwThreads / 64];
-  float s = 0.f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(x[i], x[i], s);
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-  __syncthreads();
-  float sum = 0.f;
-  for (int wv = 0; wv < (int)(blockDim.x >> 6); wv++) sum += red[wv];
+  // (the fused GEMVs' order, so both give the same normalised x)
+  static_assert(kEwThreads == 256, "wg256_sumsq");
+  const float sum = wg256_sumsq(x, n, red);
   const float inv = 1.f / sqrtf(sum / (float)n + eps);
   for (int i = threadIdx.x; i < n; i += blockDim.x) o[i] = (x[i] * w[i]) * inv;
 }
@@ -108,7 +104,8 @@ using namespace g2b;
 
 struct g2b_model {
   g2b_ctx *ctx = nullptr;
-  int32_t device = 0;
+  int32_t device = 0, n_cu = 1;
+  bool fuse = true;  // fused GEMV launches where the weight types allow them
   g2b_model_cfg cfg{};
   int32_t arch = 0, flags = 0;
   std::vector<g2b_slot> slots;  // the table; offsets into dblob
@@ -183,6 +180,14 @@ int g2b_model_load_g2bx(g2b_model **out, int32_t device, const char *path, int32
   }
   g2b_model *m = new g2b_model;
   m->device = device;
+  {
+    int n_cu = 0;
+    if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) {
+      (void)hipGetLastError();
+      n_cu = 1;
+    }
+    m->n_cu = n_cu > 0 ? n_cu : 1;
+  }
   m->cfg = c;
   m->arch = g.arch;
   m->flags = g.flags;
@@ -299,6 +304,18 @@ int g2b_model_use_graph(g2b_model *m, int32_t on) {
   return G2B_OK;
 }
 
+int g2b_model_set_fused(g2b_model *m, int32_t on) {
+  if (!m) return G2B_EINVAL;
+  if (m->fuse != (on != 0)) {
+    m->fuse = on != 0;
+    // a captured step holds the other launches: capture again
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    m->exec = nullptr;
+    m->graph_tried = false;
+  }
+  return G2B_OK;
+}
+
 }  // extern "C"
 
 namespace {
@@ -326,6 +343,23 @@ int enqueue_step(g2b_model *m) {
                      m->ptr(emb), m->d_tok, row_stride_of(emb->type, dim), (int32_t)emb->type,
                      dim);
   G2B_MODEL_HIP(hipGetLastError());
+  // A plain GEMV, or a fused one (launch_gemv: rmsnorm or SiLU x up on x,
+  // segments sharing x, a residual added to the output).
+  auto gemv = [&](float *out, const float *x, const g2b_slot *w, int32_t n, int32_t d) {
+    return g2b_matmul(cx, out, x, m->ptr(w), w->type, n, d);
+  };
+  auto fused = [&](GemvParams p, int32_t type) {
+    return launch_gemv(p, type, m->n_cu, st) == hipSuccess ? G2B_OK : G2B_EDEVICE;
+  };
+  auto rmsnorm = [&](float *o, const float *x, const g2b_slot *w) {
+    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kEwThreads), 0, st, o, x,
+                       (const float *)m->ptr(w), dim, c.eps);
+    return hipGetLastError() == hipSuccess ? G2B_OK : G2B_EDEVICE;
+  };
+  auto add = [&](float *x, const float *y, int32_t n) {
+    hipLaunchKernelGGL(k_add, dim3(ew_blocks(n)), dim3(kEwThreads), 0, st, x, y, n);
+    return hipGetLastError() == hipSuccess ? G2B_OK : G2B_EDEVICE;
+  };
   for (int32_t L = 0; L < c.n_layers; L++) {
     const g2b_slot *an = m->get(G2B_R_ATTN_NORM, L);
     const g2b_slot *wq = m->get(G2B_R_ATTN_Q, L), *wk = m->get(G2B_R_ATTN_K, L),
@@ -334,39 +368,116 @@ int enqueue_step(g2b_model *m) {
     const g2b_slot *wg = m->get(G2B_R_FFN_GATE, L), *wu = m->get(G2B_R_FFN_UP, L),
                    *wd = m->get(G2B_R_FFN_DOWN, L);
     if (!an || !wq || !wk || !wv || !wo || !fn || !wg || !wu || !wd) return G2B_EINVAL;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kEwThreads), 0, st, m->xb, m->x,
-                       (const float *)m->ptr(an), dim, c.eps);
-    G2B_MODEL_HIP(hipGetLastError());
-    G2B_MODEL_RC(g2b_matmul(cx, m->q, m->xb, m->ptr(wq), wq->type, dim, nq));
-    G2B_MODEL_RC(g2b_matmul(cx, m->k, m->xb, m->ptr(wk), wk->type, dim, nkv));
-    G2B_MODEL_RC(g2b_matmul(cx, m->v, m->xb, m->ptr(wv), wv->type, dim, nkv));
+    // rmsnorm, then Q, K, V (l5_model.c:495-503): one launch when the three
+    // matrices share a type the fused GEMV takes
+    if (m->fuse && wq->type == wk->type && wq->type == wv->type &&
+        gemv_fusable_pro(wq->type, dim)) {
+      GemvParams p{};
+      p.out = m->q;
+      p.out1 = m->k;
+      p.out2 = m->v;
+      p.x = m->x;
+      p.w = m->ptr(wq);
+      p.w1 = m->ptr(wk);
+      p.w2 = m->ptr(wv);
+      p.n = dim;
+      p.d0 = nq;
+      p.d01 = nq + nkv;
+      p.d = nq + 2 * nkv;
+      p.x_vec4 = 1;
+      p.pro = kProRmsnorm;
+      p.nw = (const float *)m->ptr(an);
+      p.eps = c.eps;
+      G2B_MODEL_RC(fused(p, wq->type));
+    } else {
+      G2B_MODEL_RC(rmsnorm(m->xb, m->x, an));
+      G2B_MODEL_RC(gemv(m->q, m->xb, wq, dim, nq));
+      G2B_MODEL_RC(gemv(m->k, m->xb, wk, dim, nkv));
+      G2B_MODEL_RC(gemv(m->v, m->xb, wv, dim, nkv));
+    }
     // QK-RMSNorm, RoPE, KV append, attention over the positions up to pos
     // (scheduled for the whole context); the output over q
     G2B_MODEL_RC(attn_forward_device_seq(cx, L, m->d_seq, m->ctx_cap - 1, m->q, m->k, m->v));
-    G2B_MODEL_RC(g2b_matmul(cx, m->xb, m->q, m->ptr(wo), wo->type, nq, dim));
-    hipLaunchKernelGGL(k_add, dim3(ew_blocks(dim)), dim3(kEwThreads), 0, st, m->x, m->xb, dim);
-    G2B_MODEL_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kEwThreads), 0, st, m->xb, m->x,
-                       (const float *)m->ptr(fn), dim, c.eps);
-    G2B_MODEL_HIP(hipGetLastError());
-    G2B_MODEL_RC(g2b_matmul(cx, m->hb, m->xb, m->ptr(wg), wg->type, dim, hid));
-    G2B_MODEL_RC(g2b_matmul(cx, m->hb2, m->xb, m->ptr(wu), wu->type, dim, hid));
-    hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(hid)), dim3(kEwThreads), 0, st, m->hb, m->hb2,
-                       hid);
-    G2B_MODEL_HIP(hipGetLastError());
-    G2B_MODEL_RC(g2b_matmul(cx, m->xb, m->hb, m->ptr(wd), wd->type, hid, dim));
-    hipLaunchKernelGGL(k_add, dim3(ew_blocks(dim)), dim3(kEwThreads), 0, st, m->x, m->xb, dim);
-    G2B_MODEL_HIP(hipGetLastError());
+    // Wo and the residual (l5_model.c:580-583)
+    if (m->fuse && gemv_fusable(wo->type, nq)) {
+      GemvParams p{};
+      p.out = m->x;
+      p.res = m->x;
+      p.x = m->q;
+      p.w = m->ptr(wo);
+      p.n = nq;
+      p.d = dim;
+      p.x_vec4 = 1;
+      G2B_MODEL_RC(fused(p, wo->type));
+    } else {
+      G2B_MODEL_RC(gemv(m->xb, m->q, wo, nq, dim));
+      G2B_MODEL_RC(add(m->x, m->xb, dim));
+    }
+    // rmsnorm, gate and up (l5_model.c:585-593)
+    if (m->fuse && wg->type == wu->type && gemv_fusable_pro(wg->type, dim)) {
+      GemvParams p{};
+      p.out = m->hb;
+      p.out1 = m->hb2;
+      p.x = m->x;
+      p.w = m->ptr(wg);
+      p.w1 = m->ptr(wu);
+      p.n = dim;
+      p.d0 = hid;
+      p.d01 = 2 * hid;
+      p.d = 2 * hid;
+      p.x_vec4 = 1;
+      p.pro = kProRmsnorm;
+      p.nw = (const float *)m->ptr(fn);
+      p.eps = c.eps;
+      G2B_MODEL_RC(fused(p, wg->type));
+    } else {
+      G2B_MODEL_RC(rmsnorm(m->xb, m->x, fn));
+      G2B_MODEL_RC(gemv(m->hb, m->xb, wg, dim, hid));
+      G2B_MODEL_RC(gemv(m->hb2, m->xb, wu, dim, hid));
+    }
+    // SiLU(gate) x up, down and the residual (l5_model.c:594-597)
+    if (m->fuse && gemv_fusable_pro(wd->type, hid)) {
+      GemvParams p{};
+      p.out = m->x;
+      p.res = m->x;
+      p.x = m->hb;
+      p.x2 = m->hb2;
+      p.pro = kProSiluMul;
+      p.w = m->ptr(wd);
+      p.n = hid;
+      p.d = dim;
+      p.x_vec4 = 1;
+      G2B_MODEL_RC(fused(p, wd->type));
+    } else {
+      hipLaunchKernelGGL(k_silu_mul, dim3(ew_blocks(hid)), dim3(kEwThreads), 0, st, m->hb, m->hb2,
+                         hid);
+      G2B_MODEL_HIP(hipGetLastError());
+      G2B_MODEL_RC(gemv(m->xb, m->hb, wd, hid, dim));
+      G2B_MODEL_RC(add(m->x, m->xb, dim));
+    }
   }
+  // final rmsnorm and the logits (l5_model.c:600-605)
   const g2b_slot *on = m->get(G2B_R_OUT_NORM, -1);
   if (!on) return G2B_EINVAL;
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kEwThreads), 0, st, m->x, m->x,
-                     (const float *)m->ptr(on), dim, c.eps);
-  G2B_MODEL_HIP(hipGetLastError());
   const g2b_slot *out = m->get(G2B_R_OUTPUT, -1);
   if (!out) out = emb;  // tied embeddings (l5_model.c:602)
   if (out->type == 1) return G2B_EUNSUP;  // F16 logits matrix: no device GEMV
-  G2B_MODEL_RC(g2b_matmul(cx, m->logits, m->x, m->ptr(out), out->type, dim, c.vocab));
+  if (m->fuse && gemv_fusable_pro(out->type, dim)) {
+    GemvParams p{};
+    p.out = m->logits;
+    p.x = m->x;
+    p.w = m->ptr(out);
+    p.n = dim;
+    p.d = c.vocab;
+    p.x_vec4 = 1;
+    p.pro = kProRmsnorm;
+    p.nw = (const float *)m->ptr(on);
+    p.eps = c.eps;
+    G2B_MODEL_RC(fused(p, out->type));
+  } else {
+    G2B_MODEL_RC(rmsnorm(m->x, m->x, on));
+    G2B_MODEL_RC(gemv(m->logits, m->x, out, dim, c.vocab));
+  }
 #undef G2B_MODEL_HIP
 #undef G2B_MODEL_RC
   return G2B_OK;

@@ -103,6 +103,17 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits);
  * forward does not change the captured step. */
 int g2b_model_use_graph(g2b_model *m, int32_t on);
 
+/* on = 1 (the default): where the weight types allow it (Q8_0 / Q4_0, rows of
+ * at most 512 blocks; Q, K and V of one type; gate and up of one type), each
+ * layer runs as six launches: rmsnorm + Q/K/V, the attention path (two), Wo
+ * + the residual, rmsnorm + gate/up, SiLU(gate) * up + down + the residual;
+ * the final rmsnorm goes into the logits GEMV.  on = 0: rmsnorm, SiLU * up
+ * and the residual adds as launches of their own, one GEMV per matrix (the
+ * path F32 weights always take).  The same arithmetic either way, apart
+ * from the order of rmsnorm's fp32 sum of squares.  Changing it drops a
+ * captured step; the next forward captures again. */
+int g2b_model_set_fused(g2b_model *m, int32_t on);
+
 #ifdef __cplusplus
 }
 #endif

@@ -266,9 +266,14 @@ def random_matrix_bytes(rng, t: int, rows: int, n: int, gain: float = 1.0) -> by
 def random_model_slots(rng, cfg: dict, flags: int, mat_type: int, emb_type: int,
                        out_type=None):
     """Every slot model_forward reads, random: norms near 1 (F32), matrices
-    of mat_type, embeddings of emb_type, an untied output of out_type (None:
-    tied to the embeddings, F_TIE_EMBD)."""
+    of mat_type (a GGML type id, or a dict role -> type with "*" for the
+    rest), embeddings of emb_type, an untied output of out_type (None: tied
+    to the embeddings, F_TIE_EMBD)."""
     d, h, nl = cfg["dim"], cfg["hidden_dim"], cfg["n_layers"]
+    types = mat_type if isinstance(mat_type, dict) else {"*": mat_type}
+
+    def mt(role):
+        return types.get(role, types["*"])
     nq, nkv, hd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"], cfg["head_dim"]
     G = 0xFFFF
 
@@ -281,15 +286,13 @@ def random_model_slots(rng, cfg: dict, flags: int, mat_type: int, emb_type: int,
     if out_type is not None:
         slots.append((R_OUTPUT, G, out_type, random_matrix_bytes(rng, out_type, cfg["vocab"], d)))
     for L in range(nl):
-        slots += [(R_ATTN_NORM, L, 0, norm(d)),
-                  (R_ATTN_Q, L, mat_type, random_matrix_bytes(rng, mat_type, nq, d)),
-                  (R_ATTN_K, L, mat_type, random_matrix_bytes(rng, mat_type, nkv, d)),
-                  (R_ATTN_V, L, mat_type, random_matrix_bytes(rng, mat_type, nkv, d)),
-                  (R_ATTN_O, L, mat_type, random_matrix_bytes(rng, mat_type, d, nq))]
+        slots += [(R_ATTN_NORM, L, 0, norm(d))]
+        slots += [(r, L, mt(r), random_matrix_bytes(rng, mt(r), rows, n))
+                  for r, rows, n in ((R_ATTN_Q, nq, d), (R_ATTN_K, nkv, d), (R_ATTN_V, nkv, d),
+                                     (R_ATTN_O, d, nq))]
         if flags & F_QK_NORM:
             slots += [(R_ATTN_Q_NORM, L, 0, norm(hd)), (R_ATTN_K_NORM, L, 0, norm(hd))]
-        slots += [(R_FFN_NORM, L, 0, norm(d)),
-                  (R_FFN_GATE, L, mat_type, random_matrix_bytes(rng, mat_type, h, d)),
-                  (R_FFN_UP, L, mat_type, random_matrix_bytes(rng, mat_type, h, d)),
-                  (R_FFN_DOWN, L, mat_type, random_matrix_bytes(rng, mat_type, d, h))]
+        slots += [(R_FFN_NORM, L, 0, norm(d))]
+        slots += [(r, L, mt(r), random_matrix_bytes(rng, mt(r), rows, n))
+                  for r, rows, n in ((R_FFN_GATE, h, d), (R_FFN_UP, h, d), (R_FFN_DOWN, d, h))]
     return slots

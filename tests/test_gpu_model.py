@@ -18,8 +18,8 @@ import os
 import numpy as np
 import pytest
 
-from helpers import (F_QK_NORM, F_TIE_EMBD, R_ATTN_Q, R_FFN_DOWN, random_model_slots,
-                     write_g2bx)
+from helpers import (F_QK_NORM, F_TIE_EMBD, R_ATTN_K, R_ATTN_O, R_ATTN_Q, R_FFN_DOWN,
+                     random_model_slots, write_g2bx)
 from oracle import orc
 from gguf2bin_amd import attn
 
@@ -41,6 +41,17 @@ CASES = {
     "qwen2_f32": (dict(dim=128, hidden_dim=192, n_layers=2, n_heads=4, n_kv_heads=4, vocab=200,
                        seq_len=64, head_dim=32, eps=1e-5, rope_theta=1e4),
                   attn.ARCH_QWEN2, 0, 0, 0, 0),
+    # Q/K/V of mixed types and an F32 Wo (their plain launches), gate/up in one
+    # launch, down over 144 blocks per row (the split-row GEMV with SiLU x up)
+    "mixed_types": (dict(dim=256, hidden_dim=4608, n_layers=2, n_heads=4, n_kv_heads=2,
+                         vocab=300, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
+                    attn.ARCH_QWEN3, F_QK_NORM, {"*": 8, R_ATTN_K: 2, R_ATTN_O: 0, R_FFN_DOWN: 2},
+                    8, 2),
+    # rows of 132 blocks: rmsnorm + Q/K/V, rmsnorm + gate/up and rmsnorm +
+    # logits on the split-row GEMV
+    "wide_dim_q4": (dict(dim=4224, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=4,
+                         vocab=128, seq_len=64, head_dim=64, eps=1e-5, rope_theta=5e5),
+                    attn.ARCH_LLAMA, 0, 2, 0, 8),
 }
 
 
@@ -109,6 +120,24 @@ def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
         e.use_graph(False)
         for i, t in enumerate(toks):
             a, b = g.forward(t, i), e.forward(t, i)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
+
+
+@pytest.mark.parametrize("name", ["qwen3_q8_tied", "llama_q4_f16emb", "mixed_types",
+                                  "wide_dim_q4"])
+def test_fused_launches_match_separate(gpu_device, tmp_path, name):
+    """The fused GEMV launches (rmsnorm, SiLU x up and the residual inside
+    them, Q/K/V and gate/up as segments of one launch) against the same step
+    as separate launches, both eager: the same arithmetic in the same order,
+    so the logits agree bit for bit."""
+    p, cfg, rng = make(tmp_path, name, seed=9)
+    toks = [int(t) for t in rng.integers(0, cfg["vocab"], 12)]
+    with attn.Model(p, kv_q8=True) as f, attn.Model(p, kv_q8=True) as u:
+        f.use_graph(False)
+        u.use_graph(False)
+        u.set_fused(False)
+        for i, t in enumerate(toks):
+            a, b = f.forward(t, i), u.forward(t, i)
             assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"step {i}"
 
 
