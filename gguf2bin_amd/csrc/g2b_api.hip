@@ -216,7 +216,10 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
 
   const int32_t nh = c->shape.n_heads, hd = c->shape.head_dim;
   const size_t nq = (size_t)nh * hd;
-  const bool fast = decode_fast_available(c->sh);
+  // (k_layer reads q, k and v as 16-byte pieces; other pointers take the
+  // generic kernels)
+  const bool fast = decode_fast_available(c->sh) &&
+                    (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) == 0;
 
   DecodeParams dp{};
   dp.sh = c->sh;
@@ -356,7 +359,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     G2B_HIP(c, hipEventRecord(ev0, c->stream));
   }
   if (use_wq) c->wq_reset = true;  // until both launches below are queued
-  G2B_HIP(c, launch_decode(dp, n_layers, c->stream, &used_fast));
+  G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
   G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {

@@ -263,7 +263,8 @@ bool decode_fast_available(const ShapeDev &sh) {
   const int group = sh.n_heads / sh.n_kv_heads;
   if (group < 1 || group > 4) return false;
   const int lanes = sh.n_kv_heads * (sh.head_dim / fast_chunk(sh));
-  return lanes <= 64;
+  // (k_layer's setup loads at most 8192 q and 2048 k floats per thread set)
+  return lanes <= 64 && sh.n_heads * sh.head_dim <= 8192 && sh.n_kv_heads * sh.head_dim <= 2048;
 }
 
 template <int FMT, int HD>
@@ -277,8 +278,9 @@ static hipError_t launch_hd(const DecodeParams &p, int group, int n_layers, hipS
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int *used_fast) {
-  if (decode_fast_available(p.sh)) {
+hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, bool fast,
+                         int *used_fast) {
+  if (fast && decode_fast_available(p.sh)) {
     if (used_fast) *used_fast = 1;
     const int group = p.sh.n_heads / p.sh.n_kv_heads;
     if (p.sh.kv_q8)

@@ -38,25 +38,31 @@ __host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
 }
 
 // k_layer's dynamic LDS: [0, rows) holds the rotated q and the new k and v
-// (floats) before the stream starts and the waves' staging regions
-// (stage_rows > 0) during it;
-// then the new K and V rows (row_pad bytes each) and n_heads floats of
-// QK-RMSNorm scratch.  After the stream, the wave merge of the partials
-// ([wave][head][kPartHead + head_dim] floats) reuses everything from 0.
+// (floats) and a transposed copy of q and k (head_dim x (n_heads +
+// n_kv_heads + 1) floats, for the QK-RMSNorm sums) before the stream starts
+// and the waves' staging regions (stage_rows > 0) during it;
+// then the new K and V rows (row_pad bytes each), n_heads + n_kv_heads
+// floats (rounded up to 4) of QK-RMSNorm factors and 3 * head_dim floats of
+// setup inputs (the q and k norm weights, the cos/sin row of pos).  After the stream, the wave
+// merge of the partials ([wave][head][kPartHead + head_dim] floats) reuses
+// everything from 0.
 struct LdsLayout {
   uint32_t rows, row_pad, total;
 };
 __host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
   const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
-  const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u);
+  const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u) +
+                       (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
   const uint32_t stage = (uint32_t)kWavesPerSplit * 2u * (uint32_t)stage_rows * sh.row_bytes;
   const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)sh.n_heads *
                          (uint32_t)(kPartHead + sh.head_dim) * 4u;
   LdsLayout l;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;
   l.rows = pre > stage ? pre : stage;
-  const uint32_t need = l.rows + 2u * l.row_pad + (uint32_t)sh.n_heads * 4u;
+  const uint32_t need =
+      l.rows + 2u * l.row_pad +
+      (uint32_t)(((sh.n_heads + sh.n_kv_heads + 3) & ~3) + 3 * sh.head_dim) * 4u;
   l.total = need > merge ? need : merge;
   return l;
 }
@@ -150,11 +156,13 @@ __host__ __device__ inline void piece_range(const PieceMap &m, int32_t c, int32_
 // Launchers: return hipSuccess or the launch error.
 hipError_t launch_append_batch(const AppendParams &p, int n_layers, hipStream_t s);
 hipError_t launch_append_rows(const AppendParams &p, int layer, int n_rows, hipStream_t s);
-// Specialised shapes: one launch does RoPE, append and attention (k_layer).
-// Generic shapes: launch_append_batch, then this (k_decode_generic).  Both
-// are followed by launch_combine.  *used_fast tells which ran.
+// Specialised shapes (decode_fast_available, and fast set by the caller):
+// one launch does RoPE, append and attention (k_layer).  Otherwise:
+// launch_append_batch, then this (k_decode_generic).  Both are followed by
+// launch_combine.  *used_fast tells which ran.
 // Returns hipErrorInvalidValue when split_len is too large for the generic kernel.
-hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, int *used_fast);
+hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, bool fast,
+                         int *used_fast);
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 // Whether a specialised decode kernel exists for this shape.
 bool decode_fast_available(const ShapeDev &sh);

@@ -268,7 +268,8 @@ __device__ __forceinline__ float fast_exp2(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
 
-// The new row of the workgroup that owns position pos: [QK-RMSNorm,] RoPE(k), then F32 copy
+// Work-queue visits: the new row of the workgroup that owns position pos:
+// [QK-RMSNorm,] RoPE(k), then F32 copy
 // or Q8_0 quantisation of k and v into LDS (rowk, rowv), then a copy of both
 // rows to the caches.  The workgroup later reads pos from LDS, so no other
 // workgroup and no cache level is involved.  Every thread calls it.
@@ -320,6 +321,260 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
   const uint32_t *lk = reinterpret_cast<const uint32_t *>(rowk);
   const uint32_t *lv = reinterpret_cast<const uint32_t *>(rowv);
   for (uint32_t i = threadIdx.x; i < sh.row_bytes / 4; i += blockDim.x) {
+    gk[i] = lk[i];
+    gv[i] = lv[i];
+  }
+}
+
+// The setup of a static-schedule visit (every thread calls it; owns_new is
+// uniform), shaped for latency: the visit is one workgroup's whole job.
+// Threads own rope groups - four pairs (j, j + hd/2) for NEOX, (2j, 2j + 1)
+// for LLaMA, j = 4i..4i+3, of one q head or (owner) new k head - and bring
+// their two float4s of x, of the norm weights and of the cos/sin row of pos
+// (l3_math.c:65-102) into registers in one round of global loads, with the
+// owner's v.  QK-RMSNorm (l3_math.c:107-114) needs each head's sum of
+// squares first: one thread per head, left to right with every product
+// rounded, inv = 1/sqrtf(ss/hd + eps) with IEEE division and square root,
+// over a transposed LDS copy.  Then (w * x) * inv and the rotation in
+// registers, into qrot (rotated q) and kr (rotated new k).  With DIG (Q8_0
+// KV), the q digit planes of every (head, CD-element chunk) - make_digits of
+// qrot * qscale - are computed once here, four threads per chunk, into dig.
+// Then, for the owner, F32 copy or Q8_0 quantisation of k and v into LDS
+// (rowk, rowv) and a copy of both rows to the caches (kv_store,
+// l5_model.c:235-247).  The owner later reads pos from LDS, so no other
+// workgroup and no cache level is involved.
+// scr: norm factors (n_heads + n_kv_heads floats).  tr: hd x (n_heads +
+// n_kv_heads + 1) floats holding q and k transposed in float4 groups -
+// elements 4i..4i+3 of head H at float4 [i][H] - so each head's sum reads
+// 16-byte pieces without bank conflicts; dig (DIG) reuses tr once the sums
+// are done: dig_stride<CD>() dwords per chunk, chunk h * (hd / CD) + c.
+template <int CD>
+constexpr int dig_stride() {
+  return (3 * (CD / 4) + 1 + 3) & ~3;  // three planes, the unit, 16-byte rows
+}
+
+template <int HD, int CD, bool DIG>
+__device__ inline void visit_setup(const ShapeDev &sh, const SeqDev &sd, int layer, bool owns_new,
+                                   const float *qi, const float *ki, const float *vi,
+                                   const float *rope, const NormDev &norm, float qscale,
+                                   float *qrot, float *kr, float *vr, uint8_t *rowk,
+                                   uint8_t *rowv, float *scr, float *tr) {
+  constexpr int half = HD / 2;
+  constexpr int gph = half / 4;  // rope groups per head
+  static_assert(half % 4 == 0, "four pairs per group");
+  const int nh = sh.n_heads, nkvh = sh.n_kv_heads;
+  const int nkv = nkvh * HD;
+  const float *wq = norm_weights(norm, layer, 0, HD);
+  const float *wk = owns_new ? norm_weights(norm, layer, 1, HD) : nullptr;
+  const float *cs = (sh.rope_on && rope) ? rope + (size_t)sd.pos * HD : nullptr;
+  const bool llama = sh.arch_llama != 0;
+  float *inv = scr;
+  const int nt = nh + nkvh + 1;  // float4 row length of tr
+  // group gi < ngq: q head gi / gph; else k head (gi - ngq) / gph.  A
+  // thread's groups gi = t, t + 256, ... all sit at i4 = t % gph (256 is a
+  // multiple of gph), so its weights and cos/sin are one set.
+  static_assert(kThreads % gph == 0, "one group position per thread");
+  constexpr int kG = 5;  // groups per thread: nq <= 8192 and nkv <= 2048
+  const int ngq = nh * gph, ng = ngq + (owns_new ? nkvh * gph : 0);
+  const int i4 = (int)threadIdx.x % gph;
+  const int oa = llama ? 8 * i4 : 4 * i4, ob = llama ? 8 * i4 + 4 : half + 4 * i4;
+  float4 xa[kG], xb[kG], qwa, qwb, kwa, kwb, c0, c1;
+#pragma unroll
+  for (int u = 0; u < kG; u++) {
+    const int gi = (int)threadIdx.x + kThreads * u;
+    if (gi < ng) {
+      const bool is_q = gi < ngq;
+      const float *x = is_q ? qi + (gi / gph) * HD : ki + ((gi - ngq) / gph) * HD;
+      xa[u] = *reinterpret_cast<const float4 *>(x + oa);
+      xb[u] = *reinterpret_cast<const float4 *>(x + ob);
+    }
+  }
+  if (wq) {
+    qwa = *reinterpret_cast<const float4 *>(wq + oa);
+    qwb = *reinterpret_cast<const float4 *>(wq + ob);
+  }
+  if (wk) {
+    kwa = *reinterpret_cast<const float4 *>(wk + oa);
+    kwb = *reinterpret_cast<const float4 *>(wk + ob);
+  }
+  if (cs) {
+    c0 = *reinterpret_cast<const float4 *>(cs + 8 * i4);
+    c1 = *reinterpret_cast<const float4 *>(cs + 8 * i4 + 4);
+  }
+  // the owner's v, as it is (two pieces per thread: nkv <= 2048)
+  const int nv4 = owns_new ? nkv / 4 : 0;
+  const int v0 = (int)threadIdx.x, v1 = (int)threadIdx.x + kThreads;
+  float4 tv0 = make_float4(0.f, 0.f, 0.f, 0.f), tv1 = tv0;
+  if (v0 < nv4) tv0 = reinterpret_cast<const float4 *>(vi)[v0];
+  if (v1 < nv4) tv1 = reinterpret_cast<const float4 *>(vi)[v1];
+  if (v0 < nv4) reinterpret_cast<float4 *>(vr)[v0] = tv0;
+  if (v1 < nv4) reinterpret_cast<float4 *>(vr)[v1] = tv1;
+  // QK-RMSNorm factors over the transposed copy: thread h < nh for q head h,
+  // nh + g for k head g
+  if (wq || wk) {
+#pragma unroll
+    for (int u = 0; u < kG; u++) {
+      const int gi = (int)threadIdx.x + kThreads * u;
+      if (gi < ng) {
+        const bool is_q = gi < ngq;
+        if (is_q ? wq != nullptr : wk != nullptr) {
+          const int H = is_q ? gi / gph : nh + (gi - ngq) / gph;
+          // the group's elements as float4s of consecutive j: LLaMA's two
+          // pieces already are; NEOX's a and b pieces are j = 4i4.. and
+          // half + 4i4..
+          const int ia = llama ? 2 * i4 : i4, ib = llama ? 2 * i4 + 1 : gph + i4;
+          reinterpret_cast<float4 *>(tr)[ia * nt + H] = xa[u];
+          reinterpret_cast<float4 *>(tr)[ib * nt + H] = xb[u];
+        }
+      }
+    }
+    __syncthreads();
+    for (int h = threadIdx.x; h < nh + nkvh; h += kThreads) {
+      const bool is_q = h < nh;
+      if (is_q ? !wq : !wk) continue;
+      float ss = 0.f;
+#pragma unroll 8
+      for (int i = 0; i < HD / 4; i++) {
+        const float4 x = reinterpret_cast<const float4 *>(tr)[i * nt + h];
+        float sq = x.x * x.x;
+        ss = ss + sq;
+        sq = x.y * x.y;
+        ss = ss + sq;
+        sq = x.z * x.z;
+        ss = ss + sq;
+        sq = x.w * x.w;
+        ss = ss + sq;
+      }
+      inv[h] = __fdiv_rn(1.f, sqrtf(__fdiv_rn(ss, (float)HD) + norm.eps));
+    }
+    __syncthreads();
+  }
+  // (w * x) * inv, then the rotation, in registers; into qrot / kr
+#pragma unroll
+  for (int u = 0; u < kG; u++) {
+    const int gi = (int)threadIdx.x + kThreads * u;
+    if (gi < ng) {
+      const bool is_q = gi < ngq;
+      const int h = is_q ? gi / gph : (gi - ngq) / gph;
+      const float4 wa = is_q ? qwa : kwa, wb = is_q ? qwb : kwb;
+      float a[4], b[4], fa[4], fb[4];
+      if (llama) {
+        a[0] = xa[u].x; b[0] = xa[u].y; a[1] = xa[u].z; b[1] = xa[u].w;
+        a[2] = xb[u].x; b[2] = xb[u].y; a[3] = xb[u].z; b[3] = xb[u].w;
+        fa[0] = wa.x; fb[0] = wa.y; fa[1] = wa.z; fb[1] = wa.w;
+        fa[2] = wb.x; fb[2] = wb.y; fa[3] = wb.z; fb[3] = wb.w;
+      } else {
+        a[0] = xa[u].x; a[1] = xa[u].y; a[2] = xa[u].z; a[3] = xa[u].w;
+        b[0] = xb[u].x; b[1] = xb[u].y; b[2] = xb[u].z; b[3] = xb[u].w;
+        fa[0] = wa.x; fa[1] = wa.y; fa[2] = wa.z; fa[3] = wa.w;
+        fb[0] = wb.x; fb[1] = wb.y; fb[2] = wb.z; fb[3] = wb.w;
+      }
+      if (is_q ? wq != nullptr : wk != nullptr) {
+        const float f = inv[is_q ? h : nh + h];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          a[k] = (fa[k] * a[k]) * f;
+          b[k] = (fb[k] * b[k]) * f;
+        }
+      }
+      if (cs) {
+        rope_pair(a[0], b[0], c0.x, c0.y);
+        rope_pair(a[1], b[1], c0.z, c0.w);
+        rope_pair(a[2], b[2], c1.x, c1.y);
+        rope_pair(a[3], b[3], c1.z, c1.w);
+      }
+      float *xh = (is_q ? qrot : kr) + h * HD;
+      if (llama) {
+        *reinterpret_cast<float4 *>(xh + oa) = make_float4(a[0], b[0], a[1], b[1]);
+        *reinterpret_cast<float4 *>(xh + ob) = make_float4(a[2], b[2], a[3], b[3]);
+      } else {
+        *reinterpret_cast<float4 *>(xh + oa) = make_float4(a[0], a[1], a[2], a[3]);
+        *reinterpret_cast<float4 *>(xh + ob) = make_float4(b[0], b[1], b[2], b[3]);
+      }
+    }
+  }
+  __syncthreads();
+  if constexpr (DIG) {
+    // make_digits per (head, chunk): thread quarter k of a chunk takes its
+    // elements k*CD/4 .. (k+1)*CD/4 - 1; the chunk maximum over the quarter's
+    // four lanes (consecutive threads)
+    constexpr int QE = CD / 4;
+    uint32_t *dig = reinterpret_cast<uint32_t *>(tr);
+    const int nch = nh * (HD / CD);
+    for (int it = threadIdx.x; it < 4 * nch; it += kThreads) {
+      const int ch = it >> 2, k = it & 3;
+      const float *src = qrot + ch * CD + k * QE;
+      float q[QE];
+#pragma unroll
+      for (int j = 0; j < QE; j += 4) {
+        const float4 v4 = *reinterpret_cast<const float4 *>(src + j);
+        q[j] = v4.x * qscale;
+        q[j + 1] = v4.y * qscale;
+        q[j + 2] = v4.z * qscale;
+        q[j + 3] = v4.w * qscale;
+      }
+      float mx = 0.f;
+#pragma unroll
+      for (int j = 0; j < QE; j++) mx = fmaxf(mx, fabsf(q[j]));
+      mx = fmaxf(mx, __shfl_xor(mx, 1));
+      mx = fmaxf(mx, __shfl_xor(mx, 2));
+      int e = 0;
+      (void)frexpf(mx, &e);
+      const float up = ldexpf(1.f, 22 - e);
+      uint32_t d[3][QE / 4];
+#pragma unroll
+      for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+        for (int j = 0; j < QE / 4; j++) d[pl][j] = 0u;
+#pragma unroll
+      for (int j = 0; j < QE; j++) {
+        const int m = (int)rintf(q[j] * up);
+        const int d0 = ((m + 128) & 255) - 128;
+        const int m1 = (m - d0) >> 8;
+        const int d1 = ((m1 + 128) & 255) - 128;
+        const int d2 = (m1 - d1) >> 8;
+        const int sh8 = 8 * (j & 3);
+        d[0][j >> 2] |= ((uint32_t)d0 & 0xffu) << sh8;
+        d[1][j >> 2] |= ((uint32_t)d1 & 0xffu) << sh8;
+        d[2][j >> 2] |= ((uint32_t)d2 & 0xffu) << sh8;
+      }
+      uint32_t *o = dig + ch * dig_stride<CD>();
+#pragma unroll
+      for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+        for (int j = 0; j < QE / 4; j++) o[pl * (CD / 4) + k * (QE / 4) + j] = d[pl][j];
+      if (k == 0) o[3 * (CD / 4)] = __float_as_uint(ldexpf(1.f, e - 22));
+    }
+  }
+  if (owns_new) {
+    if (sh.kv_q8) {
+      // four lanes per block (a multiple of 4 items, so a block's four
+      // lanes are active together)
+      const int nb = (nkv + 31) / 32;
+      for (int it = threadIdx.x; it < 8 * nb; it += kThreads) {
+        const int b = it >> 2, part = it & 3;
+        const bool is_k = b < nb;
+        const int bb = is_k ? b : b - nb;
+        const int cnt = min(32, nkv - 32 * bb);
+        q8_quant_block_x4((is_k ? kr : vr) + 32 * bb, cnt, (is_k ? rowk : rowv) + 34 * bb, part);
+      }
+    } else {
+      float *fk = reinterpret_cast<float *>(rowk), *fv = reinterpret_cast<float *>(rowv);
+      for (int e = threadIdx.x; e < nkv; e += kThreads) {
+        fk[e] = kr[e];
+        fv[e] = vr[e];
+      }
+    }
+  }
+  if (!DIG && !owns_new) return;  // qrot was published by the barrier above
+  __syncthreads();
+  if (!owns_new) return;
+  const size_t off = ((size_t)layer * (size_t)sd.ctx_cap + (size_t)sd.pos) * sh.row_bytes;
+  uint32_t *gk = reinterpret_cast<uint32_t *>(sd.k + off);
+  uint32_t *gv = reinterpret_cast<uint32_t *>(sd.v + off);
+  const uint32_t *lk = reinterpret_cast<const uint32_t *>(rowk);
+  const uint32_t *lv = reinterpret_cast<const uint32_t *>(rowv);
+  for (uint32_t i = threadIdx.x; i < sh.row_bytes / 4; i += kThreads) {
     gk[i] = lk[i];
     gv[i] = lv[i];
   }
@@ -393,7 +648,8 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
   uint8_t *rowk = lds + ll.rows;
   uint8_t *rowv = rowk + ll.row_pad;
-  float *inv = reinterpret_cast<float *>(rowv + ll.row_pad);
+  float *scr = reinterpret_cast<float *>(rowv + ll.row_pad);  // norm factors, setup inputs
+  float *trq = reinterpret_cast<float *>(lds + nq * 4 + 2 * ((nkv * 4 + 15) & ~15u));
 
   // One visit of unit (seq, li): positions [t0, tend) from HBM (static
   // mode) or the unit's claimed pieces (work queue), plus pos itself when
@@ -404,7 +660,6 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
                    int pslot, int32_t *ctr) {
     const int layer = P.layer0 + li;
     const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
-    const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
     const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
     const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
     // Register staging (STG 2): the next chunk's 16-byte pieces, lane l
@@ -451,49 +706,80 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     if constexpr (STG == 0) {
       if (t0 + wave * PPW < tend) fetch(t0 + wave * PPW, ka, va);
     }
-    {
-      // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by
-      // pair as the append does (l3_math.c:74-101)
-      const float *qi = P.q_in + sidx * nq;
-      if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
-        for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
+    if constexpr (WQ) {
+      {
+        // [QK-RMSNorm (l3_math.c:107-114),] RoPE(q) for every head, pair by
+        // pair as the append does (l3_math.c:74-101)
+        const float *cs = (P.sh.rope_on && P.rope) ? P.rope + (size_t)sd.pos * HD : nullptr;
+        const float *qi = P.q_in + sidx * nq;
+        if (const float *wq = norm_weights(P.norm, layer, 0, HD)) {
+          for (int e = threadIdx.x; e < (int)nq; e += blockDim.x) qrot[e] = qi[e];
+          __syncthreads();
+          qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, scr);
+          qi = qrot;  // rotate in place: each pair is read and written by one thread
+        }
+        constexpr int half = HD / 2;
+        for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
+          const int h = pr / half, j = pr - h * half;
+          int ia, ib;
+          rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
+          float a = qi[h * HD + ia], b = qi[h * HD + ib];
+          if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+          qrot[h * HD + ia] = a;
+          qrot[h * HD + ib] = b;
+        }
+      }
+      if (owns_new)  // (its barriers also publish qrot)
+        append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv,
+                       P.rope, P.norm, kr, vr, rowk, rowv, scr);
+      else
         __syncthreads();
-        qk_rmsnorm_block(qrot, n_heads, HD, wq, P.norm.eps, inv);
-        qi = qrot;  // rotate in place: each pair is read and written by one thread
-      }
-      constexpr int half = HD / 2;
-      for (int pr = threadIdx.x; pr < n_heads * half; pr += blockDim.x) {
-        const int h = pr / half, j = pr - h * half;
-        int ia, ib;
-        rope_pair_index(P.sh.arch_llama, j, half, ia, ib);
-        float a = qi[h * HD + ia], b = qi[h * HD + ib];
-        if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
-        qrot[h * HD + ia] = a;
-        qrot[h * HD + ib] = b;
-      }
+    } else {
+      // one round of loads, QK-RMSNorm, RoPE, the digit planes (Q8_0 KV)
+      // and the owner's append
+      visit_setup<HD, CD, FMT == 1>(P.sh, sd, layer, owns_new, P.q_in + sidx * nq,
+                                    P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope, P.norm,
+                                    P.qscale, qrot, kr, vr, rowk, rowv, scr, trq);
     }
-    if (owns_new)  // (its barriers also publish qrot)
-      append_new_row(P.sh, sd, layer, sd.pos, P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope,
-                     P.norm, kr, vr, rowk, rowv, inv);
-    else
-      __syncthreads();
+    constexpr bool kDig = FMT == 1 && !WQ;  // the digit planes come from the setup
 
-    float q[G][CD];
-#pragma unroll
-    for (int i = 0; i < G; i++)
-#pragma unroll
-      for (int j = 0; j < CD; j += 4) {
-        const float4 v4 =
-            *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
-        q[i][j + 0] = v4.x * P.qscale;
-        q[i][j + 1] = v4.y * P.qscale;
-        q[i][j + 2] = v4.z * P.qscale;
-        q[i][j + 3] = v4.w * P.qscale;
-      }
+    // q in registers: F32 rows take the values, Q8_0 rows the digit planes
+    // (from the setup's LDS copy, or made here from the values)
+    [[maybe_unused]] float q[G][CD];
     [[maybe_unused]] QDigits<CD> qd[G];
-    if constexpr (FMT == 1) {
+    if constexpr (kDig) {
+      const uint32_t *dig = reinterpret_cast<const uint32_t *>(trq);
 #pragma unroll
-      for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
+      for (int i = 0; i < G; i++) {
+        const uint32_t *o = dig + ((g * G + i) * (HD / CD) + c) * dig_stride<CD>();
+#pragma unroll
+        for (int pl = 0; pl < 3; pl++)
+#pragma unroll
+          for (int j = 0; j < CD / 4; j += 4) {
+            const uint4 v4 = *reinterpret_cast<const uint4 *>(o + pl * (CD / 4) + j);
+            qd[i].d[pl][j] = v4.x;
+            qd[i].d[pl][j + 1] = v4.y;
+            qd[i].d[pl][j + 2] = v4.z;
+            qd[i].d[pl][j + 3] = v4.w;
+          }
+        qd[i].unit = __uint_as_float(o[3 * (CD / 4)]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; i++)
+#pragma unroll
+        for (int j = 0; j < CD; j += 4) {
+          const float4 v4 =
+              *reinterpret_cast<const float4 *>(qrot + (size_t)(g * G + i) * HD + c * CD + j);
+          q[i][j + 0] = v4.x * P.qscale;
+          q[i][j + 1] = v4.y * P.qscale;
+          q[i][j + 2] = v4.z * P.qscale;
+          q[i][j + 3] = v4.w * P.qscale;
+        }
+      if constexpr (FMT == 1) {
+#pragma unroll
+        for (int i = 0; i < G; i++) qd[i] = make_digits<CD>(q[i]);
+      }
     }
     if constexpr (STG != 0) __syncthreads();  // every wave has its q: staging may overwrite qrot
 
