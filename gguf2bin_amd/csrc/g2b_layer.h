@@ -1104,23 +1104,29 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       }
     }
     __syncthreads();
+    // (four elements of one head per thread and step)
     const size_t wstr = (size_t)n_heads * pstr;
-    for (int e = threadIdx.x; e < n_heads * HD; e += blockDim.x) {
-      const int h = e / HD, d = e - h * HD;
+    for (int e4 = threadIdx.x; e4 < n_heads * (HD / 4); e4 += blockDim.x) {
+      const int h = e4 / (HD / 4), d = 4 * (e4 - h * (HD / 4));
       const float *pw = ws + (size_t)h * pstr;
       float M = pw[0];
 #pragma unroll
       for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
-      float o = 0.f, lsum = 0.f;
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      float lsum = 0.f;
 #pragma unroll
       for (int w = 0; w < kWavesPerSplit; w++) {
         const float f = exp2f(pw[w * wstr] - M);
-        o = fmaf(pw[w * wstr + kPartHead + d], f, o);
+        const float4 a = *reinterpret_cast<const float4 *>(pw + w * wstr + kPartHead + d);
+        o.x = fmaf(a.x, f, o.x);
+        o.y = fmaf(a.y, f, o.y);
+        o.z = fmaf(a.z, f, o.z);
+        o.w = fmaf(a.w, f, o.w);
         lsum = fmaf(pw[w * wstr + 1], f, lsum);
       }
       float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
                             (size_t)pslot) * pstr;
-      pp[kPartHead + d] = o;
+      *reinterpret_cast<float4 *>(pp + kPartHead + d) = o;
       if (d == 0) {
         pp[0] = M;
         pp[1] = lsum;
