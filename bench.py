@@ -244,6 +244,8 @@ def main():
     ap.add_argument("--sweep-splits", default="", help="comma list: time layer-serial per split")
     ap.add_argument("--sweep-variants", default="",
                     help="semicolon list of split,chunk,stage,piece: time layer-serial and fused")
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the whole-decode-step leg (model_forward), printed as its JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -254,6 +256,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     hip.set_device(0)
+    if args.model_only:
+        print(json.dumps({"model_forward": model_leg(args)}), flush=True)
+        return
 
     w = Workload(args.config, args, args.n_seq)
     ctx, shape, poss, caps, kvs = w.ctx, w.shape, w.poss, w.caps, w.kvs

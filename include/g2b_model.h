@@ -98,9 +98,9 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits);
 /* The first forward runs its launches one by one and then captures them as a
  * HIP graph (token and pos are read from device memory; the attention is
  * scheduled for the whole context), which every later forward replays: one
- * launch per step instead of ~14 per layer.  on = 0 keeps every step eager
- * (same launches, same results).  Tuning the model's context after the first
- * forward does not change the captured step. */
+ * graph launch per step instead of six launches per layer.  on = 0 keeps
+ * every step eager (same launches, same results).  Tuning the model's context
+ * after the first forward does not change the captured step. */
 int g2b_model_use_graph(g2b_model *m, int32_t on);
 
 /* on = 1 (the default): where the weight types allow it (Q8_0 / Q4_0, rows of

@@ -192,14 +192,15 @@ MODES = {
 
 
 def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, norms=None,
-                   setup=None, tune=None):
+                   setup=None, tune=None, misalign=0):
     """n_seq ragged sequences, all layers: device (one fused call or layer by
     layer) against the oracle, sequence by sequence.  tune: None or the
     g2b_ctx_tune arguments for the context.  norms: None, or
     (q_norm, k_norm, eps) with q_norm/k_norm None or indexable by layer (an
     entry None: that layer has no such weights); the oracle side normalises
     its inputs with them, and they are set on the context unless setup(ctx)
-    is given to do that itself."""
+    is given to do that itself.  misalign: byte offset of q, k and v in their
+    device buffers (not a multiple of 16: the generic kernels run)."""
     n_seq, nL = len(caps), o.n_layers
     rng_seed = seed * 1000
     qn, kn, eps = norms if norms else (None, None, 1e-6)
@@ -232,21 +233,28 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
             q = orc.normal(seed + 1, nL * n_seq * o.nq).reshape(nL, n_seq, o.nq)
             k = orc.normal(seed + 2, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
             v = orc.normal(seed + 3, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
-            qd, kd, vd = hip.to_device(q), hip.to_device(k), hip.to_device(v)
+            if misalign:
+                qd, kd, vd = (hip.DeviceBuffer(a.nbytes + 64) for a in (q, k, v))
+                for buf, a in ((qd, q), (kd, k), (vd, v)):
+                    buf.upload(a, misalign)
+            else:
+                qd, kd, vd = hip.to_device(q), hip.to_device(k), hip.to_device(v)
+            base = misalign
             stride = max(poss) + 1
             att = hip.DeviceBuffer(nL * n_seq * o.n_heads * stride * 4) if want_att else None
             ctx.batch_begin([(p, c, s.k, s.v) for p, c, s in zip(poss, caps, seqs)])
             if fused:
-                ctx.attn_layers(0, nL, qd.ptr, kd.ptr, vd.ptr, att.ptr if att else None, stride)
+                ctx.attn_layers(0, nL, qd.ptr + base, kd.ptr + base, vd.ptr + base,
+                                att.ptr if att else None, stride)
             else:
                 for L in range(nL):
-                    off_q = L * n_seq * o.nq * 4
-                    off_k = L * n_seq * o.nkv * 4
+                    off_q = base + L * n_seq * o.nq * 4
+                    off_k = base + L * n_seq * o.nkv * 4
                     off_a = L * n_seq * o.n_heads * stride * 4
                     ctx.attn_layers(L, 1, qd.ptr + off_q, kd.ptr + off_k, vd.ptr + off_k,
                                     (att.ptr + off_a) if att else None, stride)
             ctx.sync()
-            out = qd.download(np.float32, q.size).reshape(q.shape)
+            out = qd.download(np.float32, q.size, base).reshape(q.shape)
             w = (att.download(np.float32, nL * n_seq * o.n_heads * stride)
                  .reshape(nL, n_seq, o.n_heads, stride) if att else None)
             dev_kv = [s.download() for s in seqs]
@@ -276,6 +284,16 @@ def test_batched_ragged_vs_oracle(gpu_device, name, mode):
     fused, tune = MODES[mode]
     print(f"[batch] {name} mode={mode}", flush=True)
     run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused, tune=tune)
+
+
+@pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3"])
+def test_unaligned_qkv_take_generic_kernels(gpu_device, name):
+    """q/k/v that are not 16-byte aligned (the fast kernel reads 16-byte
+    pieces): the call runs the generic kernels, with the same parity."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    print(f"[unaligned] {name}", flush=True)
+    run_batch_case(o, [1, 37, 300], [0, 36, 211], seed=7, fused=False, misalign=4)
 
 
 QKN_SHAPES = {
