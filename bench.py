@@ -474,8 +474,9 @@ def model_leg(args):
                "ms_per_token": round(dt * 1e3, 3), "tokens_per_s": round(1 / dt, 1),
                "weight_bytes": int(wbytes),
                "weight_GBps": round(wbytes / dt / 1e9, 1),
-               # embedding, 6 per layer (fused GEMVs, attention and combine), logits
-               "launches_per_token": cfg["n_layers"] * 6 + 2}
+               # embedding, 5 per layer (four fused GEMVs and the attention: one
+               # split, no combine, at these positions), logits
+               "launches_per_token": cfg["n_layers"] * 5 + 2}
         if orc.ref_lib("avx2") is not None:
             def rel_diff(dev, ref):
                 return max(float(np.abs(dev[i] - ref[i]).max() / max(1.0, np.abs(ref[i]).max()))

@@ -205,7 +205,8 @@ int32_t choose_split(const g2b_ctx *c, int64_t slots, int64_t total_pos, int32_t
 
 int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_seq,
                int32_t max_pos, int64_t total_pos, int32_t layer0, int32_t n_layers, float *q,
-               const float *k, const float *v, float *att, int32_t att_stride) {
+               const float *k, const float *v, float *att, int32_t att_stride,
+               bool dry = false) {
   if (layer0 < 0 || n_layers < 1 || layer0 + n_layers > c->shape.n_layers)
     return fail(c, G2B_EINVAL, "layers [%d,%d) outside [0,%d)", layer0, layer0 + n_layers,
                 c->shape.n_layers);
@@ -318,6 +319,9 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     dp.split_len = split_len;
   }
   dp.max_splits = max_splits;
+  // one split per unit: the decode kernel writes the output, no combine
+  const bool direct = fast && !use_wq && max_splits == 1 && !att;
+  dp.direct_out = direct ? 1 : 0;
 
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              (size_t)(kPartHead + hd);
@@ -327,6 +331,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   }
   dp.part = c->part;
   dp.q_rot = c->qrot;
+  if (dry) return G2B_OK;  // (the buffers this schedule needs exist now)
 
   if (!fast) {  // generic shapes: append, decode, combine
     AppendParams ap{};
@@ -361,7 +366,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   if (use_wq) c->wq_reset = true;  // until both launches below are queued
   G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
-  G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
+  if (!direct || !used_fast) G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {
     // this launch dirtied its set; the combine zeroed the other one
     c->wq_dirty[c->wq_set] = std::max<int32_t>(c->wq_dirty[c->wq_set], (int32_t)n_units + 1);
@@ -384,6 +389,15 @@ int g2b::attn_forward_device_seq(g2b_ctx *c, int32_t layer, const SeqDev *d_seq,
   SeqDev none{};
   return run_layers(c, d_seq, none, 1, max_pos, (int64_t)max_pos + 1, layer, 1, q, k, v, nullptr,
                     0);
+}
+
+int g2b::attn_reserve_device_seq(g2b_ctx *c, int32_t max_pos, float *q, const float *k,
+                                 const float *v) {
+  if (!c) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  SeqDev none{};
+  return run_layers(c, nullptr, none, 1, max_pos, (int64_t)max_pos + 1, 0, 1, q, k, v, nullptr, 0,
+                    true);
 }
 
 extern "C" {

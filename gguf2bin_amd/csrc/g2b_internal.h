@@ -115,6 +115,11 @@ struct DecodeParams {
   int32_t piece_len;    // positions per small claimed piece (a multiple of stage_rows)
   int32_t piece_big;    // positions per big piece (a multiple of piece_len)
   int32_t n_layers_call;
+  // Static schedule with one split per unit (max_splits == 1, no weights
+  // output): k_layer writes the normalised output over q itself and no
+  // k_combine runs - the value k_combine would give for one partial,
+  // (float)((double)acc / (double)l).
+  int32_t direct_out;
 };
 constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte line each
 constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit
@@ -239,6 +244,10 @@ namespace g2b {
 // every step (a captured step graph); the output overwrites q.
 int attn_forward_device_seq(g2b_ctx *c, int32_t layer, const SeqDev *d_seq, int32_t max_pos,
                             float *q, const float *k, const float *v);
+// The buffers (RoPE table, split partials, counters) of that schedule, with
+// nothing launched - before a stream capture, which must not allocate.
+int attn_reserve_device_seq(g2b_ctx *c, int32_t max_pos, float *q, const float *k,
+                            const float *v);
 
 // Synthetic fill (bench / full-size tests): see g2b_synth.h.
 struct SynthParams {

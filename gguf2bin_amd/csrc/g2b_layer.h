@@ -1124,6 +1124,15 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         o.w = fmaf(a.w, f, o.w);
         lsum = fmaf(pw[w * wstr + 1], f, lsum);
       }
+      if (!WQ && P.direct_out) {
+        // the only partial of the unit: the output itself, over q
+        float *out = P.q_out + sidx * nq + (size_t)h * HD + d;
+        const double L = (double)lsum;
+        *reinterpret_cast<float4 *>(out) =
+            make_float4((float)((double)o.x / L), (float)((double)o.y / L),
+                        (float)((double)o.z / L), (float)((double)o.w / L));
+        continue;
+      }
       float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)h) * (size_t)P.max_splits +
                             (size_t)pslot) * pstr;
       *reinterpret_cast<float4 *>(pp + kPartHead + d) = o;

@@ -118,7 +118,7 @@ struct g2b_model {
   uint8_t *d_step = nullptr, *h_step = nullptr;
   SeqDev *d_seq = nullptr;
   int32_t *d_tok = nullptr;
-  bool use_graph = true, graph_tried = false;
+  bool use_graph = false, graph_tried = false;
   hipGraphExec_t exec = nullptr;
   float *x = nullptr, *xb = nullptr, *hb = nullptr, *hb2 = nullptr, *q = nullptr,
         *k = nullptr, *v = nullptr, *logits = nullptr;
@@ -322,7 +322,10 @@ namespace {
 
 // Every launch of one decode step, reading the token and pos from the step
 // inputs in device memory: the same sequence runs eagerly and is captured.
-int enqueue_step(g2b_model *m) {
+// The attention is scheduled for positions up to max_pos: the step's own pos
+// when eager (one split, no combine launch at short contexts), the whole
+// context when captured.
+int enqueue_step(g2b_model *m, int32_t max_pos) {
   const g2b_model_cfg &c = m->cfg;
   const int32_t dim = c.dim, hid = c.hidden_dim;
   const int32_t nq = c.n_heads * c.head_dim, nkv = c.n_kv_heads * c.head_dim;
@@ -395,9 +398,9 @@ int enqueue_step(g2b_model *m) {
       G2B_MODEL_RC(gemv(m->k, m->xb, wk, dim, nkv));
       G2B_MODEL_RC(gemv(m->v, m->xb, wv, dim, nkv));
     }
-    // QK-RMSNorm, RoPE, KV append, attention over the positions up to pos
-    // (scheduled for the whole context); the output over q
-    G2B_MODEL_RC(attn_forward_device_seq(cx, L, m->d_seq, m->ctx_cap - 1, m->q, m->k, m->v));
+    // QK-RMSNorm, RoPE, KV append, attention over the positions up to pos;
+    // the output over q
+    G2B_MODEL_RC(attn_forward_device_seq(cx, L, m->d_seq, max_pos, m->q, m->k, m->v));
     // Wo and the residual (l5_model.c:580-583)
     if (m->fuse && gemv_fusable(wo->type, nq)) {
       GemvParams p{};
@@ -511,14 +514,16 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
   if (m->exec && m->use_graph) {
     if (hipGraphLaunch(m->exec, st) != hipSuccess) return G2B_EDEVICE;
   } else {
-    if (int rc = enqueue_step(m)) return rc;
+    if (int rc = enqueue_step(m, pos)) return rc;
     if (m->use_graph && !m->graph_tried) {
       // capture the step once (every buffer it touches exists by now); on any
       // failure the model keeps running eagerly
       m->graph_tried = true;
       hipGraph_t graph = nullptr;
-      if (hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) == hipSuccess) {
-        const int rc = enqueue_step(m);
+      // (the whole context's attention buffers first: the capture must not allocate)
+      if (attn_reserve_device_seq(m->ctx, m->ctx_cap - 1, m->q, m->k, m->v) == G2B_OK &&
+          hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) == hipSuccess) {
+        const int rc = enqueue_step(m, m->ctx_cap - 1);
         const hipError_t e = hipStreamEndCapture(st, &graph);
         if (rc == G2B_OK && e == hipSuccess && graph &&
             hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0) != hipSuccess)
