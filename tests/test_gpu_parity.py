@@ -272,6 +272,7 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
                 check_weights(w[L, i, :, :p + 1], ratt, wex)
         assert np.array_equal(dev_kv[i][0], kc), f"K bytes of sequence {i}"
         assert np.array_equal(dev_kv[i][1], vc), f"V bytes of sequence {i}"
+    return out
 
 
 @pytest.mark.parametrize("name", sorted(SHAPES))
@@ -284,6 +285,24 @@ def test_batched_ragged_vs_oracle(gpu_device, name, mode):
     fused, tune = MODES[mode]
     print(f"[batch] {name} mode={mode}", flush=True)
     run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused, tune=tune)
+
+
+@pytest.mark.parametrize("name", ["qwen3_q8_g2", "qwen3_f32_g2", "smollm2_f32_g3",
+                                  "llama3_q8_g4", "hd64_q8_g3", "mha_q8_g1"])
+def test_static_splits_without_weights(gpu_device, name):
+    """Static splits without the weights output (the decode kernel skips the
+    raw-score writes; a single split writes the output itself): against the
+    oracle, and bit for bit against the same call with the weights
+    requested.  One sequence in 2..32 splits, then a ragged batch."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    print(f"[noatt] {name}", flush=True)
+    tune = (0, 0, 0, -1)  # static splits
+    plain = run_batch_case(o, [900], [899], seed=31, fused=False, want_att=False, tune=tune)
+    with_w = run_batch_case(o, [900], [899], seed=31, fused=False, want_att=True, tune=tune)
+    assert np.array_equal(plain.view(np.uint32), with_w.view(np.uint32))
+    run_batch_case(o, [1, 70, 900, 300], [0, 69, 899, 150], seed=32, fused=False,
+                   want_att=False, tune=tune)
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3"])
