@@ -272,12 +272,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
   if constexpr (KB > 0) {
     // Every wave runs the first trip (rows or not): its weights are issued,
     // then the workgroup prepares x (barriers) while they are in flight.
-    for (int s0 = gw, trip = 0;; s0 += stride * kGemvUnroll, trip++) {
-      BlockRaw<FMT> raw[kGemvUnroll][KB];
-      int row[kGemvUnroll];
-      bool ok[kGemvUnroll];
+    // (Twice the steps in flight for Q4_0 measured slower.)
+    constexpr int UN = kGemvUnroll;
+    for (int s0 = gw, trip = 0;; s0 += stride * UN, trip++) {
+      BlockRaw<FMT> raw[UN][KB];
+      int row[UN];
+      bool ok[UN];
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; u++) {
+      for (int u = 0; u < UN; u++) {
         const int s = s0 + u * stride;
         row[u] = s * RPS + rr;
         ok[u] = s < P.steps && row[u] < P.d;
@@ -297,14 +299,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
         lane_x<LPR, KB>(P, xs, c, nb, inv, xr);
       }
 #pragma unroll
-      for (int u = 0; u < kGemvUnroll; u++) {
+      for (int u = 0; u < UN; u++) {
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < KB; k++) acc += block_dot<FMT>(raw[u][k], xr[k]);
         acc = lanes_sum<LPR>(acc);
         if (ok[u] && c == 0) seg_store(P, row[u], acc);
       }
-      if (s0 + stride * kGemvUnroll >= P.steps) break;
+      if (s0 + stride * UN >= P.steps) break;
     }
   } else {
     for (int s0 = gw; s0 < P.steps; s0 += stride * kGemvUnroll) {
@@ -437,6 +439,47 @@ inline size_t pro_lds(const GemvParams &p) {
   return p.pro != kProNone ? (size_t)p.n * sizeof(float) : 0;
 }
 
+// Resident workgroups per CU of a k_gemv_q instance (with or without the
+// prologue's dynamic LDS), queried once.
+template <int FMT, int LPR, int KB>
+int occ_q(size_t lds) {
+  static int cached[2] = {0, 0};
+  int &o = cached[lds ? 1 : 0];
+  if (o == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_q<FMT, LPR, KB>, kGemvThreads,
+                                                     lds) != hipSuccess || n < 1) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    o = n;
+  }
+  return o;
+}
+
+template <int FMT, int LPR>
+int occ_q_lpr(int kb, size_t lds) {
+  switch (kb) {
+    case 1: return occ_q<FMT, LPR, 1>(lds);
+    case 2: return occ_q<FMT, LPR, 2>(lds);
+    case -1: return occ_q<FMT, LPR, -1>(lds);
+    default: return occ_q<FMT, LPR, 0>(lds);
+  }
+}
+
+template <int FMT>
+int occ_q_fmt(int lpr, int kb, size_t lds) {
+  switch (lpr) {
+    case 1: return occ_q_lpr<FMT, 1>(kb, lds);
+    case 2: return occ_q_lpr<FMT, 2>(kb, lds);
+    case 4: return occ_q_lpr<FMT, 4>(kb, lds);
+    case 8: return occ_q_lpr<FMT, 8>(kb, lds);
+    case 16: return occ_q_lpr<FMT, 16>(kb, lds);
+    case 32: return occ_q_lpr<FMT, 32>(kb, lds);
+    default: return occ_q_lpr<FMT, 64>(kb, lds);
+  }
+}
+
 template <int FMT, int LPR>
 hipError_t launch_q_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
   const dim3 blk(kGemvThreads);
@@ -527,17 +570,21 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   const int kb = (p.nb + lpr - 1) / lpr;
   const int rps = 64 / lpr;
   p.steps = (p.d + rps - 1) / rps;
-  // every wave loads the x of its blocks once: at least kGemvMinSteps steps
-  // per wave where there are enough, at least 4 waves per CU, at most 16
-  const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
-                                      std::min(p.steps, n_cu * 4)),
-                             n_cu * 16);
-  const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
-  p.n_waves = wgs * waves_per_wg;
   const int kbv = !p.x_vec4                     ? 0
                   : kb <= 2                     ? kb
                   : p.nb * 128 <= kGemvMaxXLds ? -1
                                                 : 0;
+  // every wave loads the x of its blocks once: at least kGemvMinSteps steps
+  // per wave where there are enough, at least 4 waves per CU, at most one
+  // resident round of workgroups (a partial second round would leave most
+  // of the chip idle at the end)
+  const size_t lds = kbv < 0 ? (size_t)p.nb * 128u : pro_lds(p);
+  const int occ = fmt == 1 ? occ_q_fmt<1>(lpr, kbv, lds) : occ_q_fmt<2>(lpr, kbv, lds);
+  const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
+                                      std::min(p.steps, n_cu * 4)),
+                             n_cu * std::max(1, occ) * waves_per_wg);
+  const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
+  p.n_waves = wgs * waves_per_wg;
   return fmt == 1 ? launch_q<1>(p, lpr, kbv, dim3(wgs), s) : launch_q<2>(p, lpr, kbv, dim3(wgs), s);
 }
 
