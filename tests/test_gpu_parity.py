@@ -293,7 +293,8 @@ def test_static_splits_without_weights(gpu_device, name):
     """Static splits without the weights output (the decode kernel skips the
     raw-score writes; a single split writes the output itself): against the
     oracle, and bit for bit against the same call with the weights
-    requested.  One sequence in 2..32 splits, then a ragged batch."""
+    requested.  One sequence in 2..32 splits, then a ragged batch, then a
+    batch of short sequences (one split each)."""
     nh, nkv, hd, arch, q8 = SHAPES[name]
     o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
     print(f"[noatt] {name}", flush=True)
@@ -303,6 +304,9 @@ def test_static_splits_without_weights(gpu_device, name):
     assert np.array_equal(plain.view(np.uint32), with_w.view(np.uint32))
     run_batch_case(o, [1, 70, 900, 300], [0, 69, 899, 150], seed=32, fused=False,
                    want_att=False, tune=tune)
+    # every sequence within one split: each unit's k_layer workgroup writes the
+    # output itself and no k_combine runs
+    run_batch_case(o, [1, 20, 33], [0, 19, 32], seed=33, fused=True, want_att=False, tune=tune)
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3"])
