@@ -104,7 +104,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
 // drifts by ~1e-5 relative once one partial dominates.
 constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 2048;
-constexpr int kCombineFewParts = 32;  // up to this many partials: 64-thread workgroups
+constexpr int kCombineFewParts = 32;  // up to this many partials: one wave per head
 
 __device__ inline float block_max_f(float x, float *red) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -207,6 +207,74 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
   }
 }
 
+// k_combine with few partials (max_splits <= kCombineFewParts): one wave per
+// head, four heads per workgroup, so the grid has a quarter of the
+// workgroups (the launch is bound by dispatching them).  Per head the same
+// arithmetic as k_combine with a 64-thread workgroup (its block reductions
+// are this wave's), so the two give the same output bit for bit.
+__global__ __launch_bounds__(kCombineThreads) void k_combine_waves(DecodeParams P, float *q_out) {
+  __shared__ float wsh[kCombineThreads / 64][kCombineFewParts];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.x * (kCombineThreads / 64) + wave;
+  const int seq = blockIdx.y, li = blockIdx.z;
+  const int HD = P.sh.head_dim, nh = P.sh.n_heads;
+  const size_t unit = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  int np;
+  if (P.wq) {
+    const int32_t *ctr = P.wq + ((size_t)P.wq_set * P.wq_cap + unit) * kWqStride;
+    np = min(ctr[1], P.max_splits);
+    int32_t *nxt = P.wq + (size_t)(P.wq_set ^ 1) * P.wq_cap * kWqStride;
+    const size_t nblk = (size_t)gridDim.x * gridDim.y * gridDim.z;
+    const size_t bid = blockIdx.x + (size_t)gridDim.x * (blockIdx.y + (size_t)gridDim.y * blockIdx.z);
+    for (size_t uu = bid; uu < (size_t)P.wq_zero_units; uu += nblk)
+      if (threadIdx.x < 2) nxt[uu * kWqStride + threadIdx.x] = 0;
+  } else {
+    np = (npos + P.split_len - 1) / P.split_len;
+  }
+  if (h >= nh) return;  // (no barrier below)
+  const size_t pstr = (size_t)(kPartHead + HD);
+  const float *base = P.part + (unit * nh + h) * (size_t)P.max_splits * pstr;
+  float *w = wsh[wave];
+  float mx = kNegBig;
+  for (int p = lane; p < np; p += 64) mx = fmaxf(mx, base[p * pstr]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const float M = mx;
+  double lsum = 0.0;
+  for (int p = lane; p < np; p += 64) {
+    const float wp = exp2f(base[p * pstr] - M);
+    w[p] = wp;
+    lsum = fma((double)base[p * pstr + 1], (double)wp, lsum);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+  const double L = lsum;
+  // (w: written and read by this wave only; LDS keeps its order)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float *out = q_out + unit * (size_t)(nh * HD) + (size_t)h * HD;
+  for (int d = lane; d < HD; d += 64) {
+    const float *a = base + kPartHead + d;
+    double o0 = 0.0, o1 = 0.0, o2 = 0.0, o3 = 0.0;
+    int p = 0;
+    for (; p + 3 < np; p += 4) {
+      o0 = fma((double)a[(size_t)p * pstr], (double)w[p], o0);
+      o1 = fma((double)a[(size_t)(p + 1) * pstr], (double)w[p + 1], o1);
+      o2 = fma((double)a[(size_t)(p + 2) * pstr], (double)w[p + 2], o2);
+      o3 = fma((double)a[(size_t)(p + 3) * pstr], (double)w[p + 3], o3);
+    }
+    for (; p < np; p++) o0 = fma((double)a[(size_t)p * pstr], (double)w[p], o0);
+    out[d] = (float)(((o0 + o1) + (o2 + o3)) / L);
+  }
+  if (P.att) {
+    float *at = P.att + (unit * nh + h) * (size_t)P.att_stride;
+    for (int t = lane; t < npos; t += 64) at[t] = (float)(exp2((double)at[t] - (double)M) / L);
+  }
+}
+
 // ---------------------------------------------------------------- dispatch
 
 static int fast_chunk(const ShapeDev &sh) {
@@ -299,12 +367,18 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, boo
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s) {
   if (p.max_splits > kCombineMaxParts) return hipErrorInvalidValue;
   dim3 grid(p.sh.n_heads, p.n_seq, n_layers);
-  // Few partials per head: one wave per workgroup.  With thousands of heads
-  // in the grid (c4: 4096) the launch is bound by dispatching waves (~7 us
-  // to start 4096 x 4 waves), not by the merge; many partials (a single
-  // long sequence) need the four waves.
-  const int threads = p.max_splits <= kCombineFewParts ? 64 : kCombineThreads;
-  hipLaunchKernelGGL(k_combine, grid, dim3(threads), 0, s, p, p.q_out);
+  // Few partials per head: one wave per head, four heads per workgroup.
+  // With thousands of heads in the grid (c4: 4096) the launch is bound by
+  // dispatching workgroups (~7 us to start 4096 of four waves), not by the
+  // merge; many partials (a single long sequence) need a workgroup's four
+  // waves on one head.
+  if (p.max_splits <= kCombineFewParts) {
+    const int hpw = kCombineThreads / 64;  // heads per workgroup
+    dim3 g4((p.sh.n_heads + hpw - 1) / hpw, p.n_seq, n_layers);
+    hipLaunchKernelGGL(k_combine_waves, g4, dim3(kCombineThreads), 0, s, p, p.q_out);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(k_combine, grid, dim3(kCombineThreads), 0, s, p, p.q_out);
   return hipGetLastError();
 }
 
