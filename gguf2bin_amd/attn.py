@@ -236,7 +236,8 @@ class Model:
         return out
 
     def use_graph(self, on: bool):
-        """Replay the captured step graph (default) or keep every step eager."""
+        """Capture the step once and replay it (on), or launch every step
+        eagerly with the attention sized for its position (off, the default)."""
         lib().g2b_model_use_graph(self.h, 1 if on else 0)
 
     def set_fused(self, on: bool):
