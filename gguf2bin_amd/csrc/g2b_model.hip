@@ -118,8 +118,26 @@ struct g2b_model {
   uint8_t *d_step = nullptr, *h_step = nullptr;
   SeqDev *d_seq = nullptr;
   int32_t *d_tok = nullptr;
-  bool use_graph = false, graph_tried = false;
-  hipGraphExec_t exec = nullptr;
+  bool use_graph = false;
+  // captured steps, one per position bucket: the attention of bucket b is
+  // scheduled for positions up to max_pos (64, 128, 256, ... positions, the
+  // last one the whole context)
+  struct GraphBucket {
+    int32_t max_pos;
+    hipGraphExec_t exec;
+    bool tried;
+  };
+  std::vector<GraphBucket> graphs;
+  void drop_graphs() {
+    for (GraphBucket &b : graphs)
+      if (b.exec) (void)hipGraphExecDestroy(b.exec);
+    graphs.clear();
+  }
+  int32_t bucket_max_pos(int32_t pos) const {
+    int64_t n = 64;
+    while (n < (int64_t)pos + 1) n *= 2;
+    return (int32_t)(n < ctx_cap ? n : ctx_cap) - 1;
+  }
   float *x = nullptr, *xb = nullptr, *hb = nullptr, *hb2 = nullptr, *q = nullptr,
         *k = nullptr, *v = nullptr, *logits = nullptr;
   // slot_get's index (l5_model.c:34-45): per layer and role, and global
@@ -139,7 +157,7 @@ int g2b_model_free(g2b_model *m) {
   if (!m) return G2B_EINVAL;
   if (m->ctx) {
     (void)g2b_sync(m->ctx);
-    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    m->drop_graphs();
     if (m->h_step) (void)hipHostFree(m->h_step);
     if (m->d_step) (void)g2b_weights_free(m->ctx, m->d_step);
     if (m->kc || m->vc) (void)g2b_kv_free(m->ctx, m->kc, m->vc);
@@ -309,9 +327,7 @@ int g2b_model_set_fused(g2b_model *m, int32_t on) {
   if (m->fuse != (on != 0)) {
     m->fuse = on != 0;
     // a captured step holds the other launches: capture again
-    if (m->exec) (void)hipGraphExecDestroy(m->exec);
-    m->exec = nullptr;
-    m->graph_tried = false;
+    m->drop_graphs();
   }
   return G2B_OK;
 }
@@ -511,23 +527,33 @@ int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits) {
   memcpy(m->h_step + 32, &token, sizeof token);
   if (hipMemcpyAsync(m->d_step, m->h_step, 64, hipMemcpyHostToDevice, st) != hipSuccess)
     return G2B_EDEVICE;
-  if (m->exec && m->use_graph) {
-    if (hipGraphLaunch(m->exec, st) != hipSuccess) return G2B_EDEVICE;
+  g2b_model::GraphBucket *bucket = nullptr;
+  if (m->use_graph) {
+    const int32_t bmax = m->bucket_max_pos(pos);
+    for (g2b_model::GraphBucket &b : m->graphs)
+      if (b.max_pos == bmax) bucket = &b;
+    if (!bucket) {
+      m->graphs.push_back({bmax, nullptr, false});
+      bucket = &m->graphs.back();
+    }
+  }
+  if (bucket && bucket->exec) {
+    if (hipGraphLaunch(bucket->exec, st) != hipSuccess) return G2B_EDEVICE;
   } else {
     if (int rc = enqueue_step(m, pos)) return rc;
-    if (m->use_graph && !m->graph_tried) {
-      // capture the step once (every buffer it touches exists by now); on any
-      // failure the model keeps running eagerly
-      m->graph_tried = true;
+    if (bucket && !bucket->tried) {
+      // capture this bucket's step once (nothing runs while capturing); on
+      // any failure the bucket keeps running eagerly
+      bucket->tried = true;
       hipGraph_t graph = nullptr;
-      // (the whole context's attention buffers first: the capture must not allocate)
-      if (attn_reserve_device_seq(m->ctx, m->ctx_cap - 1, m->q, m->k, m->v) == G2B_OK &&
+      // (the bucket's attention buffers first: the capture must not allocate)
+      if (attn_reserve_device_seq(m->ctx, bucket->max_pos, m->q, m->k, m->v) == G2B_OK &&
           hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed) == hipSuccess) {
-        const int rc = enqueue_step(m, m->ctx_cap - 1);
+        const int rc = enqueue_step(m, bucket->max_pos);
         const hipError_t e = hipStreamEndCapture(st, &graph);
         if (rc == G2B_OK && e == hipSuccess && graph &&
-            hipGraphInstantiate(&m->exec, graph, nullptr, nullptr, 0) != hipSuccess)
-          m->exec = nullptr;
+            hipGraphInstantiate(&bucket->exec, graph, nullptr, nullptr, 0) != hipSuccess)
+          bucket->exec = nullptr;
         if (graph) (void)hipGraphDestroy(graph);
       }
       (void)hipGetLastError();

@@ -95,18 +95,18 @@ g2b_ctx *g2b_model_ctx(g2b_model *m);
  * G2B_EINVAL); a missing slot fails with G2B_EINVAL and leaves them. */
 int g2b_model_forward(g2b_model *m, int32_t token, int32_t pos, float *logits);
 
-/* on = 1: the next forward runs its launches one by one and then captures
- * them as a HIP graph (token and pos are read from device memory; the
- * attention is scheduled for the whole context), which every later forward
- * replays: one graph launch per step instead of six launches per layer.
- * on = 0 (the default): every step is launched eagerly, with the attention
+/* on = 1: steps are replayed from HIP graphs, one per position bucket (64,
+ * 128, 256, ... positions, the last one the whole context): the first
+ * forward in a bucket runs its launches one by one and then captures them
+ * (token and pos are read from device memory; the attention is scheduled for
+ * the bucket's last position), later forwards in the bucket replay it - one
+ * graph launch per step instead of five or six launches per layer.  on = 0
+ * (the default): every step is launched eagerly, with the attention
  * scheduled for the step's own position (at short contexts one split and no
  * combine launch: five launches per layer).  Where both schedules cut the
  * context into the same splits (on MI355X, contexts up to 32768) the logits
- * agree bit for bit, else to fp32 summation order; on this hardware the eager
- * step is as fast as the replay or faster, because the kernels' own time,
- * not the host's launches, bounds a step.  Tuning the model's context after a capture does not change the
- * captured step. */
+ * agree bit for bit, else to fp32 summation order.  Changing the fused mode
+ * drops the captured steps. */
 int g2b_model_use_graph(g2b_model *m, int32_t on);
 
 /* on = 1 (the default): where the weight types allow it (Q8_0 / Q4_0, rows of

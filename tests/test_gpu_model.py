@@ -110,13 +110,14 @@ def test_forward_long_context(gpu_device, tmp_path):
 
 @pytest.mark.parametrize("kv_q8", [False, True])
 def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
-    """With the graph on, every forward after the first replays the step
-    captured for the whole context (split partials and k_combine); stepped in
-    turn with an eager model of the same file (its launches one by one,
-    scheduled for the step's own position: one split, the output written by
-    k_layer, no combine; the synchronisation that ends every forward between
-    the replays), each replay must give the eager step's logits bit for
-    bit.  72 positions: the eager schedule crosses from one split to two."""
+    """With the graph on, the first forward of each position bucket (64,
+    128, ... positions) captures its step and later ones replay it; stepped
+    in turn with an eager model of the same file (its launches one by one,
+    scheduled for the step's own position; the synchronisation that ends
+    every forward between the replays), each replay must give the eager
+    step's logits bit for bit.  72 positions: the first bucket (one split,
+    the output written by k_layer) and the second (two splits and
+    k_combine)."""
     p, cfg, rng = make(tmp_path, "qwen3_hd128_q8", seed=5)
     toks = [int(t) for t in rng.integers(0, cfg["vocab"], 72)]
     with attn.Model(p, kv_q8=kv_q8) as g, attn.Model(p, kv_q8=kv_q8) as e:
