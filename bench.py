@@ -481,13 +481,15 @@ def model_leg(args):
             def rel_diff(dev, ref):
                 return max(float(np.abs(dev[i] - ref[i]).max() / max(1.0, np.abs(ref[i]).max()))
                            for i in range(len(ref)))
-            # per-token time of the reference without its load: 1 vs 5 tokens
-            t0 = time.perf_counter()
+            # per-token time of the reference: its token loop alone (the driver
+            # times it, without the file load and KV allocation), positions
+            # 0..7 - at least as short as the device's positions 8..8+K - after
+            # one untimed call that pages the file in and starts the OpenMP threads
             orc.ref_model_forward(path, toks[:1], cfg["vocab"], True, 0)
-            t1 = time.perf_counter()
-            ref_q8 = orc.ref_model_forward(path, toks[:5], cfg["vocab"], True, 0)
-            t2 = time.perf_counter()
-            cdt = max((t2 - t1) - (t1 - t0), 1e-9) / 4
+            ref_q8, secs = orc.ref_model_forward(path, toks[:8], cfg["vocab"], True, 0,
+                                                 timed=True)
+            ref_q8 = ref_q8[:5]
+            cdt = secs / 8
             # parity with an F32 KV (no quantisation of the appended rows: fp32
             # summation order only), and the Q8_0-KV figure beside it
             ref_f32 = orc.ref_model_forward(path, toks[:5], cfg["vocab"], False, 0)

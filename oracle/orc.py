@@ -366,21 +366,25 @@ def ref_g2bx_info(path: str):
 
 
 def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
-                      ctx: int = 0) -> np.ndarray:
+                      ctx: int = 0, timed: bool = False):
     """The compiled reference's model_forward over tokens at positions
-    0..n-1 of a G2BX file: logits [n][vocab]."""
+    0..n-1 of a G2BX file: logits [n][vocab]; with timed, (logits, seconds
+    of the token loop alone, without the load)."""
     L = ref_lib("avx2")
     if L is None:
         raise RuntimeError("compiled reference not built (make -C oracle ref)")
     fn = L.ref_model_forward_g2bx
-    fn.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+    fn.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                   C.POINTER(C.c_double)]
     fn.restype = C.c_int
     tok = np.ascontiguousarray(tokens, np.int32)
     out = np.zeros((len(tok), vocab), np.float32)
-    rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, tok.ctypes.data, len(tok), out.ctypes.data)
+    secs = C.c_double(0.0)
+    rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, tok.ctypes.data, len(tok), out.ctypes.data,
+            C.byref(secs))
     if rc:
         raise RuntimeError(f"reference forward failed ({rc})")
-    return out
+    return (out, secs.value) if timed else out
 
 
 def random_weights(rng: np.random.Generator, t: int, n: int, d: int) -> np.ndarray:

@@ -21,6 +21,10 @@
  * (l5_model.c:505-511); its prefill applies the reference's qk_rmsnorm to
  * each k row before apply_rope, as model_forward would.
  */
+#define _POSIX_C_SOURCE 200809L
+#define _DEFAULT_SOURCE
+#include <time.h>
+
 #include "l5_model.c"
 
 void ref_q8_quant_row(const f32 *src, u8 *dst, i32 n) { q8_quant_row(src, dst, n); }
@@ -243,8 +247,11 @@ int ref_g2bx_info(const char *path, u8 *cfg40, int *arch, int *flags, u32 *n_slo
 /* model_forward (l5_model.c:461-606) over tokens[0..n) at positions 0..n-1
  * of a G2BX file, KV in Q8_0 when kv_q8, context ctx (<= 0: seq_len):
  * logits of every step into out[n][vocab].  0 on success. */
+/* Loads a G2BX file and runs model_forward over tokens at positions 0..n-1.
+ * secs (may be NULL) receives the wall time of the token loop alone
+ * (CLOCK_MONOTONIC), without the load and the KV allocation. */
 int ref_model_forward_g2bx(const char *path, int kv_q8, int ctx, const i32 *tokens, int n,
-                           f32 *out) {
+                           f32 *out, double *secs) {
   Model m;
   if (model_load_g2bx(path, &m)) return -1;
   if (kv_q8) m.flags |= F_KV_Q8;
@@ -252,7 +259,11 @@ int ref_model_forward_g2bx(const char *path, int kv_q8, int ctx, const i32 *toke
     model_free(&m);
     return -2;
   }
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
   for (int i = 0; i < n; i++) model_forward(&m, tokens[i], i, out + (size_t)i * m.c.vocab);
+  clock_gettime(CLOCK_MONOTONIC, &t1);
+  if (secs) *secs = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
   model_free(&m);
   return 0;
 }
