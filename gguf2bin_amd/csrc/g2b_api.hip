@@ -203,6 +203,25 @@ int32_t choose_split(const g2b_ctx *c, int64_t slots, int64_t total_pos, int32_t
   return (int32_t)std::max<int64_t>(sl, 1);
 }
 
+// With g2b_ctx_profile on: records the first of two timing events around
+// the next decode launch and hands back the second (*ev1), else *ev1 = null.
+int prof_begin(g2b_ctx *c, hipEvent_t *ev1) {
+  *ev1 = nullptr;
+  if (!c->prof) return G2B_OK;
+  if (c->prof_used + 2 > c->prof_ev.size()) {
+    for (int i = 0; i < 2; i++) {
+      hipEvent_t e;
+      G2B_HIP(c, hipEventCreate(&e));
+      c->prof_ev.push_back(e);
+    }
+  }
+  const hipEvent_t ev0 = c->prof_ev[c->prof_used];
+  *ev1 = c->prof_ev[c->prof_used + 1];
+  c->prof_used += 2;
+  G2B_HIP(c, hipEventRecord(ev0, c->stream));
+  return G2B_OK;
+}
+
 int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_seq,
                int32_t max_pos, int64_t total_pos, int32_t layer0, int32_t n_layers, float *q,
                const float *k, const float *v, float *att, int32_t att_stride,
@@ -250,6 +269,20 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
+
+  // Short contexts (every pos < kShortMaxPos), no weights output: k_short,
+  // one workgroup per (KV head, sequence, layer), writes the output over q
+  // itself - no partials, no combine.  An explicit split length or
+  // work-queue piece (g2b_ctx_tune) keeps the split kernel.
+  if (fast && !att && max_pos < kShortMaxPos && c->split_override == 0 && c->tune_piece == 0 &&
+      short_available(c->sh)) {
+    if (dry) return G2B_OK;
+    hipEvent_t ev1 = nullptr;
+    if (int rc = prof_begin(c, &ev1)) return rc;
+    G2B_HIP(c, launch_short(dp, n_layers, c->stream));
+    if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
+    return G2B_OK;
+  }
 
   // Work queue (staged streaming) when few enough waves share each unit's
   // counters - with more units (sequence, layer) than resident workgroups,
@@ -355,20 +388,8 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     G2B_HIP(c, launch_append_batch(ap, n_layers, c->stream));
   }
   int used_fast = 0;
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  if (c->prof) {
-    if (c->prof_used + 2 > c->prof_ev.size()) {
-      for (int i = 0; i < 2; i++) {
-        hipEvent_t e;
-        G2B_HIP(c, hipEventCreate(&e));
-        c->prof_ev.push_back(e);
-      }
-    }
-    ev0 = c->prof_ev[c->prof_used];
-    ev1 = c->prof_ev[c->prof_used + 1];
-    c->prof_used += 2;
-    G2B_HIP(c, hipEventRecord(ev0, c->stream));
-  }
+  hipEvent_t ev1 = nullptr;
+  if (int rc = prof_begin(c, &ev1)) return rc;
   if (use_wq) c->wq_reset = true;  // until both launches below are queued
   G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));

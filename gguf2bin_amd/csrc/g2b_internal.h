@@ -171,6 +171,12 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, boo
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 // Whether a specialised decode kernel exists for this shape.
 bool decode_fast_available(const ShapeDev &sh);
+// Short contexts (every sequence's pos < kShortMaxPos, no weights output):
+// k_short does RoPE, append and attention with one workgroup per (KV head,
+// sequence, layer) and writes the output over q itself (no combine).
+constexpr int kShortMaxPos = 128;
+bool short_available(const ShapeDev &sh);
+hipError_t launch_short(const DecodeParams &p, int n_layers, hipStream_t s);
 // Resident 256-thread decode workgroups per CU for this shape and the
 // k_layer variant DecodeParams' tune_chunk / stage_mode / stage_rows / wq
 // select (occupancy).

@@ -1,0 +1,346 @@
+// g2b_short.hip - k_short: decode attention of short contexts, one
+// workgroup per (KV head, sequence, layer).
+//
+// Same work as k_layer for one (sequence, layer) - l5_model.c:505-516
+// (QK-RMSNorm, RoPE, kv_store of the new row) and :518-577 (scores over
+// positions 0..pos, softmax with 1/sqrt(hd), V-accumulate, output over q) -
+// but split by KV head instead of by positions: at a few hundred positions
+// the work is the setup's chain of dependent steps, not the KV bytes (a
+// 48-position Qwen3-0.6B layer reads 100 KB), and one KV head's share of
+// it - its G query heads, its k and v slice, its slice of every row - is
+// independent of the other heads'.  Q8_0 blocks never straddle heads
+// (head_dim is a multiple of 32), so each workgroup quantises and stores its
+// own slice of the new row bit-exactly with the shared block quantiser.
+//
+// Per workgroup (256 threads, four waves):
+//   1. q of the group's G heads and the new k into LDS (one float4 each).
+//   2. QK-RMSNorm factors: one thread per head, squares summed left to right
+//      (qk_rmsnorm_block's order); inv = 1/sqrtf(ss/hd + eps).
+//   3. (w * x) * inv, then the RoPE rotation of pos, per pair (ia, ib).
+//   4. The new k and v slice: F32 copy or Q8_0 quantisation (four lanes per
+//      block) into LDS, then to the caches.
+//   5. Scores of positions 0..pos: NB = hd/32 consecutive lanes per
+//      position, a 32-element piece each, fp32 dot products with the G
+//      heads' q, summed over the NB lanes; position pos from the LDS copy.
+//   6. Softmax statistics: wave g for head g (max, exp2, sum).
+//   7. V-accumulate: wave w takes positions w, w+4, ..., each lane hd/64
+//      elements; the four waves' sums merge in LDS, divided by the sum of
+//      weights and written over q.
+// Scores are in the log2 domain (q . k * log2(e)/sqrt(hd)), so the weights
+// are exp2(s - max): the reference's softmax within fp32 rounding.
+#include "g2b_internal.h"
+
+namespace g2b {
+namespace {
+
+constexpr int kSThreads = 256;
+constexpr int kSMaxG = 4;  // query heads per KV head (decode_fast_available)
+
+template <int FMT, int HD>
+struct ShortGeom {
+  static constexpr int NB = HD / 32;                 // 32-element pieces per head slice
+  static constexpr int HB = FMT ? NB * 34 : HD * 4;  // bytes of a head's slice of a row
+  static constexpr int HBP = (HB + 15) & ~15;        // LDS copy, 16-byte padded
+  static constexpr int XS = HD + 4;                  // LDS row of a head (bank offset)
+  static constexpr int EPL = HD / 64;                // V elements per lane
+};
+
+// Piece b (elements 32b..32b+31) of a head slice (4-byte aligned; global or
+// LDS) as 32 floats before the Q8_0 scale, and the scale (1 for F32).
+// Q8_0: block b starts at byte 34b; the nine dwords from (34b) & ~3 cover
+// it (two bytes early for odd b, two bytes into block b+1 for even b, which
+// exists: NB is even), so the window never leaves the slice.
+template <int FMT>
+__device__ __forceinline__ float load_piece(const uint8_t *slice, int b, float (&x)[32]) {
+  if constexpr (FMT == 1) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(slice + ((34 * b) & ~3));
+    uint32_t d[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) d[i] = w[i];
+    const bool odd = (b & 1) != 0;
+    const float scale = half_bits_to_f32_hw(odd ? (d[0] >> 16) : (d[0] & 0xFFFFu));
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t q = odd ? d[i + 1] : __builtin_amdgcn_alignbit(d[i + 1], d[i], 16);
+      x[4 * i + 0] = (float)(int8_t)(q & 0xFFu);
+      x[4 * i + 1] = (float)(int8_t)((q >> 8) & 0xFFu);
+      x[4 * i + 2] = (float)(int8_t)((q >> 16) & 0xFFu);
+      x[4 * i + 3] = (float)(int8_t)(q >> 24);
+    }
+    return scale;
+  } else {
+    const float4 *p = reinterpret_cast<const float4 *>(slice + 128 * b);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 v = p[i];
+      x[4 * i + 0] = v.x;
+      x[4 * i + 1] = v.y;
+      x[4 * i + 2] = v.z;
+      x[4 * i + 3] = v.w;
+    }
+    return 1.f;
+  }
+}
+
+// V elements e0 .. e0 + EPL - 1 (e0 a multiple of EPL) of a head slice,
+// dequantised as kv_val_row does (d * q).
+template <int FMT, int EPL>
+__device__ __forceinline__ void load_v(const uint8_t *slice, int e0, float (&v)[EPL]) {
+  if constexpr (FMT == 1) {
+    const int b = e0 >> 5;
+    const uint8_t *blk = slice + 34 * b;
+    const float d = half_bits_to_f32_hw(*reinterpret_cast<const uint16_t *>(blk));
+    if constexpr (EPL == 2) {
+      const uint32_t q = *reinterpret_cast<const uint16_t *>(blk + 2 + (e0 & 31));
+      v[0] = d * (float)(int8_t)(q & 0xFFu);
+      v[1] = d * (float)(int8_t)(q >> 8);
+    } else {
+      v[0] = d * (float)(int8_t)blk[2 + (e0 & 31)];
+    }
+  } else {
+    const float *f = reinterpret_cast<const float *>(slice) + e0;
+    if constexpr (EPL == 2) {
+      const float2 t = *reinterpret_cast<const float2 *>(f);
+      v[0] = t.x;
+      v[1] = t.y;
+    } else {
+      v[0] = f[0];
+    }
+  }
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <int FMT, int HD>
+__global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
+  using Geo = ShortGeom<FMT, HD>;
+  constexpr int NB = Geo::NB, HB = Geo::HB, XS = Geo::XS, EPL = Geo::EPL;
+  constexpr int half = HD / 2;
+  __shared__ __align__(16) float xs[(kSMaxG + 1) * XS];  // q heads 0..G-1, then k
+  __shared__ __align__(16) uint8_t rowk[Geo::HBP], rowv[Geo::HBP];
+  __shared__ float sc[kSMaxG * kShortMaxPos];  // scores, then weights
+  __shared__ __align__(16) float accs[4 * kSMaxG * HD];
+  __shared__ float inv[kSMaxG + 1], lsum[kSMaxG];
+
+  const int kvh = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const int layer = P.layer0 + li;
+  const ShapeDev &sh = P.sh;
+  const int G = sh.n_heads / sh.n_kv_heads;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int pos = sd.pos;
+  // (the host schedules this kernel only when every sequence's pos is below
+  // kShortMaxPos; a descriptor that breaks that leaves its output untouched
+  // rather than index past the score table)
+  if (pos < 0 || pos >= kShortMaxPos) return;
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const size_t nq = (size_t)sh.n_heads * HD, nkv = (size_t)sh.n_kv_heads * HD;
+  float *qo = P.q_out + sidx * nq + (size_t)kvh * G * HD;  // q in; the output goes here
+  const float *ki = P.k_in + sidx * nkv + (size_t)kvh * HD;
+  const float *vi = P.v_in + sidx * nkv + (size_t)kvh * HD;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+
+  // 1. q (G heads) and k into LDS
+  constexpr int P4 = HD / 4;
+  for (int i = t; i < (G + 1) * P4; i += kSThreads) {
+    const int h = i / P4, j = i - h * P4;
+    const float *src = h < G ? qo + h * HD : ki;
+    *reinterpret_cast<float4 *>(xs + h * XS + 4 * j) =
+        *reinterpret_cast<const float4 *>(src + 4 * j);
+  }
+  const float *wq = norm_weights(P.norm, layer, 0, HD);
+  const float *wk = norm_weights(P.norm, layer, 1, HD);
+  __syncthreads();
+
+  // 2. QK-RMSNorm factors
+  if (t <= G) {
+    const float *w = t < G ? wq : wk;
+    if (w) {
+      const float *x = xs + t * XS;
+      float ss = 0.f;
+#pragma unroll 8
+      for (int j = 0; j < HD; j += 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + j);
+        float sq = v.x * v.x;
+        ss = ss + sq;
+        sq = v.y * v.y;
+        ss = ss + sq;
+        sq = v.z * v.z;
+        ss = ss + sq;
+        sq = v.w * v.w;
+        ss = ss + sq;
+      }
+      inv[t] = __fdiv_rn(1.f, sqrtf(__fdiv_rn(ss, (float)HD) + P.norm.eps));
+    }
+  }
+  __syncthreads();
+
+  // 3. (w * x) * inv, then RoPE(pos), per pair
+  const float *cs = (sh.rope_on && P.rope) ? P.rope + (size_t)pos * HD : nullptr;
+  for (int i = t; i < (G + 1) * half; i += kSThreads) {
+    const int h = i / half, j = i - h * half;
+    int ia, ib;
+    rope_pair_index(sh.arch_llama, j, half, ia, ib);
+    float *x = xs + h * XS;
+    float a = x[ia], b = x[ib];
+    if (const float *w = h < G ? wq : wk) {
+      const float f = inv[h];
+      a = (w[ia] * a) * f;
+      b = (w[ib] * b) * f;
+    }
+    if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+    x[ia] = a;
+    x[ib] = b;
+  }
+  __syncthreads();
+
+  // 4. the new row's slice: LDS copy, then the caches
+  const float *kr = xs + G * XS;
+  if constexpr (FMT == 1) {
+    if (t < 8 * NB) {  // blocks 0..NB-1 of k, then of v; four lanes each
+      const int b = t >> 2, part = t & 3;
+      const bool is_k = b < NB;
+      const int bb = is_k ? b : b - NB;
+      q8_quant_block_x4((is_k ? kr : vi) + 32 * bb, 32, (is_k ? rowk : rowv) + 34 * bb, part);
+    }
+  } else {
+    for (int i = t; i < 2 * P4; i += kSThreads) {
+      const bool is_k = i < P4;
+      const int j = is_k ? i : i - P4;
+      const float4 v = *reinterpret_cast<const float4 *>((is_k ? kr : vi) + 4 * j);
+      *reinterpret_cast<float4 *>((is_k ? rowk : rowv) + 16 * j) = v;
+    }
+  }
+  __syncthreads();
+  const uint32_t row = sh.row_bytes;
+  const size_t lay = (size_t)layer * (size_t)sd.ctx_cap;
+  uint8_t *const kb = sd.k + lay * row + (size_t)kvh * HB;
+  uint8_t *const vb = sd.v + lay * row + (size_t)kvh * HB;
+  {
+    constexpr int W = HB / 4;  // dwords of a slice (HB is a multiple of 4)
+    const size_t off = (size_t)pos * row;
+    for (int i = t; i < 2 * W; i += kSThreads) {
+      const bool is_k = i < W;
+      const int j = is_k ? i : i - W;
+      uint8_t *dst = (is_k ? kb : vb) + off;
+      reinterpret_cast<uint32_t *>(dst)[j] =
+          reinterpret_cast<const uint32_t *>(is_k ? rowk : rowv)[j];
+    }
+  }
+
+  // 5. scores
+  const float qscale = P.qscale;
+  constexpr int PPR = kSThreads / NB;  // positions per round
+  for (int t0 = 0; t0 <= pos; t0 += PPR) {
+    const int tp = t0 + t / NB, b = t % NB;
+    if (tp <= pos) {  // (uniform over a position's NB lanes)
+      const uint8_t *slice = tp < pos ? kb + (size_t)tp * row : rowk;
+      float k[32];
+      const float d = load_piece<FMT>(slice, b, k);
+#pragma unroll
+      for (int g = 0; g < kSMaxG; g++) {
+        if (g < G) {
+          const float *q = xs + g * XS + 32 * b;
+          float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+          for (int j = 0; j < 32; j += 4) {
+            const float4 q4 = *reinterpret_cast<const float4 *>(q + j);
+            a0 = fmaf(q4.x, k[j + 0], a0);
+            a1 = fmaf(q4.y, k[j + 1], a1);
+            a2 = fmaf(q4.z, k[j + 2], a2);
+            a3 = fmaf(q4.w, k[j + 3], a3);
+          }
+          float s = ((a0 + a1) + (a2 + a3)) * d;
+#pragma unroll
+          for (int o = 1; o < NB; o <<= 1) s += __shfl_xor(s, o);
+          if (b == 0) sc[g * kShortMaxPos + tp] = s * qscale;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // 6. softmax statistics: wave g for head g
+  if (wave < G) {
+    float *s = sc + wave * kShortMaxPos;
+    float m = kNegBig;
+    for (int i = lane; i <= pos; i += 64) m = fmaxf(m, s[i]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int i = lane; i <= pos; i += 64) {
+      const float p = __builtin_amdgcn_exp2f(s[i] - m);
+      s[i] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) lsum[wave] = l;
+  }
+  __syncthreads();
+
+  // 7. V-accumulate, wave w over positions w, w + 4, ...
+  const int e0 = lane * EPL;
+  float acc[kSMaxG][EPL];
+#pragma unroll
+  for (int g = 0; g < kSMaxG; g++)
+#pragma unroll
+    for (int i = 0; i < EPL; i++) acc[g][i] = 0.f;
+#pragma unroll 4
+  for (int tp = wave; tp <= pos; tp += 4) {
+    const uint8_t *slice = tp < pos ? vb + (size_t)tp * row : rowv;
+    float v[EPL];
+    load_v<FMT, EPL>(slice, e0, v);
+#pragma unroll
+    for (int g = 0; g < kSMaxG; g++) {
+      if (g < G) {
+        const float p = sc[g * kShortMaxPos + tp];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) acc[g][i] = fmaf(p, v[i], acc[g][i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < kSMaxG; g++)
+#pragma unroll
+    for (int i = 0; i < EPL; i++) accs[(wave * kSMaxG + g) * HD + e0 + i] = acc[g][i];
+  __syncthreads();
+  for (int i = t; i < G * HD; i += kSThreads) {
+    const int g = i / HD, e = i - g * HD;
+    const float s = (accs[(0 * kSMaxG + g) * HD + e] + accs[(1 * kSMaxG + g) * HD + e]) +
+                    (accs[(2 * kSMaxG + g) * HD + e] + accs[(3 * kSMaxG + g) * HD + e]);
+    qo[g * HD + e] = s / lsum[g];
+  }
+}
+
+}  // namespace
+
+bool short_available(const ShapeDev &sh) {
+  return decode_fast_available(sh) && sh.n_heads / sh.n_kv_heads <= kSMaxG;
+}
+
+hipError_t launch_short(const DecodeParams &p, int n_layers, hipStream_t s) {
+  if (!short_available(p.sh) || n_layers < 1 || p.n_seq < 1) return hipErrorInvalidValue;
+  dim3 grid(p.sh.n_kv_heads, p.n_seq, n_layers);
+  if (p.sh.kv_q8) {
+    if (p.sh.head_dim == 128)
+      hipLaunchKernelGGL((k_short<1, 128>), grid, dim3(kSThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_short<1, 64>), grid, dim3(kSThreads), 0, s, p);
+  } else {
+    if (p.sh.head_dim == 128)
+      hipLaunchKernelGGL((k_short<0, 128>), grid, dim3(kSThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((k_short<0, 64>), grid, dim3(kSThreads), 0, s, p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace g2b

@@ -319,6 +319,35 @@ def test_unaligned_qkv_take_generic_kernels(gpu_device, name):
     run_batch_case(o, [1, 37, 300], [0, 36, 211], seed=7, fused=False, misalign=4)
 
 
+SHORT_SHAPES = sorted(n for n in SHAPES if "generic" not in n)
+
+
+@pytest.mark.parametrize("name", SHORT_SHAPES)
+@pytest.mark.parametrize("norm", ["none", "qk"])
+def test_short_contexts_vs_oracle(gpu_device, name, norm):
+    """Every pos below 128 and no weights output: the short-context kernel
+    (one workgroup per KV head, sequence and layer; output written over q,
+    no combine) - outputs within the bars and K/V bytes bit-exact against
+    the oracle, all layers in one call and layer by layer, pos 0 and 127
+    (the last position it takes) included; then the same inputs through the
+    split kernel (an explicit split length of 64 keeps it)."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    seed = zlib.crc32(name.encode()) % 1000 + (7 if norm == "qk" else 0)
+    norms = None
+    if norm == "qk":
+        qn = (1 + 0.25 * orc.normal(seed + 40, 2 * hd)).reshape(2, hd)
+        kn = (1 + 0.25 * orc.normal(seed + 41, 2 * hd)).reshape(2, hd)
+        norms = (qn, kn, 1e-6)
+    caps, poss = [1, 2, 37, 128, 129], [0, 1, 36, 127, 64]
+    print(f"[short] {name} norm={norm}", flush=True)
+    a = run_batch_case(o, caps, poss, seed, fused=True, want_att=False, norms=norms)
+    b = run_batch_case(o, caps, poss, seed, fused=False, want_att=False, norms=norms)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    run_batch_case(o, caps, poss, seed, fused=True, want_att=False, norms=norms,
+                   tune=(64, 0, 0, 0))
+
+
 QKN_SHAPES = {
     # name: (SHAPES entry, which norms, eps)
     "qwen3_q8_g2": ("qwen3_q8_g2", "qk", 1e-6),
