@@ -13,7 +13,9 @@
 // own slice of the new row bit-exactly with the shared block quantiser.
 //
 // Per workgroup (256 threads, four waves):
-//   1. q of the group's G heads and the new k into LDS (one float4 each).
+//   1. q of the group's G heads and the new k and v into LDS (one float4
+//      each); then every KV load of the call is issued at once (K pieces of
+//      positions < pos, and each wave's V elements), to land during 2-4.
 //   2. QK-RMSNorm factors: one thread per head, squares summed left to right
 //      (qk_rmsnorm_block's order); inv = 1/sqrtf(ss/hd + eps).
 //   3. (w * x) * inv, then the RoPE rotation of pos, per pair (ia, ib).
@@ -45,67 +47,94 @@ struct ShortGeom {
   static constexpr int EPL = HD / 64;                // V elements per lane
 };
 
-// Piece b (elements 32b..32b+31) of a head slice (4-byte aligned; global or
-// LDS) as 32 floats before the Q8_0 scale, and the scale (1 for F32).
-// Q8_0: block b starts at byte 34b; the nine dwords from (34b) & ~3 cover
-// it (two bytes early for odd b, two bytes into block b+1 for even b, which
-// exists: NB is even), so the window never leaves the slice.
+// Raw bytes of piece b (elements 32b..32b+31) of a head slice (4-byte
+// aligned; global or LDS).  Q8_0: block b starts at byte 34b; the nine
+// dwords from (34b) & ~3 cover it (two bytes early for odd b, two bytes into
+// block b+1 for even b, which exists: NB is even), so the window never
+// leaves the slice.  F32: eight float4s.
 template <int FMT>
-__device__ __forceinline__ float load_piece(const uint8_t *slice, int b, float (&x)[32]) {
+struct PieceRaw {
+  uint32_t d[9];
+};
+template <>
+struct PieceRaw<0> {
+  float4 f[8];
+};
+
+template <int FMT>
+__device__ __forceinline__ void fetch_piece(const uint8_t *slice, int b, PieceRaw<FMT> &r) {
   if constexpr (FMT == 1) {
     const uint32_t *w = reinterpret_cast<const uint32_t *>(slice + ((34 * b) & ~3));
-    uint32_t d[9];
 #pragma unroll
-    for (int i = 0; i < 9; i++) d[i] = w[i];
+    for (int i = 0; i < 9; i++) r.d[i] = w[i];
+  } else {
+    const float4 *p = reinterpret_cast<const float4 *>(slice + 128 * b);
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.f[i] = p[i];
+  }
+}
+
+// The piece as 32 floats before the Q8_0 scale; returns the scale (1 for F32).
+template <int FMT>
+__device__ __forceinline__ float decode_piece(const PieceRaw<FMT> &r, int b, float (&x)[32]) {
+  if constexpr (FMT == 1) {
     const bool odd = (b & 1) != 0;
-    const float scale = half_bits_to_f32_hw(odd ? (d[0] >> 16) : (d[0] & 0xFFFFu));
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const uint32_t q = odd ? d[i + 1] : __builtin_amdgcn_alignbit(d[i + 1], d[i], 16);
+      const uint32_t q = odd ? r.d[i + 1] : __builtin_amdgcn_alignbit(r.d[i + 1], r.d[i], 16);
       x[4 * i + 0] = (float)(int8_t)(q & 0xFFu);
       x[4 * i + 1] = (float)(int8_t)((q >> 8) & 0xFFu);
       x[4 * i + 2] = (float)(int8_t)((q >> 16) & 0xFFu);
       x[4 * i + 3] = (float)(int8_t)(q >> 24);
     }
-    return scale;
+    return half_bits_to_f32_hw(odd ? (r.d[0] >> 16) : (r.d[0] & 0xFFFFu));
   } else {
-    const float4 *p = reinterpret_cast<const float4 *>(slice + 128 * b);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const float4 v = p[i];
-      x[4 * i + 0] = v.x;
-      x[4 * i + 1] = v.y;
-      x[4 * i + 2] = v.z;
-      x[4 * i + 3] = v.w;
+      x[4 * i + 0] = r.f[i].x;
+      x[4 * i + 1] = r.f[i].y;
+      x[4 * i + 2] = r.f[i].z;
+      x[4 * i + 3] = r.f[i].w;
     }
     return 1.f;
   }
 }
 
-// V elements e0 .. e0 + EPL - 1 (e0 a multiple of EPL) of a head slice,
-// dequantised as kv_val_row does (d * q).
+// Raw bytes of V elements e0 .. e0 + EPL - 1 (e0 a multiple of EPL) of a
+// head slice: Q8_0 the quants (q) and the block's scale bits (s); F32 the
+// values' bits (q, and s for the second).
 template <int FMT, int EPL>
-__device__ __forceinline__ void load_v(const uint8_t *slice, int e0, float (&v)[EPL]) {
+__device__ __forceinline__ void fetch_v(const uint8_t *slice, int e0, uint32_t &q, uint32_t &s) {
   if constexpr (FMT == 1) {
-    const int b = e0 >> 5;
-    const uint8_t *blk = slice + 34 * b;
-    const float d = half_bits_to_f32_hw(*reinterpret_cast<const uint16_t *>(blk));
-    if constexpr (EPL == 2) {
-      const uint32_t q = *reinterpret_cast<const uint16_t *>(blk + 2 + (e0 & 31));
-      v[0] = d * (float)(int8_t)(q & 0xFFu);
-      v[1] = d * (float)(int8_t)(q >> 8);
-    } else {
-      v[0] = d * (float)(int8_t)blk[2 + (e0 & 31)];
-    }
+    const uint8_t *blk = slice + 34 * (e0 >> 5);
+    s = *reinterpret_cast<const uint16_t *>(blk);
+    if constexpr (EPL == 2)
+      q = *reinterpret_cast<const uint16_t *>(blk + 2 + (e0 & 31));
+    else
+      q = blk[2 + (e0 & 31)];
   } else {
-    const float *f = reinterpret_cast<const float *>(slice) + e0;
+    const uint32_t *f = reinterpret_cast<const uint32_t *>(slice) + e0;
     if constexpr (EPL == 2) {
-      const float2 t = *reinterpret_cast<const float2 *>(f);
-      v[0] = t.x;
-      v[1] = t.y;
+      const uint2 t = *reinterpret_cast<const uint2 *>(f);
+      q = t.x;
+      s = t.y;
     } else {
-      v[0] = f[0];
+      q = f[0];
+      s = 0u;
     }
+  }
+}
+
+// Dequantised as kv_val_row does (d * q).
+template <int FMT, int EPL>
+__device__ __forceinline__ void decode_v(uint32_t q, uint32_t s, float (&v)[EPL]) {
+  if constexpr (FMT == 1) {
+    const float d = half_bits_to_f32_hw(s);
+    v[0] = d * (float)(int8_t)(q & 0xFFu);
+    if constexpr (EPL == 2) v[1] = d * (float)(int8_t)((q >> 8) & 0xFFu);
+  } else {
+    v[0] = __uint_as_float(q);
+    if constexpr (EPL == 2) v[1] = __uint_as_float(s);
   }
 }
 
@@ -126,7 +155,11 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   using Geo = ShortGeom<FMT, HD>;
   constexpr int NB = Geo::NB, HB = Geo::HB, XS = Geo::XS, EPL = Geo::EPL;
   constexpr int half = HD / 2;
-  __shared__ __align__(16) float xs[(kSMaxG + 1) * XS];  // q heads 0..G-1, then k
+  constexpr int PPR = kSThreads / NB;                      // score positions per round
+  constexpr int RK = (kShortMaxPos + PPR - 1) / PPR;       // score rounds
+  constexpr int VI = kShortMaxPos / 4;                     // V positions per wave
+  // q heads 0..G-1, the new k (row G) and the new v (row G + 1)
+  __shared__ __align__(16) float xs[(kSMaxG + 2) * XS];
   __shared__ __align__(16) uint8_t rowk[Geo::HBP], rowv[Geo::HBP];
   __shared__ float sc[kSMaxG * kShortMaxPos];  // scores, then weights
   __shared__ __align__(16) float accs[4 * kSMaxG * HD];
@@ -148,15 +181,40 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   const float *ki = P.k_in + sidx * nkv + (size_t)kvh * HD;
   const float *vi = P.v_in + sidx * nkv + (size_t)kvh * HD;
   const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  const uint32_t row = sh.row_bytes;
+  const size_t lay = (size_t)layer * (size_t)sd.ctx_cap;
+  uint8_t *const kb = sd.k + lay * row + (size_t)kvh * HB;
+  uint8_t *const vb = sd.v + lay * row + (size_t)kvh * HB;
 
-  // 1. q (G heads) and k into LDS
+  // 1. q (G heads), k and v: one float4 per thread, into registers first
   constexpr int P4 = HD / 4;
-  for (int i = t; i < (G + 1) * P4; i += kSThreads) {
-    const int h = i / P4, j = i - h * P4;
-    const float *src = h < G ? qo + h * HD : ki;
-    *reinterpret_cast<float4 *>(xs + h * XS + 4 * j) =
-        *reinterpret_cast<const float4 *>(src + 4 * j);
+  const bool has_x = t < (G + 2) * P4;
+  const int xh = t / P4, xj = t - xh * P4;
+  float4 x4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (has_x) {
+    const float *src = xh < G ? qo + xh * HD : (xh == G ? ki : vi);
+    x4 = *reinterpret_cast<const float4 *>(src + 4 * xj);
   }
+  // Every KV load of the call is issued now, so that it is in flight during
+  // the setup: the K pieces of positions < pos (each thread one piece per
+  // round) and, per wave, the V elements of positions wave, wave + 4, ...
+  // below pos.  Positions at or past pos read row 0 instead (in bounds,
+  // never used), which keeps the loads unconditional.
+  const int b = t % NB;
+  PieceRaw<FMT> kraw[RK];
+#pragma unroll
+  for (int r = 0; r < RK; r++) {
+    const int tp = r * PPR + t / NB;
+    fetch_piece<FMT>(kb + (size_t)(tp < pos ? tp : 0) * row, b, kraw[r]);
+  }
+  const int e0 = lane * EPL;
+  uint32_t vq[VI], vsb[VI];
+#pragma unroll
+  for (int i = 0; i < VI; i++) {
+    const int tp = wave + 4 * i;
+    fetch_v<FMT, EPL>(vb + (size_t)(tp < pos ? tp : 0) * row, e0, vq[i], vsb[i]);
+  }
+  if (has_x) *reinterpret_cast<float4 *>(xs + xh * XS + 4 * xj) = x4;
   const float *wq = norm_weights(P.norm, layer, 0, HD);
   const float *wk = norm_weights(P.norm, layer, 1, HD);
   __syncthreads();
@@ -191,61 +249,57 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     int ia, ib;
     rope_pair_index(sh.arch_llama, j, half, ia, ib);
     float *x = xs + h * XS;
-    float a = x[ia], b = x[ib];
+    float a = x[ia], c = x[ib];
     if (const float *w = h < G ? wq : wk) {
       const float f = inv[h];
       a = (w[ia] * a) * f;
-      b = (w[ib] * b) * f;
+      c = (w[ib] * c) * f;
     }
-    if (cs) rope_pair(a, b, cs[2 * j], cs[2 * j + 1]);
+    if (cs) rope_pair(a, c, cs[2 * j], cs[2 * j + 1]);
     x[ia] = a;
-    x[ib] = b;
+    x[ib] = c;
   }
   __syncthreads();
 
   // 4. the new row's slice: LDS copy, then the caches
-  const float *kr = xs + G * XS;
+  const float *kr = xs + G * XS, *vr = xs + (G + 1) * XS;
   if constexpr (FMT == 1) {
     if (t < 8 * NB) {  // blocks 0..NB-1 of k, then of v; four lanes each
-      const int b = t >> 2, part = t & 3;
-      const bool is_k = b < NB;
-      const int bb = is_k ? b : b - NB;
-      q8_quant_block_x4((is_k ? kr : vi) + 32 * bb, 32, (is_k ? rowk : rowv) + 34 * bb, part);
+      const int bq = t >> 2, part = t & 3;
+      const bool is_k = bq < NB;
+      const int bb = is_k ? bq : bq - NB;
+      q8_quant_block_x4((is_k ? kr : vr) + 32 * bb, 32, (is_k ? rowk : rowv) + 34 * bb, part);
     }
   } else {
     for (int i = t; i < 2 * P4; i += kSThreads) {
       const bool is_k = i < P4;
       const int j = is_k ? i : i - P4;
-      const float4 v = *reinterpret_cast<const float4 *>((is_k ? kr : vi) + 4 * j);
+      const float4 v = *reinterpret_cast<const float4 *>((is_k ? kr : vr) + 4 * j);
       *reinterpret_cast<float4 *>((is_k ? rowk : rowv) + 16 * j) = v;
     }
   }
   __syncthreads();
-  const uint32_t row = sh.row_bytes;
-  const size_t lay = (size_t)layer * (size_t)sd.ctx_cap;
-  uint8_t *const kb = sd.k + lay * row + (size_t)kvh * HB;
-  uint8_t *const vb = sd.v + lay * row + (size_t)kvh * HB;
   {
     constexpr int W = HB / 4;  // dwords of a slice (HB is a multiple of 4)
     const size_t off = (size_t)pos * row;
     for (int i = t; i < 2 * W; i += kSThreads) {
       const bool is_k = i < W;
       const int j = is_k ? i : i - W;
-      uint8_t *dst = (is_k ? kb : vb) + off;
-      reinterpret_cast<uint32_t *>(dst)[j] =
+      reinterpret_cast<uint32_t *>((is_k ? kb : vb) + off)[j] =
           reinterpret_cast<const uint32_t *>(is_k ? rowk : rowv)[j];
     }
   }
 
-  // 5. scores
+  // 5. scores: position tp's NB pieces on NB consecutive lanes
   const float qscale = P.qscale;
-  constexpr int PPR = kSThreads / NB;  // positions per round
-  for (int t0 = 0; t0 <= pos; t0 += PPR) {
-    const int tp = t0 + t / NB, b = t % NB;
+#pragma unroll
+  for (int r = 0; r < RK; r++) {
+    const int tp = r * PPR + t / NB;
     if (tp <= pos) {  // (uniform over a position's NB lanes)
-      const uint8_t *slice = tp < pos ? kb + (size_t)tp * row : rowk;
+      PieceRaw<FMT> pr = kraw[r];
+      if (tp == pos) fetch_piece<FMT>(rowk, b, pr);
       float k[32];
-      const float d = load_piece<FMT>(slice, b, k);
+      const float d = decode_piece<FMT>(pr, b, k);
 #pragma unroll
       for (int g = 0; g < kSMaxG; g++) {
         if (g < G) {
@@ -286,24 +340,27 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   }
   __syncthreads();
 
-  // 7. V-accumulate, wave w over positions w, w + 4, ...
-  const int e0 = lane * EPL;
+  // 7. V-accumulate, wave w over positions w, w + 4, ... (pos itself from LDS)
   float acc[kSMaxG][EPL];
 #pragma unroll
   for (int g = 0; g < kSMaxG; g++)
 #pragma unroll
     for (int i = 0; i < EPL; i++) acc[g][i] = 0.f;
-#pragma unroll 4
-  for (int tp = wave; tp <= pos; tp += 4) {
-    const uint8_t *slice = tp < pos ? vb + (size_t)tp * row : rowv;
-    float v[EPL];
-    load_v<FMT, EPL>(slice, e0, v);
 #pragma unroll
-    for (int g = 0; g < kSMaxG; g++) {
-      if (g < G) {
-        const float p = sc[g * kShortMaxPos + tp];
+  for (int i = 0; i < VI; i++) {
+    const int tp = wave + 4 * i;
+    if (tp <= pos) {
+      uint32_t q = vq[i], sb = vsb[i];
+      if (tp == pos) fetch_v<FMT, EPL>(rowv, e0, q, sb);
+      float v[EPL];
+      decode_v<FMT, EPL>(q, sb, v);
 #pragma unroll
-        for (int i = 0; i < EPL; i++) acc[g][i] = fmaf(p, v[i], acc[g][i]);
+      for (int g = 0; g < kSMaxG; g++) {
+        if (g < G) {
+          const float p = sc[g * kShortMaxPos + tp];
+#pragma unroll
+          for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, v[e], acc[g][e]);
+        }
       }
     }
   }
