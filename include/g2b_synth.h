@@ -52,7 +52,9 @@ int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
  * to LDS; automatic: 2 wherever the row is a whole number of 16-byte pieces,
  * else -1), piece = the work-queue schedule (-1 static splits only, > 0
  * positions per claimed piece; automatic: work queue when every (sequence,
- * layer) of the call can have a resident workgroup). */
+ * layer) of the call can have a resident workgroup).  Contexts below 128
+ * positions without the weights output run the short-context kernel (one
+ * workgroup per KV head) unless split_len > 0 or piece != 0 is set. */
 int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t chunk, int32_t stage, int32_t piece);
 
 /* Kernel timing with HIP events on the context's stream: while enabled,
