@@ -8,23 +8,27 @@ head_dim 128, NEOX RoPE theta 1e6, Q8_0 KV (~128 GB resident in HBM).
 
 One step = for every sequence and layer: RoPE(q, k), append k/v at pos,
 attention over pos+1 positions, output over q.  The timed step is
-layer-serial (28 g2b_attn_layers calls, each one k_layer launch - RoPE,
-append, attention over the splits - and one k_combine launch that merges
-the split partials), as a real model's layer loop would run it; a
-one-call-for-all-layers variant is reported beside it.  Inputs are synthetic, seeded, generated on the device
-(KV prefill through the same RoPE + append arithmetic) and resident in HBM
-before timing starts.  The q buffer is restored from a pristine copy at the
-start of each step (that 0.1% of traffic is inside the timed region).
+layer-serial (one g2b_attn_layers call per layer: the decode kernel - RoPE,
+append, attention - and, where the schedule splits a sequence, the combine
+launch that merges the split partials), as a real model's layer loop would
+run it; a one-call-for-all-layers variant is reported beside it.  Inputs
+are synthetic, seeded, generated on the device (KV prefill through the same
+RoPE + append arithmetic) and resident in HBM before timing starts.  The q
+buffer is restored from a pristine copy at the start of each step (that
+0.1% of traffic is inside the timed region).
 
 Bytes per step are algorithmic, as BASELINE states them:
   sum over seq, layer of (pos+1)*2*row + 2*row + 4*(2*nq + 2*nkv).
 
-CPU baseline: the C99 oracle (a restatement of the reference path, built
-with the reference flags) on a bounded sample of the same units and the
-same KV bytes the GPU used, timed on the host cores; its outputs double as
-a full-size parity check.  After the headline, the other BASELINE configs
-(c1, c2, c3, c5) are measured the same way (layer-serial and all layers in
-one call) and reported under all_configs.  rank 0 prints one JSON line.
+Every config (the headline, then c1, c2, c3, c5 under all_configs) reports
+the same block: the layer-serial step, its dominant decode kernel against
+the HBM roofline (HIP-event launch time; HBM traffic from the committed
+rocprofv3 summary profiles/traffic_<config>.json), the all-layers call, the
+CPU baseline - the C99 oracle (a restatement of the reference path, built
+with the reference flags) on the same KV bytes and inputs, mode A one thread
+over sequences in turn, mode B OpenMP over sequences - and a full-size
+parity sample (the oracle's outputs and appended rows against the GPU's,
+and two units in float64).  rank 0 prints one JSON line.
 """
 from __future__ import annotations
 
@@ -102,14 +106,21 @@ def launch_bytes(s: attn.Shape, poss, layers_per_launch: int) -> int:
 
 
 def load_traffic(workload: str):
-    """HBM bytes per decode launch measured with rocprofv3 --pmc (FETCH_SIZE,
-    WRITE_SIZE) and scaled by a copy kernel of known size, when that summary
-    has been committed under profiles/."""
-    p = os.path.join(ROOT, "profiles", f"traffic_k_layer_{workload}.json")
+    """HBM bytes per launch of the workload's dominant decode kernel, measured
+    with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by a copy kernel
+    of known size, when that summary has been committed under profiles/."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         return json.load(f)
+
+
+# CPU sample of each config: (sequences run in turn on one thread, sequences
+# over all host threads).  c1/c2 hold one sequence: the whole step, both
+# modes one thread (the reference attention is single-threaded and mode B
+# parallelises over sequences only).
+CPU_SAMPLE = {"c1": (1, 1), "c2": (1, 1), "c3": (8, 64), "c4": (4, 32), "c5": (1, 8)}
 
 
 class Workload:
@@ -188,21 +199,57 @@ class Workload:
         ctx.profile(False)
         return e0.elapsed_ms(e1) / steps, wall / steps * 1e3, dms, nlaunch
 
-    def summary(self, steps, warmup):
-        """Layer-serial and all-layers-in-one-call figures of this config."""
-        ms, _, dms, dn = self.timed(self.step_layer_serial, steps, warmup)
-        fms, _, fdms, fdn = self.timed(self.step_fused, steps, 1)
+    def summary(self, args, steps, warmup, cpu_min_s, fused=True, cpu=True):
+        """Every figure of this config: the layer-serial step (us, GB/s, % of
+        peak), its dominant decode kernel against the HBM roofline (with the
+        committed rocprofv3 traffic), the all-layers-in-one-call step, the
+        CPU baseline in both modes and the full-size parity sample.  Leaves
+        the layer-serial outputs in qw."""
+        ms, wall_ms, dms, dn = self.timed(self.step_layer_serial, steps, warmup)
         sb, L = self.bytes_per_step, self.shape.n_layers
+        gbps = sb / (ms * 1e-3) / 1e9
+        dec_ms = dms / max(dn, 1)
         per_launch = launch_bytes(self.shape, self.poss, 1)
-        return {"workload": self.desc, "n_seq": self.n_seq,
-                "ctx_min": min(self.poss), "ctx_max": max(self.poss),
-                "us_per_step": round(ms * 1e3, 2), "GBps": round(sb / (ms * 1e-3) / 1e9, 2),
-                "pct_hbm_peak": round(100 * sb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
-                "k_layer_avg_us": round(dms / max(dn, 1) * 1e3, 2),
-                "k_layer_GBps": round(per_launch / (dms / max(dn, 1) * 1e-3) / 1e9, 2),
-                "all_layers_one_call_us_per_step": round(fms * 1e3, 2),
-                "all_layers_one_call_GBps": round(sb / (fms * 1e-3) / 1e9, 2),
-                "bytes_per_step": sb}
+        dec_gbps = per_launch / (dec_ms * 1e-3) / 1e9
+        log(f"{self.name}: layer-serial {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), "
+            f"{gbps:.1f} GB/s, {100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak; decode kernel "
+            f"{dn} launches, avg {dec_ms * 1e3:.2f} us, {dec_gbps:.1f} GB/s")
+        traffic = load_traffic(self.name)
+        roof = {"bound": "hbm", "kernel": traffic.get("kernel") if traffic else "decode kernel",
+                "achieved": round(dec_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": per_launch,
+                "avg_launch_us": round(dec_ms * 1e3, 3),
+                "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None}
+        if traffic:
+            roof["traffic_source"] = traffic.get("source")
+            roof["traffic_over_algorithmic"] = traffic.get("traffic_over_algorithmic")
+        out = {"workload": self.desc, "n_seq": self.n_seq,
+               "ctx_min": min(self.poss), "ctx_max": max(self.poss),
+               "us_per_step": round(ms * 1e3, 2), "GBps": round(gbps, 2),
+               "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+               "bytes_per_step": sb, "kv_fill_s": round(self.t_fill, 2),
+               "step": "layer-serial: one g2b_attn_layers call per layer",
+               "roofline": roof}
+        if fused:
+            fms, _, fdms, fdn = self.timed(self.step_fused, steps, 1)
+            out["all_layers_one_call"] = {
+                "us_per_step": round(fms * 1e3, 2), "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
+                "pct_hbm_peak": round(100 * sb / (fms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+                "decode_kernel_avg_us": round(fdms / max(fdn, 1) * 1e3, 2)}
+            log(f"{self.name}: all layers in one call {fms * 1e3:.1f} us/step, "
+                f"{out['all_layers_one_call']['GBps']} GB/s")
+        # the layer-serial outputs, for the parity sample
+        self.step_layer_serial()
+        self.ctx.sync()
+        if cpu:
+            na, nb = CPU_SAMPLE.get(self.name, (1, 1))
+            if args.cpu_seq_a:
+                na = args.cpu_seq_a
+            if args.cpu_seq_b:
+                nb = args.cpu_seq_b
+            out["cpu_baseline"], out["parity_full_size"] = cpu_leg(self, na, nb, cpu_min_s)
+            out["gpu_over_cpu"] = round(gbps / out["cpu_baseline"]["value"], 1)
+        return out
 
     def close(self):
         for k, v in self.kvs:
@@ -220,17 +267,20 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--n-seq", type=int, default=0, help="override the sequence count")
     ap.add_argument("--seed", type=int, default=20241201)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline and parity legs")
     ap.add_argument("--no-fused", action="store_true", help="skip the all-layers-in-one-call run")
     ap.add_argument("--no-gemv", action="store_true", help="skip the weight-GEMV measurement")
     ap.add_argument("--no-model", action="store_true",
                     help="skip the whole-decode-step (model_forward) measurement")
     ap.add_argument("--no-others", action="store_true",
                     help="skip the other BASELINE configs (reported under all_configs)")
-    ap.add_argument("--cpu-seq-a", type=int, default=4, help="sequences in the 1-thread sample")
-    ap.add_argument("--cpu-seq-b", type=int, default=32, help="sequences in the all-threads sample")
+    ap.add_argument("--cpu-seq-a", type=int, default=0,
+                    help="sequences in the 1-thread sample (0 = the config's default)")
+    ap.add_argument("--cpu-seq-b", type=int, default=0,
+                    help="sequences in the all-threads sample (0 = the config's default)")
     ap.add_argument("--cpu-min-s", type=float, default=8.0,
-                    help="repeat each CPU sample until it has run this long")
+                    help="repeat each CPU sample of the headline config until it has run this "
+                         "long (the other configs: a third of it)")
     ap.add_argument("--split", type=int, default=0, help="static split length (0 = automatic)")
     ap.add_argument("--chunk", type=int, default=0, help="Q8 elements per lane (0 = auto)")
     ap.add_argument("--stage", type=int, default=0, choices=(-1, 0, 1, 2),
@@ -261,8 +311,7 @@ def main():
         return
 
     w = Workload(args.config, args, args.n_seq)
-    ctx, shape, poss, caps, kvs = w.ctx, w.shape, w.poss, w.caps, w.kvs
-    L, n_seq = shape.n_layers, w.n_seq
+    ctx, shape, poss = w.ctx, w.shape, w.poss
     if args.calibrate_copy:
         nb = args.calibrate_copy << 20
         src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
@@ -278,7 +327,7 @@ def main():
             ctx.tune(sl, args.chunk, args.stage, -1)
             sms, _, sd, sn = w.timed(w.step_layer_serial, max(3, args.steps // 2), 1)
             log(f"split {sl}: {sms * 1e3:.1f} us/step, {sb / sms / 1e6:.1f} GB/s, "
-                f"k_layer avg {sd / max(sn, 1) * 1e3:.1f} us")
+                f"decode kernel avg {sd / max(sn, 1) * 1e3:.1f} us")
         ctx.tune(args.split, args.chunk, args.stage, args.piece)
     if args.sweep_variants:
         for v in args.sweep_variants.split(";"):
@@ -287,39 +336,13 @@ def main():
             sms, _, sd, sn = w.timed(w.step_layer_serial, max(3, args.steps // 2), 1)
             fms, _, fd, fn = w.timed(w.step_fused, max(3, args.steps // 2), 1)
             log(f"variant split={sl} chunk={ch} stage={st} piece={pc}: layer-serial "
-                f"{sms * 1e3:.1f} us/step ({sb / sms / 1e6:.1f} GB/s, k_layer "
+                f"{sms * 1e3:.1f} us/step ({sb / sms / 1e6:.1f} GB/s, decode kernel "
                 f"{sd / max(sn, 1) * 1e3:.1f} us), fused {fms * 1e3:.1f} us/step "
                 f"({sb / fms / 1e6:.1f} GB/s)")
         ctx.tune(args.split, args.chunk, args.stage, args.piece)
 
-    ms, wall_ms, dec_ms, dec_n = w.timed(w.step_layer_serial, args.steps, args.warmup)
-    gbps = sb / (ms * 1e-3) / 1e9
-    log(f"layer-serial: {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), {gbps:.1f} GB/s, "
-        f"{100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak")
-    dec_avg_ms = dec_ms / max(dec_n, 1)
-    dec_bytes = launch_bytes(shape, poss, 1)
-    dec_gbps = dec_bytes / (dec_avg_ms * 1e-3) / 1e9
-    log(f"k_layer: {dec_n} launches, avg {dec_avg_ms * 1e3:.1f} us, {dec_gbps:.1f} GB/s")
-
-    fused = None
-    if not args.no_fused:
-        fms, fwall, fdec, fn = w.timed(w.step_fused, args.steps, 1)
-        fused = {"us_per_step": round(fms * 1e3, 2),
-                 "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
-                 "k_layer_avg_us": round(fdec / max(fn, 1) * 1e3, 2),
-                 "k_layer_GBps": round(launch_bytes(shape, poss, L) /
-                                       (fdec / max(fn, 1) * 1e-3) / 1e9, 2)}
-        log(f"all layers in one call: {fms * 1e3:.1f} us/step, {fused['GBps']} GB/s")
-
-    # Leave the layer-serial outputs in qw for the parity sample.
-    w.step_layer_serial()
-    ctx.sync()
-
-    cpu = None
-    parity = None
-    if not args.no_cpu:
-        cpu, parity = cpu_leg(args, ctx, shape, poss, caps, kvs, w.q0, w.qw, w.kb, w.vb)
-    t_fill = w.t_fill
+    head = w.summary(args, args.steps, args.warmup, args.cpu_min_s, fused=not args.no_fused,
+                     cpu=not args.no_cpu)
     w.close()
 
     others = None
@@ -329,42 +352,34 @@ def main():
             if name == args.config:
                 continue
             o = Workload(name, args)
-            others[name] = o.summary(max(5, args.steps // 2), 2)
-            log(f"{name}: layer-serial {others[name]['us_per_step']} us/step "
-                f"({others[name]['GBps']} GB/s, {others[name]['pct_hbm_peak']}% of HBM peak), "
-                f"all layers in one call {others[name]['all_layers_one_call_us_per_step']} us/step")
+            others[name] = o.summary(args, max(5, args.steps // 2), 2, args.cpu_min_s / 3,
+                                     cpu=not args.no_cpu)
             o.close()
 
     gemv = None if args.no_gemv else gemv_leg(args)
     model = None if args.no_model else model_leg(args)
 
-    traffic = load_traffic(args.config)
-    roof = {"bound": "hbm", "kernel": "k_layer", "achieved": round(dec_gbps, 2),
-            "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(dec_gbps / HBM_PEAK_GBPS, 4),
-            "bytes_per_launch": dec_bytes, "avg_launch_us": round(dec_avg_ms * 1e3, 2),
-            "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None}
-    if traffic:
-        roof["traffic_source"] = traffic.get("source")
-
+    ms = head["us_per_step"] * 1e-3
+    gbps = head["GBps"]
     line = {
-        "metric": METRIC, "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1,
+        "metric": METRIC, "value": gbps, "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"{args.config}: {w.desc}", "n_seq": n_seq,
-                   "ctx_min": min(poss), "ctx_max": max(poss), "layers": L,
+        "config": {"workload": f"{args.config}: {w.desc}", "n_seq": w.n_seq,
+                   "ctx_min": min(poss), "ctx_max": max(poss), "layers": shape.n_layers,
                    "n_heads": shape.n_heads, "n_kv_heads": shape.n_kv_heads,
                    "head_dim": shape.head_dim, "kv": "q8_0" if shape.kv_q8 else "f32",
-                   "step": "layer-serial: per layer one g2b_attn_layers call = k_layer + k_combine",
+                   "step": "layer-serial: per layer one g2b_attn_layers call",
                    "parallelism": "single GPU"},
-        "us_per_step": round(ms * 1e3, 2),
-        "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "us_per_step": head["us_per_step"],
+        "pct_hbm_peak": head["pct_hbm_peak"],
         "bytes_per_step": sb,
-        "kv_fill_s": round(t_fill, 2),
-        "roofline": roof,
-        "cpu_baseline": cpu,
-        "all_layers_one_call": fused,
-        "parity_full_size": parity,
+        "kv_fill_s": head["kv_fill_s"],
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "all_layers_one_call": head.get("all_layers_one_call"),
+        "parity_full_size": head.get("parity_full_size"),
         "all_configs": others,
         "gemv": gemv,
         "model_forward": model,
@@ -511,35 +526,46 @@ def model_leg(args):
         os.unlink(path)
 
 
-def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):
-    """Time the oracle on a bounded sample of the same units (same KV bytes,
-    same inputs) and compare its outputs and appended rows with the GPU's."""
+def cpu_leg(w: Workload, na: int, nb: int, min_s: float):
+    """The CPU baseline and the full-size parity sample of one config: the
+    oracle (a C99 restatement of the reference path, built with the
+    reference's flags) on the first nb sequences x every layer, with the KV
+    bytes and inputs the GPU used, in mode A (the first na sequences in turn
+    on one thread, as the reference's single-threaded attention runs them)
+    and mode B (OpenMP over the nb sequences, all host threads), each
+    repeated for at least min_s seconds.  Its outputs are compared with the
+    GPU's layer-serial outputs, the appended rows byte for byte, and two
+    (sequence, layer) units are also evaluated in float64 from the same
+    bytes."""
     from oracle import orc  # CPU baseline and checker only
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from helpers import exact_attention  # float64 checker
 
+    shape, poss, caps, kvs = w.shape, w.poss, w.caps, w.kvs
     o = orc.Shape(shape.n_layers, shape.n_heads, shape.n_kv_heads, shape.head_dim,
                   shape.rope_theta, shape.arch, shape.kv_q8)
     L, nq, nkv, rb = shape.n_layers, shape.nq, shape.nkv, row_bytes(shape)
     n_seq = len(poss)
-    nb = max(1, min(args.cpu_seq_b, n_seq))
-    na = max(1, min(args.cpu_seq_a, nb))
+    nb = max(1, min(nb, n_seq))
+    na = max(1, min(na, nb))
     idx = list(range(nb))
     nQ, nK = L * n_seq * nq, L * n_seq * nkv
-    q_all = q0.download(np.float32, nQ).reshape(L, n_seq, nq)
-    k_all = kb.download(np.float32, nK).reshape(L, n_seq, nkv)
-    v_all = vb.download(np.float32, nK).reshape(L, n_seq, nkv)
-    out_gpu = qw.download(np.float32, nQ).reshape(L, n_seq, nq)
+    q_all = w.q0.download(np.float32, nQ).reshape(L, n_seq, nq)
+    k_all = w.kb.download(np.float32, nK).reshape(L, n_seq, nkv)
+    v_all = w.vb.download(np.float32, nK).reshape(L, n_seq, nkv)
+    out_gpu = w.qw.download(np.float32, nQ).reshape(L, n_seq, nq)
     t0 = time.perf_counter()
     host = []
     for i in idx:
         nbytes = attn.kv_bytes(shape, caps[i])
         host.append((hip.copy_d2h(kvs[i][0], np.uint8, nbytes),
                      hip.copy_d2h(kvs[i][1], np.uint8, nbytes)))
-    log(f"cpu sample: {nb} sequences copied to host in {time.perf_counter() - t0:.1f}s")
+    log(f"{w.name} cpu sample: {nb} sequences copied to host in {time.perf_counter() - t0:.1f}s")
     gpu_rows = [(kc.reshape(L, caps[i], rb)[:, poss[i]].copy(),
                  vc.reshape(L, caps[i], rb)[:, poss[i]].copy()) for i, (kc, vc) in zip(idx, host)]
 
     def sample(ids, threads):
-        """Run the sample repeatedly for at least --cpu-min-s; seconds per pass."""
+        """Run the sample repeatedly for at least min_s; seconds per pass."""
         pos = np.array([poss[i] for i in ids], np.int32)
         cap = np.array([caps[i] for i in ids], np.int32)
         sel = np.array(ids)
@@ -548,27 +574,36 @@ def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):
         v = np.ascontiguousarray(v_all[:, sel])
         reps, t = 0, orc.now()
         while True:
+            # (the appended rows are rewritten with the same bytes every pass)
             out = orc.attn_batch(o, 0, L, pos, cap, [host[j][0] for j in range(len(ids))],
                                  [host[j][1] for j in range(len(ids))], q, k, v, threads)
             reps += 1
-            if orc.now() - t >= args.cpu_min_s:
+            if orc.now() - t >= min_s:
                 break
         return (orc.now() - t) / reps, out, reps
 
-    threads = orc.max_threads()
+    threads = orc.max_threads() if nb > 1 else 1
     ta, out_a, reps_a = sample(idx[:na], 1)
     tb, out_b, reps_b = sample(idx, threads)
     bytes_a = step_bytes(shape, [poss[i] for i in idx[:na]])
     bytes_b = step_bytes(shape, [poss[i] for i in idx])
     gbps_a, gbps_b = bytes_a / ta / 1e9, bytes_b / tb / 1e9
-    log(f"cpu: 1 thread {gbps_a:.2f} GB/s ({reps_a} x {ta:.2f}s), {threads} threads "
-        f"{gbps_b:.2f} GB/s ({reps_b} x {tb:.2f}s)")
+    log(f"{w.name} cpu: 1 thread {gbps_a:.2f} GB/s ({reps_a} x {ta:.3f}s), {threads} threads "
+        f"{gbps_b:.2f} GB/s ({reps_b} x {tb:.3f}s)")
 
     err = float(np.max(np.abs(out_b - out_gpu[:, idx])))
     rows_exact = all(
         np.array_equal(host[j][0].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][0]) and
         np.array_equal(host[j][1].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][1])
         for j, i in enumerate(idx))
+    # float64 evaluation of two units (the first and last sampled sequence,
+    # first and last layer) from the same cache bytes
+    f64_gpu = f64_orc = 0.0
+    for j, layer in ((0, 0), (len(idx) - 1, L - 1)):
+        i = idx[j]
+        ex = exact_attention(o, caps[i], layer, poss[i], host[j][0], host[j][1], q_all[layer, i])
+        f64_gpu = max(f64_gpu, float(np.max(np.abs(out_gpu[layer, i] - ex))))
+        f64_orc = max(f64_orc, float(np.max(np.abs(out_b[layer, j] - ex))))
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -578,17 +613,25 @@ def cpu_leg(args, ctx, shape, poss, caps, kvs, q0, qw, kb, vb):
                     break
     except OSError:
         pass
+    mode_b = ("OpenMP over sequences, all host threads" if threads > 1 else
+              "one sequence: the reference attention has no threads inside a sequence")
     cpu = {"value": round(gbps_b, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-           "sample": f"{nb} of {len(poss)} sequences x {L} layers (all host threads, OpenMP "
-                     f"over sequences), same KV bytes and inputs as the GPU, {reps_b} passes",
+           "sample": f"{nb} of {n_seq} sequences x {L} layers ({mode_b}), same KV bytes and "
+                     f"inputs as the GPU, {reps_b} passes",
+           "us_per_step_of_sample": round(tb * 1e6, 1),
            "seconds": round(tb * reps_b, 2), "cpu": cpu_model,
            "one_thread": {"value": round(gbps_a, 3), "unit": "GB/s", "cores": 1,
                           "sample": f"{na} sequences x {L} layers, sequences in turn "
                                     f"(the reference attention is single-threaded), "
                                     f"{reps_a} passes",
+                          "us_per_step_of_sample": round(ta * 1e6, 1),
                           "seconds": round(ta * reps_a, 2)}}
     parity = {"units_checked": nb * L, "max_abs_out_err_vs_oracle": err,
-              "appended_rows_bit_exact": bool(rows_exact)}
+              "appended_rows_bit_exact": bool(rows_exact),
+              "float64_units": 2, "max_abs_out_err_gpu_vs_float64": f64_gpu,
+              "max_abs_out_err_oracle_vs_float64": f64_orc}
+    log(f"{w.name} parity: {nb * L} units, max |gpu - oracle| {err:.3g}, rows bit-exact "
+        f"{rows_exact}, float64: gpu {f64_gpu:.3g}, oracle {f64_orc:.3g}")
     return cpu, parity
 
 

@@ -28,7 +28,8 @@ ARCH_LLAMA, ARCH_QWEN2, ARCH_QWEN3 = 0, 1, 2
 EXPORTS = [
     "g2b_ctx_create", "g2b_ctx_destroy", "g2b_ctx_set_stream", "g2b_ctx_stream",
     "g2b_strerror", "g2b_ctx_last_error", "g2b_kv_row_bytes", "g2b_kv_bytes",
-    "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_append_rows", "g2b_set_qk_norm",
+    "g2b_kv_offset", "g2b_kv_alloc", "g2b_kv_free", "g2b_kv_read", "g2b_kv_append_rows",
+    "g2b_set_qk_norm",
     "g2b_model_kv_bytes", "g2b_clamp_ctx", "g2b_hbm_bytes", "g2b_auto_budget", "g2b_hbm_info",
     "g2b_matmul_row_bytes", "g2b_matmul", "g2b_matmul_host", "g2b_weights_upload",
     "g2b_weights_free", "g2b_g2bx_open", "g2b_g2bx_close", "g2b_g2bx_slot",
@@ -147,6 +148,7 @@ def lib() -> C.CDLL:
             "g2b_weights_free": ([vp, vp], C.c_int),
             "g2b_kv_alloc": ([vp, i32, C.POINTER(vp), C.POINTER(vp)], C.c_int),
             "g2b_kv_free": ([vp, vp, vp], C.c_int),
+            "g2b_kv_read": ([vp, vp, u64, u64, vp], C.c_int),
             "g2b_kv_append_rows": ([vp, vp, vp, i32, i32, i32, i32, fp, fp], C.c_int),
             "g2b_set_qk_norm": ([vp, i32, vp, vp, C.c_float], C.c_int),
             "g2b_batch_begin": ([vp, i32, C.POINTER(_Seq)], C.c_int),
@@ -387,6 +389,13 @@ class Context:
 
     def kv_free(self, k: int, v: int):
         self._check(lib().g2b_kv_free(self.h, k, v), "g2b_kv_free")
+
+    def kv_read(self, cache: int, offset: int, nbytes: int) -> np.ndarray:
+        """nbytes of a device cache from byte offset, as host uint8."""
+        out = np.empty(nbytes, np.uint8)
+        self._check(lib().g2b_kv_read(self.h, cache, offset, nbytes, out.ctypes.data),
+                    "g2b_kv_read")
+        return out
 
     def kv_append_rows(self, kc: int, vc: int, ctx_cap: int, layer: int, pos0: int,
                        n_rows: int, k_dev: int, v_dev: int):

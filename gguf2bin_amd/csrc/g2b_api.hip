@@ -17,6 +17,7 @@
 
 #include "g2b_attn.h"
 #include "g2b_internal.h"
+#include "g2b_limits.h"
 #include "g2b_matmul.h"
 #include "g2b_synth.h"
 
@@ -101,9 +102,10 @@ size_t row_bytes_of(const g2b_shape *s) {
   return s->kv_q8 ? (nkv + 31u) / 32u * 34u : nkv * 4u;
 }
 
-// Readable slack after each cache: the specialised loaders fetch whole
-// dwords around 34-byte blocks.
-constexpr size_t kKvSlack = 256;
+constexpr size_t kKvSlack = G2B_KV_SLACK;
+static_assert(sizeof(SeqDev) == G2B_SEQ_DESC_BYTES, "descriptor size the budget assumes");
+static_assert(kPartHead == (int)G2B_PART_HEAD, "partial layout the budget assumes");
+static_assert(kWqStride * sizeof(int32_t) == G2B_WQ_LINE_BYTES, "counter line the budget assumes");
 
 // The staged KV loads read 16-byte pieces from the cache bases.
 bool misaligned(const void *p) { return ((uintptr_t)p & 15u) != 0; }
@@ -114,9 +116,11 @@ int set_device(g2b_ctx *c) {
 }
 
 // Grow a device buffer (contents are not kept); waits for queued work first.
-int grow(g2b_ctx *c, float **buf, size_t *cap, size_t need_floats) {
+// Grows by half again at least, but never past limit_floats (>= need_floats),
+// the size g2b_hbm_bytes budgets for the buffer.
+int grow(g2b_ctx *c, float **buf, size_t *cap, size_t need_floats, size_t limit_floats) {
   if (*cap >= need_floats) return G2B_OK;
-  size_t n = std::max(need_floats, *cap + *cap / 2);
+  size_t n = std::max(need_floats, std::min(*cap + *cap / 2, limit_floats));
   if (*buf) {
     G2B_HIP(c, hipStreamSynchronize(c->stream));
     G2B_HIP(c, hipFree(*buf));
@@ -289,6 +293,11 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // the workgroups take the units in turn; otherwise static splits, sized
   // so the launch's workgroups form whole rounds.
   const int64_t n_units = (int64_t)n_seq * n_layers;
+  // split partials per sequence and layer: at most 512 (k_combine stages a
+  // weight per partial), and n_seq of them within g2b_splits_per_layer_cap,
+  // the bound g2b_hbm_bytes budgets
+  const int32_t splits_per_seq =
+      (int32_t)std::min<uint64_t>(512, g2b_splits_per_layer_cap(n_seq) / (uint64_t)n_seq);
   const int64_t wq_slots = fast && dp.stage_mode != 0 ? slots_for(c, dp, true) : 0;
   const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
@@ -302,7 +311,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
       if (c->wq) G2B_HIP(c, hipFree(c->wq));
       c->wq = nullptr;
       c->wq_cap = 0;
-      const int32_t cap = (int32_t)std::max<int64_t>(wq_lines, 256);
+      const int32_t cap = (int32_t)std::max<int64_t>(wq_lines, G2B_WQ_MIN_LINES);
       const size_t bytes = (size_t)2 * cap * kWqStride * sizeof(int32_t);
       if (hipMalloc((void **)&c->wq, bytes) != hipSuccess) {
         c->wq = nullptr;
@@ -320,7 +329,8 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
       c->wq_reset = false;
     }
     max_splits = (int32_t)std::min<int64_t>(
-        std::max<int64_t>(kWqMinParts, (slots + n_units - 1) / n_units + 8), 2048);
+        std::max<int64_t>(kWqMinParts, (slots + n_units - 1) / n_units + 8),
+        std::min<int64_t>(2048, splits_per_seq));
     const int32_t R = dp.stage_rows;
     const int64_t streamed = (total_pos - n_seq) * (int64_t)n_layers;  // positions [0, pos)
     // (automatic: about kWqClaimsPerWave claims per wave of the grid; with
@@ -349,12 +359,17 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     // 1304 us per layer-serial step at 0.72 of a round against 1490 us at
     // 0.9, 1559 us at 1.13 and 1458 us at 1.5 rounds
     const int64_t split_slots = fast && dp.stage_rows == 0 ? slots * 7 / 10 : slots;
-    const int32_t split_len =
+    int32_t split_len =
         choose_split(c, std::max<int64_t>(split_slots, 1), total_pos, max_pos, n_layers, fast,
                      min_len);
     max_splits = (max_pos + 1 + split_len - 1) / split_len;
-    if (max_splits > 512)
-      return fail(c, G2B_EUNSUP, "context %d needs %d splits (> 512)", max_pos + 1, max_splits);
+    if (max_splits > splits_per_seq) {  // lengthen the splits to stay within the budget
+      split_len = (int32_t)(((int64_t)max_pos + splits_per_seq) / splits_per_seq);
+      max_splits = (max_pos + 1 + split_len - 1) / split_len;
+    }
+    if (!fast && split_len > kGenericMaxSplit)
+      return fail(c, G2B_EUNSUP, "context %d of %d sequences needs splits of %d positions "
+                  "(> %d on the generic kernel)", max_pos + 1, n_seq, split_len, kGenericMaxSplit);
     dp.split_len = split_len;
   }
   dp.max_splits = max_splits;
@@ -364,9 +379,12 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
 
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              (size_t)(kPartHead + hd);
-  if (int rc = grow(c, &c->part, &c->part_cap, part_floats)) return rc;
+  const size_t part_limit = (size_t)c->shape.n_layers * (size_t)g2b_splits_per_layer_cap(n_seq) *
+                            nh * (size_t)(kPartHead + hd);
+  if (int rc = grow(c, &c->part, &c->part_cap, part_floats, part_limit)) return rc;
   if (!fast) {
-    if (int rc = grow(c, &c->qrot, &c->qrot_cap, (size_t)n_layers * n_seq * nq)) return rc;
+    const size_t qf = (size_t)n_layers * n_seq * nq;
+    if (int rc = grow(c, &c->qrot, &c->qrot_cap, qf, qf)) return rc;
   }
   dp.part = c->part;
   dp.q_rot = c->qrot;
@@ -566,6 +584,18 @@ int g2b_kv_free(g2b_ctx *c, void *kc, void *vc) {
   return G2B_OK;
 }
 
+int g2b_kv_read(g2b_ctx *c, const void *cache, uint64_t offset, uint64_t nbytes, void *host) {
+  if (!c) return G2B_EINVAL;
+  if (!cache) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (!host && nbytes) return fail(c, G2B_EINVAL, "null host buffer");
+  if (nbytes == 0) return G2B_OK;
+  if (int rc = set_device(c)) return rc;
+  G2B_HIP(c, hipMemcpyAsync(host, (const uint8_t *)cache + offset, (size_t)nbytes,
+                            hipMemcpyDeviceToHost, c->stream));
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
 int g2b_kv_append_rows(g2b_ctx *c, void *kc, void *vc, int32_t ctx_cap, int32_t layer,
                        int32_t pos0, int32_t n_rows, const float *k, const float *v) {
   if (!c) return G2B_EINVAL;
@@ -655,7 +685,7 @@ int g2b_batch_begin(g2b_ctx *c, int32_t n_seq, const g2b_seq *seqs) {
     c->h_seqs = nullptr;
     c->seqs_cap = 0;
     c->seqs_ev_live = false;
-    const int32_t cap = std::max(n_seq, 64);
+    const int32_t cap = std::max<int32_t>(n_seq, (int32_t)G2B_SEQ_DESC_MIN);
     if (hipMalloc((void **)&c->d_seqs, cap * sizeof(SeqDev)) != hipSuccess ||
         hipHostMalloc((void **)&c->h_seqs, cap * sizeof(SeqDev), hipHostMallocDefault) !=
             hipSuccess) {
@@ -730,7 +760,8 @@ int g2b_attn_forward_host(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_ca
   const size_t nq = (size_t)c->shape.n_heads * c->shape.head_dim;
   const size_t nkv = (size_t)c->shape.n_kv_heads * c->shape.head_dim;
   const size_t natt = att ? (size_t)c->shape.n_heads * (size_t)ctx_cap : 0;
-  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nq + 2 * nkv + natt)) return rc;
+  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nq + 2 * nkv + natt, nq + 2 * nkv + natt))
+    return rc;
   float *dq = c->hstage, *dk = dq + nq, *dv = dk + nkv, *da = att ? dv + nkv : nullptr;
   G2B_HIP(c, hipMemcpyAsync(dq, q, nq * 4, hipMemcpyHostToDevice, c->stream));
   G2B_HIP(c, hipMemcpyAsync(dk, k, nkv * 4, hipMemcpyHostToDevice, c->stream));
@@ -791,7 +822,8 @@ int g2b_matmul_host(g2b_ctx *c, float *out, const float *x, const void *w, int32
   if (int rc = set_device(c)) return rc;
   if (!out || d <= 0) return g2b_matmul(c, nullptr, nullptr, nullptr, type, 0, 0);
   const size_t nx = (x && w && n > 0) ? (size_t)n : 0;
-  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nx + (size_t)d + 4)) return rc;
+  if (int rc = grow(c, &c->hstage, &c->hstage_cap, nx + (size_t)d + 4, nx + (size_t)d + 4))
+    return rc;
   float *dx = c->hstage, *dout = dx + ((nx + 3) & ~(size_t)3);
   if (nx) G2B_HIP(c, hipMemcpyAsync(dx, x, nx * 4, hipMemcpyHostToDevice, c->stream));
   if (int rc = g2b_matmul(c, dout, nx ? dx : nullptr, w, type, n, d)) return rc;

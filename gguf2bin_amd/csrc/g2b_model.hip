@@ -230,7 +230,9 @@ int g2b_model_load_g2bx(g2b_model **out, int32_t device, const char *path, int32
                        role == G2B_R_FFN_NORM || role == G2B_R_ATTN_Q_NORM ||
                        role == G2B_R_ATTN_K_NORM;
       const uint64_t need = vec ? (uint64_t)n * 4u : rows * row_stride_of(s->type, n);
-      return s->nbytes >= need;
+      // (the slot must also lie inside the blob: g2b_g2bx_open refuses
+      // offsets that wrap, and sizes the blob to the largest slot end)
+      return s->nbytes >= need && s->off <= g.data_size && s->nbytes <= g.data_size - s->off;
     };
     bool ok = fits(G2B_R_TOK_EMBD, -1, (uint64_t)c.vocab, c.dim) &&
               fits(G2B_R_OUTPUT, -1, (uint64_t)c.vocab, c.dim) &&

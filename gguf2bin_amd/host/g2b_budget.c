@@ -16,6 +16,7 @@
  * tokenizer and weights are not part of it.
  */
 #include "g2b_attn.h"
+#include "../csrc/g2b_limits.h"
 
 /* kv_q8_rowsize (l5_model.c:47) or nkv*4, for the given mode. */
 static uint64_t row_bytes_mode(const g2b_shape *s, int32_t kv_q8) {
@@ -38,21 +39,46 @@ int32_t g2b_clamp_ctx(int32_t ctx, int32_t seq_len) {
   return ctx;
 }
 
-/* Upper bound of the split partials a one-layer call allocates: partial
- * slots for max(2048, 64 * n_seq) splits, each (4 + head_dim) floats per q
- * head (running max, sum, two pad floats, accumulator). */
-static uint64_t scratch_bytes(const g2b_shape *s, int32_t n_seq) {
-  uint64_t splits = 64u * (uint64_t)n_seq;
-  if (splits < 2048u) splits = 2048u;
-  return splits * (uint64_t)s->n_heads * (4u + (uint64_t)s->head_dim) * 4u;
+static uint64_t grain(uint64_t b) {
+  return (b + G2B_ALLOC_GRAIN - 1u) / G2B_ALLOC_GRAIN * G2B_ALLOC_GRAIN;
+}
+
+/* The context's own buffers for n_seq sequences at context ctx, for any call
+ * form (one layer per call up to all layers in one call), each allocation
+ * rounded up to the allocation grain - what g2b_api.hip allocates:
+ *   RoPE table: grown by doubling, so at most max(2*ctx, 256) positions of
+ *     head_dim floats;
+ *   split partials: n_layers x g2b_splits_per_layer_cap(n_seq) splits x
+ *     n_heads x (4 + head_dim) floats (a call over fewer layers needs less);
+ *   rotated q of the generic path: n_layers x n_seq x nq floats;
+ *   work-queue counters: two sets of max(n_layers*n_seq + 1, 256) lines;
+ *   batch descriptors: max(n_seq, 64) of them;
+ *   QK-RMSNorm weights and flags: n_layers x (2*head_dim + 1) words;
+ *   the host entry point's staging: nq + 2*nkv + n_heads*ctx floats. */
+static uint64_t ctx_bytes(const g2b_shape *s, int32_t ctx, int32_t n_seq) {
+  const uint64_t L = (uint64_t)s->n_layers, nh = (uint64_t)s->n_heads;
+  const uint64_t hd = (uint64_t)s->head_dim, ns = (uint64_t)n_seq;
+  const uint64_t nq = nh * hd, nkv = (uint64_t)s->n_kv_heads * hd;
+  uint64_t rope_pos = 2u * (uint64_t)ctx;
+  if (rope_pos < 256u) rope_pos = 256u;
+  uint64_t wq_lines = L * ns + 1u;
+  if (wq_lines < G2B_WQ_MIN_LINES) wq_lines = G2B_WQ_MIN_LINES;
+  const uint64_t descs = ns > G2B_SEQ_DESC_MIN ? ns : G2B_SEQ_DESC_MIN;
+  return grain(rope_pos * hd * 4u) +
+         grain(L * g2b_splits_per_layer_cap(n_seq) * nh * (G2B_PART_HEAD + hd) * 4u) +
+         grain(L * ns * nq * 4u) +
+         grain(2u * wq_lines * G2B_WQ_LINE_BYTES) +
+         grain(descs * G2B_SEQ_DESC_BYTES) +
+         grain(L * 2u * hd * 4u) + grain(L * 4u) +
+         grain((nq + 2u * nkv + nh * (uint64_t)ctx) * 4u);
 }
 
 uint64_t g2b_hbm_bytes(const g2b_shape *s, int32_t ctx, int32_t kv_q8, int32_t n_seq) {
   if (!shape_ok(s) || ctx <= 0 || n_seq < 1) return 0;
-  const uint64_t kv = (uint64_t)n_seq * 2u * (uint64_t)s->n_layers * (uint64_t)ctx *
-                      row_bytes_mode(s, kv_q8);
-  const uint64_t rope = (uint64_t)ctx * (uint64_t)s->head_dim * 4u;
-  return kv + rope + scratch_bytes(s, n_seq);
+  /* alloc_rt's two caches per sequence, with their read slack */
+  const uint64_t cache = grain((uint64_t)s->n_layers * (uint64_t)ctx * row_bytes_mode(s, kv_q8) +
+                               G2B_KV_SLACK);
+  return (uint64_t)n_seq * 2u * cache + ctx_bytes(s, ctx, n_seq);
 }
 
 int g2b_auto_budget(const g2b_shape *s, int32_t seq_len, int32_t n_seq, uint64_t budget,

@@ -82,6 +82,12 @@ int g2b_g2bx_open(const char *path, g2b_g2bx *out) {
     sl->type = s[3];
     sl->nbytes = le32(s + 4);
     sl->off = le64(s + 8);
+    /* an offset whose end wraps would pass every later size check */
+    if (sl->off > UINT64_MAX - sl->nbytes) {
+      fclose(f);
+      g2b_g2bx_close(out);
+      return G2B_EINVAL;
+    }
     const uint64_t e = sl->off + sl->nbytes;
     if (e > max_end) max_end = e;
   }

@@ -100,12 +100,17 @@ uint64_t g2b_kv_offset(const g2b_shape *shape, int32_t ctx_cap, int32_t layer, i
  *   sequence at the full seq_len in the given mode (0 when seq_len <= 0).
  * g2b_clamp_ctx: model_set_ctx's clamp (l5_model.c:166-169): ctx <= 0 -> 256,
  *   then at most seq_len when seq_len > 0.
- * g2b_hbm_bytes: HBM that n_seq sequences of the shape at context ctx take on
- *   the device - their K and V caches, the RoPE table (ctx*head_dim floats)
- *   and an upper bound of the split partials of a one-layer call
- *   (max(2048, 64*n_seq) splits x n_heads x (4+head_dim) floats).  Takes the
- *   place of est_for (l5_model.c:174-187), whose host buffers and tokenizer
- *   are not in HBM.  0 for a bad shape, ctx <= 0 or n_seq < 1.
+ * g2b_hbm_bytes: an upper bound of the HBM that one context serving n_seq
+ *   sequences of the shape at context ctx allocates - their K and V caches
+ *   and the context's buffers for any call form, g2b_attn_layers over all
+ *   layers in one call included: the RoPE table (up to max(2*ctx, 256)
+ *   positions), the split partials (at most max(2048, 64*n_seq) splits per
+ *   layer of a call, n_heads x (4+head_dim) floats each), the generic path's
+ *   rotated q, the work-queue counters, the batch descriptors, the
+ *   QK-RMSNorm weights and the host entry point's staging, each allocation
+ *   rounded up to 2 MiB.  Takes the place of est_for (l5_model.c:174-187),
+ *   whose host buffers and tokenizer are not in HBM.  0 for a bad shape,
+ *   ctx <= 0 or n_seq < 1.
  * g2b_auto_budget: model_auto_budget (l5_model.c:218-230) against an HBM
  *   budget for n_seq sequences: starting from kv_q8 = shape->kv_q8 and
  *   ctx = seq_len (2048 when seq_len <= 0), switch to Q8_0 if F32 does not
@@ -131,6 +136,10 @@ int g2b_hbm_info(g2b_ctx *ctx, uint64_t *free_bytes, uint64_t *total_bytes);
 int g2b_kv_alloc(g2b_ctx *ctx, int32_t ctx_cap, void **kcache, void **vcache);
 /* free_rt's KV part (l5_model.c:117-118). */
 int g2b_kv_free(g2b_ctx *ctx, void *kcache, void *vcache);
+/* Copy nbytes of a device cache from byte offset `offset` into host memory
+ * and wait: what reading Model.kcache/kcq directly does on the host (e.g.
+ * kv_key_row, l5_model.c:248-265, or a tool comparing caches). */
+int g2b_kv_read(g2b_ctx *ctx, const void *cache, uint64_t offset, uint64_t nbytes, void *host);
 
 /* QK-RMSNorm of one layer: with F_QK_NORM set, model_forward runs
  * qk_rmsnorm (l3_math.c:107-114) on q with attn_q_norm and on the new k with

@@ -366,13 +366,16 @@ def ref_g2bx_info(path: str):
 
 
 def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
-                      ctx: int = 0, timed: bool = False):
+                      ctx: int = 0, timed: bool = False, variant: str = "avx2"):
     """The compiled reference's model_forward over tokens at positions
     0..n-1 of a G2BX file: logits [n][vocab]; with timed, (logits, seconds
-    of the token loop alone, without the load)."""
-    L = ref_lib("avx2")
+    of the token loop alone, without the load).  variant "gpu": the
+    reference with the drop-in patch of INTEGRATION.md section 1
+    (libg2bref_gpu.so), whose attention runs on the device (G2B_GPU is set
+    for the call)."""
+    L = ref_lib(variant)
     if L is None:
-        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+        raise RuntimeError(f"compiled reference '{variant}' not built (make -C oracle ref refgpu)")
     fn = L.ref_model_forward_g2bx
     fn.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
                    C.POINTER(C.c_double)]
@@ -380,8 +383,18 @@ def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
     tok = np.ascontiguousarray(tokens, np.int32)
     out = np.zeros((len(tok), vocab), np.float32)
     secs = C.c_double(0.0)
-    rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, tok.ctypes.data, len(tok), out.ctypes.data,
-            C.byref(secs))
+    old = os.environ.get("G2B_GPU")
+    if variant == "gpu":
+        os.environ["G2B_GPU"] = "1"
+    try:
+        rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, tok.ctypes.data, len(tok),
+                out.ctypes.data, C.byref(secs))
+    finally:
+        if variant == "gpu":
+            if old is None:
+                del os.environ["G2B_GPU"]
+            else:
+                os.environ["G2B_GPU"] = old
     if rc:
         raise RuntimeError(f"reference forward failed ({rc})")
     return (out, secs.value) if timed else out

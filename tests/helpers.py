@@ -296,3 +296,19 @@ def random_model_slots(rng, cfg: dict, flags: int, mat_type: int, emb_type: int,
         slots += [(r, L, mt(r), random_matrix_bytes(rng, mt(r), rows, n))
                   for r, rows, n in ((R_FFN_GATE, h, d), (R_FFN_UP, h, d), (R_FFN_DOWN, d, h))]
     return slots
+
+
+def require_ref(variant: str = "avx2"):
+    """The compiled reference (oracle/_ref, built from /root/reference by
+    build() in the build container and shipped with the tree).  Its absence
+    fails the test instead of skipping it: the model, budget, loader and
+    GEMV parity rest on it, and a run without it must not read as green."""
+    import pytest
+    from oracle import orc
+
+    L = orc.ref_lib(variant)
+    if L is None:
+        pytest.fail(f"compiled reference oracle/_ref/libg2bref_{variant}.so is missing: build it "
+                    "with `make -C oracle ref` (needs /root/reference) before running the "
+                    "parity tests", pytrace=False)
+    return L

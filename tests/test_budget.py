@@ -16,6 +16,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
+from helpers import require_ref
 from oracle import orc
 from gguf2bin_amd import attn
 
@@ -29,16 +30,9 @@ CFGS = [
 SEQ_LENS = [0, 1, 100, 256, 257, 300, 4096, 40000]
 
 
-def ref_or_skip():
-    L = orc.ref_lib("avx2")
-    if L is None:
-        pytest.skip("compiled reference not built (make -C oracle ref)")
-    return L
-
-
 @pytest.mark.parametrize("cfg", CFGS)
 def test_oracle_est_for_matches_reference(cfg):
-    L = ref_or_skip()
+    L = require_ref()
     dim, hid, nl, nh, nkvh, vocab, hd = cfg
     for ctx in (1, 255, 256, 2048, 40000):
         for q8 in (0, 1):
@@ -50,7 +44,7 @@ def test_oracle_est_for_matches_reference(cfg):
 def test_oracle_auto_budget_matches_reference(cfg):
     """Budgets around every threshold of the loop: below the floor, between
     halvings, just under / at / over the F32 and Q8_0 estimates."""
-    L = ref_or_skip()
+    L = require_ref()
     dim, hid, nl, nh, nkvh, vocab, hd = cfg
     for seq_len in SEQ_LENS:
         for q8 in (0, 1):
@@ -118,23 +112,38 @@ def test_auto_budget_follows_reference_loop(nl, nh, nkvh, hd, q8_in, n_seq):
                 assert est(start, 0) > budget
 
 
+def _grain(b, g=2 << 20):
+    return -(-b // g) * g
+
+
 def test_hbm_bytes_terms():
+    """The estimate's structure: whole allocation grains; two caches per
+    sequence (each its cache bytes and 256 bytes of read slack, rounded up);
+    the partials of a call over all layers at the per-layer cap of
+    max(2048, 64*n_seq) splits; monotone in n_seq and ctx.  That the runtime
+    stays within it is measured on the device (test_gpu_budget.py)."""
+    G = 2 << 20
     for (nl, nh, nkvh, hd) in [(2, 4, 2, 32), (28, 16, 8, 128), (30, 9, 3, 64)]:
         for q8 in (False, True):
             s = shape(nl, nh, nkvh, hd, q8)
             for ctx in (1, 300, 8193):
-                kv1 = 2 * attn.kv_bytes(s, ctx)  # K and V of one sequence
-                # linear in n_seq with slope = KV + scratch of 64 splits per
-                # sequence once 64*n_seq exceeds the 2048-split floor
-                a = attn.hbm_bytes(s, ctx, q8, 100)
-                b = attn.hbm_bytes(s, ctx, q8, 101)
-                assert b - a == kv1 + 64 * nh * (4 + hd) * 4
-                # below the floor only the KV grows
-                assert attn.hbm_bytes(s, ctx, q8, 2) - attn.hbm_bytes(s, ctx, q8, 1) == kv1
-                # one more position: one more K and V row per layer and sequence,
-                # one more RoPE row
-                d = attn.hbm_bytes(s, ctx + 1, q8, 3) - attn.hbm_bytes(s, ctx, q8, 3)
-                assert d == 3 * 2 * nl * attn.kv_row_bytes(s) + hd * 4
+                cache = _grain(attn.kv_bytes(s, ctx) + 256)
+                prev = 0
+                for n_seq in (1, 2, 31, 32, 33, 100, 101):
+                    b = attn.hbm_bytes(s, ctx, q8, n_seq)
+                    assert b % G == 0
+                    assert b > prev
+                    prev = b
+                    splits = max(2048, 64 * n_seq)
+                    parts = nl * splits * nh * (4 + hd) * 4
+                    assert b >= 2 * n_seq * cache + _grain(parts) + _grain(ctx * hd * 4)
+                    # the sequence-independent part does not depend on n_seq
+                    # below the split floor (n_seq <= 32), nor the caches'
+                    # share on anything but n_seq
+                    if n_seq <= 31:
+                        nxt = attn.hbm_bytes(s, ctx, q8, n_seq + 1)
+                        assert nxt - b >= 2 * cache
+                assert attn.hbm_bytes(s, ctx + 1, q8, 3) >= attn.hbm_bytes(s, ctx, q8, 3)
             assert attn.model_kv_bytes(s, 4096, q8) == 2 * attn.kv_bytes(s, 4096)
             assert attn.model_kv_bytes(s, 0, q8) == 0
 

@@ -14,17 +14,12 @@ import numpy as np
 import pytest
 
 from helpers import (F_QK_NORM, G2BX_CFG, R_ATTN_Q, R_FFN_DOWN, R_TOK_EMBD, random_model_slots,
-                     write_g2bx)
+                     require_ref, write_g2bx)
 from oracle import orc
 from gguf2bin_amd import attn
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 TINY = os.path.join(HERE, "golden", "tiny.g2bx")
-
-
-def ref_or_skip():
-    if orc.ref_lib("avx2") is None:
-        pytest.skip("compiled reference not built (make -C oracle ref)")
 
 
 def cfg40(cfg: dict) -> bytes:
@@ -36,7 +31,7 @@ def test_tiny_parse_matches_reference_loader():
     assert g["version"] == 1 and g["arch"] == attn.ARCH_QWEN3 and g["flags"] == 3
     assert g["cfg"]["dim"] == 64 and g["cfg"]["n_layers"] == 2 and g["cfg"]["head_dim"] == 16
     assert len(g["slots"]) == 24 and len(g["data"]) == 47616
-    ref_or_skip()
+    require_ref()
     c40, arch, flags, slots = orc.ref_g2bx_info(TINY)
     assert c40 == cfg40(g["cfg"])
     assert (arch, flags) == (g["arch"], g["flags"])
@@ -65,7 +60,7 @@ def test_random_file_parse_matches_reference_loader(tmp_path, seed):
     for (r, l, t, n, o), s in zip(g["slots"], slots):
         assert (r, l, t, n) == (s[0], s[1], s[2], len(s[3]))
         assert g["data"][o:o + n] == s[3]
-    ref_or_skip()
+    require_ref()
     c40, arch, flags, rslots = orc.ref_g2bx_info(p)
     assert c40 == cfg40(g["cfg"]) and rslots == g["slots"]
 
@@ -112,3 +107,19 @@ def test_rejects_bad_files(tmp_path):
         assert e.value.code == attn.G2B_EINVAL, name
     with pytest.raises(attn.G2BError):
         attn.g2bx_open(str(tmp_path / "missing.g2bx"))
+
+
+def test_rejects_wrapping_slot(tmp_path):
+    """A slot whose off + nbytes wraps past 2^64 would leave the blob small
+    and the slot pointing outside it; the parse refuses it (the reference
+    trusts the file)."""
+    good = bytearray(open(TINY, "rb").read())
+    # first slot entry at 52: role, layer(2), type, nbytes(4), off(8)
+    nbytes = struct.unpack_from("<I", good, 52 + 4)[0]
+    assert nbytes > 0
+    struct.pack_into("<Q", good, 52 + 8, (1 << 64) - nbytes // 2)
+    p = tmp_path / "wrap.g2bx"
+    p.write_bytes(bytes(good))
+    with pytest.raises(attn.G2BError) as e:
+        attn.g2bx_open(str(p))
+    assert e.value.code == attn.G2B_EINVAL

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from helpers import (F_QK_NORM, F_TIE_EMBD, R_ATTN_K, R_ATTN_O, R_ATTN_Q, R_FFN_DOWN,
-                     random_model_slots, write_g2bx)
+                     random_model_slots, require_ref, write_g2bx)
 from oracle import orc
 from gguf2bin_amd import attn
 
@@ -55,11 +55,6 @@ CASES = {
 }
 
 
-def ref_or_skip():
-    if orc.ref_lib("avx2") is None:
-        pytest.skip("compiled reference not built (make -C oracle ref)")
-
-
 def make(tmp_path, name, seed=0):
     cfg, arch, flags, mt, et, ot = CASES[name]
     rng = np.random.default_rng(seed + sum(map(ord, name)))
@@ -82,7 +77,7 @@ def check(dev, ref, what, kv_q8=False):
 @pytest.mark.parametrize("kv_q8", [False, True])
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_forward_matches_reference(gpu_device, tmp_path, name, kv_q8):
-    ref_or_skip()
+    require_ref()
     p, cfg, rng = make(tmp_path, name)
     toks = rng.integers(0, cfg["vocab"], 24)
     print(f"[model] {name} kv_q8={kv_q8}", flush=True)
@@ -95,7 +90,7 @@ def test_forward_matches_reference(gpu_device, tmp_path, name, kv_q8):
 
 def test_forward_long_context(gpu_device, tmp_path):
     """300 steps of one model: attention over many splits as pos grows."""
-    ref_or_skip()
+    require_ref()
     cfg = dict(dim=256, hidden_dim=384, n_layers=2, n_heads=4, n_kv_heads=2, vocab=256,
                seq_len=512, head_dim=64, eps=1e-6, rope_theta=1e6)
     rng = np.random.default_rng(77)
@@ -115,11 +110,13 @@ def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
     in turn with an eager model of the same file (its launches one by one,
     scheduled for the step's own position; the synchronisation that ends
     every forward between the replays), each replay must give the eager
-    step's logits bit for bit.  72 positions: the first bucket (one split,
-    the output written by k_layer) and the second (two splits and
-    k_combine)."""
+    step's logits bit for bit.  200 positions cover three buckets: 63 and
+    127, whose captured attention is k_short (as every eager step below 128
+    positions), and 255, whose captured attention is k_layer over two splits
+    and k_combine, replayed against eager steps at positions 128-199 (k_layer
+    with one or two splits: its own output, or k_combine)."""
     p, cfg, rng = make(tmp_path, "qwen3_hd128_q8", seed=5)
-    toks = [int(t) for t in rng.integers(0, cfg["vocab"], 72)]
+    toks = [int(t) for t in rng.integers(0, cfg["vocab"], 200)]
     with attn.Model(p, kv_q8=kv_q8) as g, attn.Model(p, kv_q8=kv_q8) as e:
         g.use_graph(True)
         e.use_graph(False)
@@ -148,7 +145,7 @@ def test_fused_launches_match_separate(gpu_device, tmp_path, name):
 
 def test_tiny_g2bx(gpu_device):
     """The reference's own tiny model (all-zero Q4_0 weights: logits 0)."""
-    ref_or_skip()
+    require_ref()
     ref = orc.ref_model_forward(TINY, [1, 5, 9], 128)
     with attn.Model(TINY) as m:
         assert m.arch == attn.ARCH_QWEN3 and m.flags == 3
@@ -189,3 +186,24 @@ def test_forward_errors(gpu_device, tmp_path):
     with pytest.raises(attn.G2BError) as e:
         attn.Model(t)
     assert e.value.code == attn.G2B_EINVAL
+
+
+@pytest.mark.parametrize("name", ["qwen3_q8_tied", "qwen3_hd128_q8", "llama_q4_f16emb"])
+@pytest.mark.parametrize("kv_q8", [False, True])
+def test_patched_reference_runs_device_attention(gpu_device, tmp_path, name, kv_q8):
+    """The reference's own model_forward with INTEGRATION.md section 1 applied
+    (oracle/refpatch.py; KV from g2b_kv_alloc in alloc_rt, the attention block
+    as g2b_attn_forward_host, QK-RMSNorm weights handed over at load) against
+    the unpatched reference on the same file: everything but the attention
+    is the reference's own code.  140 tokens reach the split kernel.  F32 KV:
+    within 2e-5 of the logit scale; Q8_0 KV: the appended rows are the same
+    bytes for the same k/v, but a last-bit difference of the attention output
+    reaches the next layer's k/v (the bar of test_forward_matches_reference)."""
+    require_ref()
+    require_ref("gpu")
+    p, cfg, rng = make(tmp_path, name, seed=13)
+    n = min(140, cfg["seq_len"])
+    toks = [int(t) for t in rng.integers(0, cfg["vocab"], n)]
+    ref = orc.ref_model_forward(p, toks, cfg["vocab"], kv_q8, 0)
+    dev = orc.ref_model_forward(p, toks, cfg["vocab"], kv_q8, 0, variant="gpu")
+    check(dev, ref, f"{name} patched reference", kv_q8)

@@ -11,6 +11,7 @@ without a GPU:
 import numpy as np
 import pytest
 
+from helpers import require_ref
 from oracle import orc
 from gguf2bin_amd import attn
 
@@ -19,15 +20,10 @@ TYPES = [orc.T_Q8_0, orc.T_Q4_0, orc.T_F32]
 SHAPES = [(32, 1), (64, 5), (100, 9), (576, 33), (1024, 64), (3072, 17)]
 
 
-def ref_or_skip(variant):
-    if orc.ref_lib(variant) is None:
-        pytest.skip("compiled reference not built (make -C oracle ref)")
-
-
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n,d", SHAPES)
 def test_scalar_restatement_bit_exact_with_reference(t, n, d):
-    ref_or_skip("scalar")
+    require_ref("scalar")
     rng = np.random.default_rng(n * 7 + d + t)
     w = orc.random_weights(rng, t, n, d)
     x = rng.standard_normal(n).astype(np.float32)
