@@ -601,7 +601,8 @@ def cpu_leg(w: Workload, na: int, nb: int, min_s: float):
     f64_gpu = f64_orc = 0.0
     for j, layer in ((0, 0), (len(idx) - 1, L - 1)):
         i = idx[j]
-        ex = exact_attention(o, caps[i], layer, poss[i], host[j][0], host[j][1], q_all[layer, i])
+        ex, _ = exact_attention(o, caps[i], layer, poss[i], host[j][0], host[j][1],
+                                q_all[layer, i])
         f64_gpu = max(f64_gpu, float(np.max(np.abs(out_gpu[layer, i] - ex))))
         f64_orc = max(f64_orc, float(np.max(np.abs(out_b[layer, j] - ex))))
     cpu_model = ""
