@@ -38,7 +38,7 @@ EXPORTS = [
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
-    "g2b_ctx_profile", "g2b_ctx_profile_read", "g2b_ctx_tune",
+    "g2b_ctx_profile", "g2b_ctx_profile_read", "g2b_ctx_tune", "g2b_ctx_tune_kernel",
 ]
 
 
@@ -164,6 +164,7 @@ def lib() -> C.CDLL:
             "g2b_synth_copy": ([vp, vp, vp, u64], C.c_int),
             "g2b_ctx_profile": ([vp, i32], C.c_int),
             "g2b_ctx_tune": ([vp, i32, i32, i32, i32], C.c_int),
+            "g2b_ctx_tune_kernel": ([vp, i32], C.c_int),
             "g2b_ctx_profile_read": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)],
                                      C.c_int),
         }
@@ -460,6 +461,10 @@ class Context:
         KV row path (-1 per-lane HBM loads, 1 / 2 staged through LDS), schedule
         (-1 static splits, > 0 work-queue piece length in positions)."""
         self._check(lib().g2b_ctx_tune(self.h, split_len, chunk, stage, piece), "g2b_ctx_tune")
+
+    def tune_kernel(self, kernel: int):
+        """0 automatic, 1 k_layer only, 2 k_tiles where it applies."""
+        self._check(lib().g2b_ctx_tune_kernel(self.h, kernel), "g2b_ctx_tune_kernel")
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

@@ -68,6 +68,8 @@ struct g2b_ctx {
   int32_t wq_dirty[2] = {0, 0};  // units of each set a launch may have left non-zero
   bool wq_reset = false;         // a launch failed after using the counters
   int32_t tune_stage = 0;      // -1: k_layer loads straight from HBM; 1, 2: staging mode
+  int32_t tune_kernel = 0;     // 0 automatic, 1 k_layer only, 2 k_tiles where it applies
+  int32_t occ_tiles[2] = {0, 0};  // k_tiles workgroups per CU (static, work queue)
 
   // decode-launch timing (g2b_ctx_profile)
   bool prof = false;
@@ -76,6 +78,7 @@ struct g2b_ctx {
 
   std::string err;
 };
+
 
 namespace {
 
@@ -192,6 +195,13 @@ int32_t slots_for(g2b_ctx *c, const DecodeParams &dp, bool wq) {
   return std::max(1, c->n_cu) * std::max(1, occ);
 }
 
+// Resident k_tiles workgroups on the device (cached).
+int32_t tiles_slots(g2b_ctx *c, bool wq) {
+  int32_t &occ = c->occ_tiles[wq ? 1 : 0];
+  if (occ <= 0) occ = tiles_blocks_per_cu(c->sh, wq);
+  return std::max(1, c->n_cu) * std::max(1, occ);
+}
+
 // min_len: the shortest split worth a workgroup (its waves get a few
 // wave-steps or chunks each; shorter splits cost more in setup and partials
 // than they gain in parallelism).
@@ -288,6 +298,16 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     return G2B_OK;
   }
 
+  // k_tiles (K scores on the matrix cores) for Q8_0 KV with wide GQA groups,
+  // no weights output; it stages tiles of kTilesRows positions per
+  // workgroup, so pieces and splits are multiples of that.
+  const bool tiles = fast && !att && c->tune_kernel != 1 && c->tune_chunk == 0 &&
+                     (c->tune_stage == 0 || c->tune_stage == 2) && tiles_available(c->sh);
+  if (tiles) {
+    dp.stage_mode = 2;
+    dp.stage_rows = kTilesRows;
+  }
+
   // Work queue (staged streaming) when few enough waves share each unit's
   // counters - with more units (sequence, layer) than resident workgroups,
   // the workgroups take the units in turn; otherwise static splits, sized
@@ -298,11 +318,13 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // the bound g2b_hbm_bytes budgets
   const int32_t splits_per_seq =
       (int32_t)std::min<uint64_t>(512, g2b_splits_per_layer_cap(n_seq) / (uint64_t)n_seq);
-  const int64_t wq_slots = fast && dp.stage_mode != 0 ? slots_for(c, dp, true) : 0;
+  const int64_t wq_slots = tiles                        ? tiles_slots(c, true)
+                           : fast && dp.stage_mode != 0 ? slots_for(c, dp, true)
+                                                         : 0;
   const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
                        wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
-  const int64_t slots = use_wq ? wq_slots : slots_for(c, dp, false);
+  const int64_t slots = use_wq ? wq_slots : tiles ? tiles_slots(c, false) : slots_for(c, dp, false);
   int32_t max_splits;
   if (use_wq) {
     const int64_t wq_lines = n_units + 1;  // the units and the next-unit counter
@@ -352,6 +374,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   } else {
     // (measured: four staged chunks or eight per-lane wave-steps per wave)
     const int32_t min_len = !fast                ? 64
+                            : tiles             ? 8 * kTilesRows
                             : dp.stage_rows > 0 ? kWavesPerSplit * 4 * dp.stage_rows
                                                 : kWavesPerSplit * 8 * decode_ppw(c->sh, dp.tune_chunk);
     // Per-lane loads (stage_rows == 0): splits sized for ~0.7 of the resident
@@ -409,7 +432,12 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   hipEvent_t ev1 = nullptr;
   if (int rc = prof_begin(c, &ev1)) return rc;
   if (use_wq) c->wq_reset = true;  // until both launches below are queued
-  G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
+  if (tiles) {
+    used_fast = 1;
+    G2B_HIP(c, launch_tiles(dp, n_layers, c->stream));
+  } else {
+    G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
+  }
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
   if (!direct || !used_fast) G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {
@@ -923,6 +951,12 @@ int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t chunk, int32_t stage, in
   c->tune_chunk = chunk;
   c->tune_stage = stage;
   c->tune_piece = piece;
+  return G2B_OK;
+}
+
+int g2b_ctx_tune_kernel(g2b_ctx *c, int32_t kernel) {
+  if (!c || kernel < 0 || kernel > 2) return G2B_EINVAL;
+  c->tune_kernel = kernel;
   return G2B_OK;
 }
 

@@ -177,6 +177,15 @@ bool decode_fast_available(const ShapeDev &sh);
 constexpr int kShortMaxPos = 128;
 bool short_available(const ShapeDev &sh);
 hipError_t launch_short(const DecodeParams &p, int n_layers, hipStream_t s);
+// Q8_0 KV with head_dim 128, 8 KV heads and 3 or 4 q heads per KV head, no
+// weights output: k_tiles (g2b_tiles.h) does RoPE, append and attention with
+// the K scores on the int8 matrix cores, in tiles of kTilesRows positions
+// staged per workgroup; schedules (static splits, work queue) and partials
+// as k_layer's.
+constexpr int kTilesRows = 16;
+bool tiles_available(const ShapeDev &sh);
+hipError_t launch_tiles(const DecodeParams &p, int n_layers, hipStream_t s);
+int tiles_blocks_per_cu(const ShapeDev &sh, bool wq);
 // Resident 256-thread decode workgroups per CU for this shape and the
 // k_layer variant DecodeParams' tune_chunk / stage_mode / stage_rows / wq
 // select (occupancy).

@@ -1,0 +1,480 @@
+// g2b_tiles.h - k_tiles, the decode kernel for Q8_0 KV with wide GQA groups,
+// whose K scores run on the int8 matrix cores.
+//
+// Replaces the score / softmax / V-accumulate loops of
+// /root/reference/src/l5_model.c:518-557 for Q8_0 KV caches with head_dim
+// 128, 8 KV heads and 3 or 4 q heads per KV head (Llama-3-8B's shape).  With
+// that many q heads per KV head, k_layer's per-lane integer dot products
+// (three v_dot4 chains per head and 4 bytes) make the loop bound by VALU
+// issue; here one v_mfma_i32_16x16x32_i8 computes, for one 32-element block
+// of one KV head and 16 positions, all G x 3 digit-plane dot products:
+//   A (16 x 32 int8): row 4h + p = digit plane p of q head h of the group
+//                     (plane 3 and heads >= G are zero rows),
+//   B (32 x 16 int8): the block's 32 quants of 16 positions (the cache bytes
+//                     as they are),
+//   C (16 x 16 int32): exact sums; lane (h = lane/16, t = lane%16) holds the
+//                     three planes of head h at position t.
+// q is held as three signed int8 digits of a 23-bit fixed point relative to
+// each (head, block)'s largest |q| (the digit planes k_layer uses), so the
+// block's score is (d2*65536 + d1*256 + d0)-weighted sums, exact in int32,
+// then one fp32 rounding and the block's fp16 scale; blocks are summed in
+// fp32.  Softmax stays in that layout (each lane one (head, position); the
+// running maximum of a head is shared by its 16 lanes through DPP), and V is
+// accumulated on the VALU: lane (KV head of the wave's pair, four dims) takes
+// p * v_scale for its block from a per-wave LDS exchange and does 4 x G FMAs
+// per position.
+//
+// Streaming: a workgroup stages tiles of 16 positions - the K and V rows of
+// 16 consecutive positions are two contiguous runs of 16 x row bytes - with
+// coalesced non-temporal 16-byte loads, the next tile's loads in registers
+// while the current tile is consumed from LDS.  Each wave owns two KV heads
+// of every tile, so the waves of a workgroup never merge states: each writes
+// the partials (or, with one split, the output) of its own heads.
+//
+// Schedules are k_layer's: static splits (workgroup = split x sequence x
+// layer) or the work queue (pieces of a unit claimed per workgroup).  The
+// setup (QK-RMSNorm, RoPE, digit planes, the owner's append) is k_layer's
+// visit_setup; the owner consumes its new row from LDS.
+#pragma once
+#include "g2b_layer.h"
+
+namespace g2b {
+
+constexpr int kTileRows = kTilesRows;  // positions per tile (the MFMA's 16 columns)
+constexpr int kTilesKvPerWave = 2;
+constexpr int kTilesHd = 128;
+
+// Shapes k_tiles serves.
+__host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
+  if (!sh.kv_q8 || sh.head_dim != kTilesHd) return false;
+  if (sh.n_kv_heads != kWavesPerSplit * kTilesKvPerWave) return false;
+  if (sh.n_heads % sh.n_kv_heads) return false;
+  const int g = sh.n_heads / sh.n_kv_heads;
+  return g >= 3 && g <= 4;
+}
+
+// k_tiles' dynamic LDS: [0, ra) is the setup's scratch (rotated q, new k and
+// v, the transposed copy for the QK-RMSNorm sums, then the digit planes) and,
+// once every wave holds its q operands, the staged tile (K rows, then V
+// rows); then the new K and V rows, the setup's norm factors and inputs, and
+// each wave's exchange of p * v_scale ([kv][block][position][head]) and
+// rescale factors ([kv][head]).
+struct TilesLds {
+  uint32_t ra, row_pad, scr, px, total;
+};
+__host__ __device__ inline uint32_t tiles_px_floats() {
+  return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTileRows * 4 + kTilesKvPerWave * 4);
+}
+__host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
+  const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
+  const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
+  const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u) +
+                       (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
+  const uint32_t tile = 2u * (uint32_t)kTileRows * sh.row_bytes;
+  TilesLds l;
+  l.ra = ((pre > tile ? pre : tile) + 15u) & ~15u;
+  l.row_pad = (sh.row_bytes + 15u) & ~15u;
+  l.scr = l.ra + 2u * l.row_pad;
+  const uint32_t scr_floats =
+      (uint32_t)(((sh.n_heads + sh.n_kv_heads + 3) & ~3) + 3 * sh.head_dim);
+  l.px = (l.scr + scr_floats * 4u + 15u) & ~15u;
+  l.total = l.px + (uint32_t)kWavesPerSplit * tiles_px_floats() * 4u;
+  return l;
+}
+
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+  static_assert(N == 16, "rows of 16 lanes");
+  x = fmaxf(x, dpp_f<0xB1>(x));   // lane ^ 1
+  x = fmaxf(x, dpp_f<0x4E>(x));   // lane ^ 2
+  x = fmaxf(x, dpp_f<0x141>(x));  // other quad of 8
+  x = fmaxf(x, dpp_f<0x140>(x));  // other half of 16
+  return x;
+}
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Staged tile loads per thread and tensor (a tile of 16 rows of up to 1088
+// bytes is at most 1088 16-byte pieces over 256 threads).
+constexpr int kTileLoads = 5;
+
+// G: q heads per KV head (3 or 4).  WQ: work-queue schedule.
+template <int G, bool WQ>
+__global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
+  constexpr int HD = kTilesHd, NB = HD / 32, KPW = kTilesKvPerWave, TP = kTileRows;
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ int32_t s_bcast, s_piece;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int n_heads = P.sh.n_heads;
+  const int nkv = P.sh.n_kv_heads * HD;
+  const size_t nq = (size_t)n_heads * HD;
+  const uint32_t row = P.sh.row_bytes;
+  const TilesLds ll = tiles_lds_layout(P.sh);
+  float *qrot = reinterpret_cast<float *>(lds);
+  float *kr = reinterpret_cast<float *>(lds + nq * 4);
+  float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
+  float *trq = reinterpret_cast<float *>(lds + nq * 4 + 2 * ((nkv * 4 + 15) & ~15u));
+  uint8_t *tk = lds, *tv = lds + (size_t)TP * row;  // the staged tile
+  uint8_t *rowk = lds + ll.ra, *rowv = rowk + ll.row_pad;
+  float *scr = reinterpret_cast<float *>(lds + ll.scr);
+  float *px = reinterpret_cast<float *>(lds + ll.px) + (size_t)wave * tiles_px_floats();
+  float *pfac = px + KPW * NB * TP * 4;  // [kv][head] rescale factors
+
+  // lane roles: MFMA row / column (A row, B and C column = position) and
+  // quarter (A/B k-quarter, C row group = q head of the group)
+  const int col = lane & 15, quarter = lane >> 4;
+  // V: KV head of the wave's pair, four dims 4*vd .. 4*vd+3 (block vd / 8)
+  const int vkv = lane >> 5, vd = lane & 31, vblk = vd >> 3;
+
+  auto visit = [&](const SeqDev &sd, int seq, int li, int t0, int tend, bool owns_new,
+                   int pslot, int32_t *ctr) {
+    const int layer = P.layer0 + li;
+    const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+    const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+    const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
+    u32x4 rk[kTileLoads], rv[kTileLoads];
+    // loads of the tile of n rows at ts: thread tid takes pieces tid,
+    // tid + 256, ... of the K run and of the V run
+    auto issue = [&](int ts, int n) {
+      const uint32_t np = (uint32_t)n * row / 16u;
+      const uint8_t *gk = kb + (size_t)ts * row + 16u * (uint32_t)tid;
+      const uint8_t *gv = vb + (size_t)ts * row + 16u * (uint32_t)tid;
+#pragma unroll
+      for (int i = 0; i < kTileLoads; i++) {
+        if ((uint32_t)(kThreads * i + tid) < np) {
+          rk[i] = __builtin_nontemporal_load(
+              (const __attribute__((address_space(1))) u32x4 *)(gk + 16u * kThreads * i));
+          rv[i] = __builtin_nontemporal_load(
+              (const __attribute__((address_space(1))) u32x4 *)(gv + 16u * kThreads * i));
+        }
+      }
+    };
+    auto stash = [&](int n) {
+      const uint32_t np = (uint32_t)n * row / 16u;
+#pragma unroll
+      for (int i = 0; i < kTileLoads; i++) {
+        const uint32_t pc = (uint32_t)(kThreads * i + tid);
+        if (pc < np) {
+          *reinterpret_cast<u32x4 *>(tk + 16u * pc) = rk[i];
+          *reinterpret_cast<u32x4 *>(tv + 16u * pc) = rv[i];
+        }
+      }
+    };
+    // Static schedule: the first tile is in flight during the setup.
+    if (!WQ && t0 < tend) issue(t0, min(TP, tend - t0));
+
+    // [QK-RMSNorm,] RoPE, the digit planes of q (32-element chunks = the
+    // Q8_0 blocks) and the owner's append, all in LDS
+    visit_setup<HD, 32, true>(P.sh, sd, layer, owns_new, P.q_in + sidx * nq, P.k_in + sidx * nkv,
+                              P.v_in + sidx * nkv, P.rope, P.norm, P.qscale, qrot, kr, vr, rowk,
+                              rowv, scr, trq);
+    // A operands: digit plane (col & 3) of head (col >> 2), bytes
+    // 8*quarter .. of block b; and the C lanes' units 2^(e-22) of
+    // (head quarter, block b)
+    uint64_t qa[KPW][NB];
+    float un[KPW][NB];
+    {
+      const uint32_t *dig = reinterpret_cast<const uint32_t *>(trq);
+      constexpr int DS = dig_stride<32>();
+      const int ah = col >> 2, ap = col & 3;
+#pragma unroll
+      for (int kk = 0; kk < KPW; kk++) {
+        const int kvg = wave * KPW + kk;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          uint64_t a = 0;
+          if (ah < G && ap < 3) {
+            const uint32_t *o = dig + ((kvg * G + ah) * NB + b) * DS + ap * 8 + 2 * quarter;
+            a = (uint64_t)o[0] | ((uint64_t)o[1] << 32);
+          }
+          qa[kk][b] = a;
+          un[kk][b] = quarter < G
+                          ? __uint_as_float(dig[((kvg * G + quarter) * NB + b) * DS + 24])
+                          : 0.f;
+        }
+      }
+    }
+
+    float m[KPW], l[KPW], acc[G][4];
+#pragma unroll
+    for (int kk = 0; kk < KPW; kk++) {
+      m[kk] = kNegBig;
+      l[kk] = 0.f;
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[h][j] = 0.f;
+
+    // V lane addressing inside a row: dims 4*vd.. of head (wave*KPW + vkv)
+    const uint32_t voff = 34u * (uint32_t)((wave * KPW + vkv) * NB + vblk) + 2u + 4u * (vd & 7);
+    const uint32_t vsel = (voff & 2u) ? 0x05040302u : 0x03020100u;
+    const uint32_t valn = voff & ~3u;
+
+    // One tile: rows [0, nrows) at K / V (row stride `row`), positions
+    // tpos0.. (rows past nrows read row 0 and are masked).
+    auto consume = [&](const uint8_t *K, const uint8_t *V, int nrows) {
+      const int rr = col < nrows ? col : 0;
+      const uint8_t *krow = K + (size_t)rr * row;
+      const uint8_t *vrow = V + (size_t)rr * row;
+      const bool valid = col < nrows && quarter < G;
+      float s[KPW];
+#pragma unroll
+      for (int kk = 0; kk < KPW; kk++) {
+        const int kvg = wave * KPW + kk;
+        float sc = 0.f;
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const uint32_t blk = (uint32_t)(kvg * NB + b);
+          const uint32_t off = 34u * blk + 2u + 8u * (uint32_t)quarter;
+          const uint32_t *w = reinterpret_cast<const uint32_t *>(krow + (off & ~3u));
+          const uint32_t sel = (off & 2u) ? 0x05040302u : 0x03020100u;
+          const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+          const uint64_t bop = (uint64_t)__builtin_amdgcn_perm(w1, w0, sel) |
+                               ((uint64_t)__builtin_amdgcn_perm(w2, w1, sel) << 32);
+          const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              (long)qa[kk][b], (long)bop, i32x4{0, 0, 0, 0}, 0, 0, 0);
+          const uint32_t sw = *reinterpret_cast<const uint32_t *>(krow + ((34u * blk) & ~3u));
+          const float ks = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
+          // |c2| <= 32*128*127, so c2*256 + c1 fits in int32
+          const float part = fmaf((float)(c[2] * 256 + c[1]), 256.f, (float)c[0]);
+          sc = fmaf(part, ks * un[kk][b], sc);
+        }
+        s[kk] = valid ? sc : -INFINITY;
+      }
+      // online softmax per (KV head, q head): the 16 lanes of a head share
+      // its reference m (raised lazily, as k_layer does)
+      bool need = false;
+      float mt[KPW];
+#pragma unroll
+      for (int kk = 0; kk < KPW; kk++) {
+        const float mx = group_max<16>(s[kk]);
+        mt[kk] = fmaxf(m[kk], mx);
+        need |= mx > m[kk] + kRescaleSlack;
+      }
+      const bool rescale = __any(need);
+      if (rescale) {
+#pragma unroll
+        for (int kk = 0; kk < KPW; kk++) {
+          const float a = fast_exp2(m[kk] - mt[kk]);
+          l[kk] *= a;
+          m[kk] = mt[kk];
+          if (col == 0) pfac[kk * 4 + quarter] = a;
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < KPW; kk++) {
+        const int kvg = wave * KPW + kk;
+        const float p = fast_exp2(s[kk] - m[kk]);  // 0 for masked lanes
+        l[kk] += p;
+        // p * (the V row's block scale) for each block of the KV head
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+          const uint32_t blk = (uint32_t)(kvg * NB + b);
+          const uint32_t sw = *reinterpret_cast<const uint32_t *>(vrow + ((34u * blk) & ~3u));
+          const float vs = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
+          px[((kk * NB + b) * TP + col) * 4 + quarter] = p * vs;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (rescale) {
+        const float4 f = *reinterpret_cast<const float4 *>(pfac + vkv * 4);
+        const float fa[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) acc[h][j] *= fa[h];
+      }
+      const float *pv = px + (vkv * NB + vblk) * TP * 4;
+      auto vstep = [&](int t) {
+        const float4 p4 = *reinterpret_cast<const float4 *>(pv + t * 4);
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(V + (size_t)t * row + valn);
+        const uint32_t x = __builtin_amdgcn_perm(w[1], w[0], vsel);
+        const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float v = i8f(x, j);
+#pragma unroll
+          for (int h = 0; h < G; h++) acc[h][j] = fmaf(pw[h], v, acc[h][j]);
+        }
+      };
+      if (nrows == TP) {
+#pragma unroll
+        for (int t = 0; t < TP; t++) vstep(t);
+      } else {
+        for (int t = 0; t < nrows; t++) vstep(t);
+      }
+      // (px is written again only after these reads: the next tile's K
+      // phase follows a workgroup barrier)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    if constexpr (!WQ) {
+      for (int ts = t0; ts < tend;) {
+        const int n = min(TP, tend - ts);
+        __syncthreads();  // the previous tile (or the setup's scratch) is no longer read
+        stash(n);
+        __syncthreads();
+        const int ns = ts + TP;
+        if (ns < tend) issue(ns, min(TP, tend - ns));
+        consume(tk, tv, n);
+        ts = ns;
+      }
+    } else {
+      // Pieces of [0, tend) claimed per workgroup from ctr[0]; thread 0
+      // keeps one claim in flight and publishes it at the piece switch.
+      // (the first claim travels in s_bcast, which the unit loop does not
+      // touch during a visit, so thread 0 may write s_piece in the first
+      // trip while others still read it)
+      const PieceMap pm = piece_map(tend, P.piece_big, P.piece_len);
+      int32_t pn = 0;
+      if (tid == 0) {
+        s_bcast = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      int pc = __builtin_amdgcn_readfirstlane(s_bcast);
+      int ts = 0, pe = 0;
+      if (pc < pm.npieces) {
+        piece_range(pm, pc, tend, ts, pe);
+        issue(ts, min(TP, pe - ts));
+      }
+      while (pc < pm.npieces) {
+        const int n = min(TP, pe - ts);
+        const bool last = ts + TP >= pe;  // last tile of the piece
+        if (last && tid == 0) {
+          s_piece = pn;
+          pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();  // the previous tile is no longer read; s_piece is published
+        stash(n);
+        int ns = ts + TP, npe = pe, npc = pc;
+        if (last) {
+          npc = s_piece;
+          if (npc < pm.npieces) piece_range(pm, npc, tend, ns, npe);
+        }
+        __syncthreads();
+        if (npc < pm.npieces) issue(ns, min(TP, npe - ns));
+        consume(tk, tv, n);
+        pc = npc;
+        ts = ns;
+        pe = npe;
+      }
+    }
+    if (owns_new) consume(rowk, rowv, 1);
+
+    // The partials (or the output) of the wave's heads: the sums of each
+    // head's 16 lanes; m is already shared by them.
+    float lsum[KPW];
+#pragma unroll
+    for (int kk = 0; kk < KPW; kk++) lsum[kk] = group_sum<16>(l[kk]);
+    constexpr int pstr = kPartHead + HD;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      // this V lane's head: (wave*KPW + vkv)*G + h; its m and l sit in the
+      // lanes of row group h
+      // (readlane moves the bits as an int)
+      const int m0 = __builtin_amdgcn_readlane(__float_as_int(m[0]), 16 * h);
+      const int m1 = __builtin_amdgcn_readlane(__float_as_int(m[1]), 16 * h);
+      const int l0 = __builtin_amdgcn_readlane(__float_as_int(lsum[0]), 16 * h);
+      const int l1 = __builtin_amdgcn_readlane(__float_as_int(lsum[1]), 16 * h);
+      const float mh = __int_as_float(vkv ? m1 : m0);
+      const float lh = __int_as_float(vkv ? l1 : l0);
+      const int head = (wave * KPW + vkv) * G + h;
+      if (!WQ && P.direct_out) {
+        float *out = P.q_out + sidx * nq + (size_t)head * HD + 4 * vd;
+        const double L = (double)lh;
+        *reinterpret_cast<float4 *>(out) =
+            make_float4((float)((double)acc[h][0] / L), (float)((double)acc[h][1] / L),
+                        (float)((double)acc[h][2] / L), (float)((double)acc[h][3] / L));
+      } else {
+        float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)head) * (size_t)P.max_splits +
+                              (size_t)pslot) * pstr;
+        *reinterpret_cast<float4 *>(pp + kPartHead + 4 * vd) =
+            make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        if (vd == 0) {
+          pp[0] = mh;
+          pp[1] = lh;
+        }
+      }
+    }
+    __syncthreads();  // LDS is free for the next visit
+  };
+
+  if constexpr (!WQ) {
+    const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+    const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+    const int npos = sd.pos + 1;
+    const int t0 = split * P.split_len;
+    if (t0 >= npos) return;
+    const int t1 = min(npos, t0 + P.split_len);
+    const bool owns_new = t1 == npos;
+    visit(sd, seq, li, t0, owns_new ? t1 - 1 : t1, owns_new, split, nullptr);
+  } else {
+    const int n_units = P.n_seq * P.n_layers_call;
+    int32_t *const wq = P.wq + (size_t)P.wq_set * (size_t)P.wq_cap * kWqStride;
+    int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)n_units));
+    uint32_t probe = blockIdx.x * 2654435761u;
+    int32_t *const fresh = wq + (size_t)n_units * kWqStride;
+    bool fresh_left = (int)gridDim.x < n_units;
+    for (;;) {
+      int32_t *ctr = wq + (size_t)unit * kWqStride;
+      if (tid == 0)
+        s_bcast = __hip_atomic_fetch_add(ctr + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      const int pslot = __builtin_amdgcn_readfirstlane(s_bcast);
+      __syncthreads();
+      if (pslot < P.max_splits) {
+        const int seq = unit % P.n_seq, li = unit / P.n_seq;
+        const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+        visit(sd, seq, li, 0, sd.pos, pslot == 0, pslot, ctr);
+      }
+      if (fresh_left) {
+        if (tid == 0)
+          s_bcast = (int)gridDim.x +
+                    __hip_atomic_fetch_add(fresh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const int nu = __builtin_amdgcn_readfirstlane(s_bcast);
+        __syncthreads();
+        if (nu < n_units) {
+          unit = nu;
+          continue;
+        }
+        fresh_left = false;
+      }
+      if (wave == 0) {
+        int found = -1;
+        probe = probe * 1664525u + 1013904223u;
+        const int start = (int)(probe % (uint32_t)n_units);
+        for (int b = 0; b < n_units && found < 0; b += 64) {
+          const int v = b + lane;
+          bool ok = false;
+          if (v < n_units) {
+            const int uu = (start + v) % n_units;
+            const int32_t *cu = wq + (size_t)uu * kWqStride;
+            const int pos2 = P.seqs ? P.seqs[uu % P.n_seq].pos : P.one.pos;
+            const int np2 = piece_map(pos2, P.piece_big, P.piece_len).npieces;
+            const int32_t nx = __hip_atomic_load(cu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int32_t ns = __hip_atomic_load(cu + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = nx + kWqStealMin <= np2 && ns < P.max_splits;
+          }
+          const uint64_t mask = __ballot(ok);
+          if (mask) found = (start + b + (int)__builtin_ctzll(mask)) % n_units;
+        }
+        if (lane == 0) s_bcast = found;
+      }
+      __syncthreads();
+      unit = __builtin_amdgcn_readfirstlane(s_bcast);
+      __syncthreads();
+      if (unit < 0) break;
+    }
+  }
+}
+
+}  // namespace g2b

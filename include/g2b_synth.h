@@ -57,6 +57,12 @@ int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
  * workgroup per KV head) unless split_len > 0 or piece != 0 is set. */
 int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t chunk, int32_t stage, int32_t piece);
 
+/* Decode kernel choice: 0 automatic (k_tiles - K scores on the int8 matrix
+ * cores - for Q8_0 KV with head_dim 128, 8 KV heads and 3-4 q heads per KV
+ * head when neither the weights output, a chunk nor a stage other than 2 is
+ * asked for; else k_layer), 1 k_layer only, 2 as 0. */
+int g2b_ctx_tune_kernel(g2b_ctx *ctx, int32_t kernel);
+
 /* Kernel timing with HIP events on the context's stream: while enabled,
  * every decode-kernel launch is bracketed by two events.  _read waits for
  * them, returns the summed milliseconds and the number of launches since
