@@ -36,6 +36,7 @@ EXPORTS = [
     "g2b_model_load_g2bx", "g2b_model_free", "g2b_model_info", "g2b_model_ctx",
     "g2b_model_forward", "g2b_model_use_graph", "g2b_model_set_fused",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
+    "g2b_attn_forward_noalloc",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
     "g2b_ctx_profile", "g2b_ctx_profile_read", "g2b_ctx_tune", "g2b_ctx_tune_kernel",
@@ -155,6 +156,7 @@ def lib() -> C.CDLL:
             "g2b_attn_layers": ([vp, i32, i32, fp, fp, fp, fp, i32], C.c_int),
             "g2b_attn_forward": ([vp, i32, i32, i32, vp, vp, fp, fp, fp, fp], C.c_int),
             "g2b_attn_forward_host": ([vp, i32, i32, i32, vp, vp, fp, fp, fp, fp], C.c_int),
+            "g2b_attn_forward_noalloc": ([vp, i32, i32, i32, vp, vp, fp, fp, fp], C.c_int),
             "g2b_rope_table": ([i32, i32, i32, C.c_float, fp], C.c_int),
             "g2b_sync": ([vp], C.c_int),
             "g2b_stream_seed": ([u64, i32, i32, i32], u64),
@@ -434,6 +436,12 @@ class Context:
                      k: int, v: int, att: Optional[int] = None):
         self._check(lib().g2b_attn_forward(self.h, layer, pos, ctx_cap, kc, vc, q, k, v, att),
                     "g2b_attn_forward")
+
+    def attn_forward_noalloc(self, layer: int, pos: int, ctx_cap: int, kc: int, vc: int, q: int,
+                             k: int, v: int):
+        """g2b_attn_forward over the library's fixed scratch (allocates nothing)."""
+        self._check(lib().g2b_attn_forward_noalloc(self.h, layer, pos, ctx_cap, kc, vc, q, k, v),
+                    "g2b_attn_forward_noalloc")
 
     def attn_forward_host(self, layer: int, pos: int, ctx_cap: int, kc: int, vc: int,
                           q: np.ndarray, k: np.ndarray, v: np.ndarray, want_att: bool = False):

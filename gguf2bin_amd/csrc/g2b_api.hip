@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <string>
+#include <mutex>
 #include <vector>
 
 #include "g2b_attn.h"
@@ -76,9 +77,22 @@ struct g2b_ctx {
   std::vector<hipEvent_t> prof_ev;  // pairs: [2i] before, [2i+1] after launch i
   size_t prof_used = 0;             // events used in the current window
 
+  float *fixed = nullptr;  // this device's copy of `scratch` (g2b_attn_forward_noalloc)
+
   std::string err;
 };
 
+// Scratch of the allocation-free entry point g2b_attn_forward_noalloc: the
+// split partials (and the generic path's rotated q) of its calls, in
+// file-scope device memory instead of buffers the context allocates.  Each
+// GPU the library runs on holds its own copy until the process ends; calls on
+// one GPU share it (each call overwrites what it uses and reads nothing it did
+// not write), so calls that overlap on one GPU race.  Host code never names
+// the array itself (that is a host-side stand-in): it uses the address
+// hipGetSymbolAddress gives per device, taken once per device at context
+// creation.
+constexpr size_t kFixedScratchBytes = (size_t)2 << 20;
+static __device__ __align__(256) float scratch[kFixedScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -116,6 +130,23 @@ bool misaligned(const void *p) { return ((uintptr_t)p & 15u) != 0; }
 int set_device(g2b_ctx *c) {
   G2B_HIP(c, hipSetDevice(c->device));
   return G2B_OK;
+}
+
+// This device's address of `scratch`, looked up once per device (the device
+// must be current).
+std::mutex g_fixed_mu;
+std::vector<float *> g_fixed_ptr;  // by device id
+hipError_t fixed_scratch_of(int32_t device, float **out) {
+  std::lock_guard<std::mutex> lock(g_fixed_mu);
+  if ((size_t)device >= g_fixed_ptr.size()) g_fixed_ptr.resize((size_t)device + 1, nullptr);
+  if (!g_fixed_ptr[(size_t)device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_fixed_ptr[(size_t)device] = (float *)p;
+  }
+  *out = g_fixed_ptr[(size_t)device];
+  return hipSuccess;
 }
 
 // Grow a device buffer (contents are not kept); waits for queued work first.
@@ -236,17 +267,27 @@ int prof_begin(g2b_ctx *c, hipEvent_t *ev1) {
   return G2B_OK;
 }
 
+// fixed: nullptr, or device memory of fixed_floats floats that holds this
+// call's partials (and rotated q) - then nothing is allocated: no work queue,
+// the RoPE table must already cover the positions, and the splits are
+// lengthened until the partials fit.
 int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_seq,
                int32_t max_pos, int64_t total_pos, int32_t layer0, int32_t n_layers, float *q,
                const float *k, const float *v, float *att, int32_t att_stride,
-               bool dry = false) {
+               bool dry = false, float *fixed = nullptr, size_t fixed_floats = 0) {
   if (layer0 < 0 || n_layers < 1 || layer0 + n_layers > c->shape.n_layers)
     return fail(c, G2B_EINVAL, "layers [%d,%d) outside [0,%d)", layer0, layer0 + n_layers,
                 c->shape.n_layers);
   if (!q || !k || !v) return fail(c, G2B_EINVAL, "q/k/v must be device pointers");
   if (att && att_stride < max_pos + 1)
     return fail(c, G2B_EINVAL, "att_stride %d < pos+1 = %d", att_stride, max_pos + 1);
-  if (int rc = ensure_rope(c, max_pos + 1)) return rc;
+  if (fixed) {
+    if (c->sh.rope_on && c->rope_len < max_pos + 1)
+      return fail(c, G2B_EINVAL, "the RoPE table covers %d positions, pos %d needs more: "
+                  "allocate the KV with g2b_kv_alloc first", c->rope_len, max_pos);
+  } else if (int rc = ensure_rope(c, max_pos + 1)) {
+    return rc;
+  }
 
   const int32_t nh = c->shape.n_heads, hd = c->shape.head_dim;
   const size_t nq = (size_t)nh * hd;
@@ -316,12 +357,22 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // split partials per sequence and layer: at most 512 (k_combine stages a
   // weight per partial), and n_seq of them within g2b_splits_per_layer_cap,
   // the bound g2b_hbm_bytes budgets
-  const int32_t splits_per_seq =
+  int32_t splits_per_seq =
       (int32_t)std::min<uint64_t>(512, g2b_splits_per_layer_cap(n_seq) / (uint64_t)n_seq);
+  // the fixed scratch: rotated q (generic path) first, then the partials
+  const size_t fixed_qrot = fixed && !fast ? ((size_t)n_layers * n_seq * nq + 63) & ~(size_t)63 : 0;
+  if (fixed) {
+    const size_t per_split = (size_t)n_layers * n_seq * nh * (size_t)(kPartHead + hd);
+    const size_t fit = fixed_floats > fixed_qrot ? (fixed_floats - fixed_qrot) / per_split : 0;
+    if (fit < 1)
+      return fail(c, G2B_EUNSUP, "one split's partials (%zu bytes) exceed the %zu-byte scratch",
+                  (fixed_qrot + per_split) * 4, fixed_floats * 4);
+    splits_per_seq = (int32_t)std::min<size_t>((size_t)splits_per_seq, fit);
+  }
   const int64_t wq_slots = tiles                        ? tiles_slots(c, true)
                            : fast && dp.stage_mode != 0 ? slots_for(c, dp, true)
                                                          : 0;
-  const bool use_wq = fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
+  const bool use_wq = !fixed && fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
                        wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
   const int64_t slots = use_wq ? wq_slots : tiles ? tiles_slots(c, false) : slots_for(c, dp, false);
@@ -402,15 +453,21 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
 
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              (size_t)(kPartHead + hd);
-  const size_t part_limit = (size_t)c->shape.n_layers * (size_t)g2b_splits_per_layer_cap(n_seq) *
-                            nh * (size_t)(kPartHead + hd);
-  if (int rc = grow(c, &c->part, &c->part_cap, part_floats, part_limit)) return rc;
-  if (!fast) {
-    const size_t qf = (size_t)n_layers * n_seq * nq;
-    if (int rc = grow(c, &c->qrot, &c->qrot_cap, qf, qf)) return rc;
+  if (fixed) {
+    dp.q_rot = fixed;
+    dp.part = fixed + fixed_qrot;
+  } else {
+    const size_t part_limit = (size_t)c->shape.n_layers *
+                              (size_t)g2b_splits_per_layer_cap(n_seq) * nh *
+                              (size_t)(kPartHead + hd);
+    if (int rc = grow(c, &c->part, &c->part_cap, part_floats, part_limit)) return rc;
+    if (!fast) {
+      const size_t qf = (size_t)n_layers * n_seq * nq;
+      if (int rc = grow(c, &c->qrot, &c->qrot_cap, qf, qf)) return rc;
+    }
+    dp.part = c->part;
+    dp.q_rot = c->qrot;
   }
-  dp.part = c->part;
-  dp.q_rot = c->qrot;
   if (dry) return G2B_OK;  // (the buffers this schedule needs exist now)
 
   if (!fast) {  // generic shapes: append, decode, combine
@@ -421,7 +478,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     ap.n_seq = n_seq;
     ap.layer0 = layer0;
     ap.q_in = q;
-    ap.q_rot = c->qrot;
+    ap.q_rot = fixed ? fixed : c->qrot;
     ap.k_in = k;
     ap.v_in = v;
     ap.rope = c->rope;
@@ -538,6 +595,13 @@ int g2b_ctx_create(g2b_ctx **out, int32_t device, const g2b_shape *s) {
     return G2B_EDEVICE;
   }
   c->stream = c->own;
+  if (fixed_scratch_of(device, &c->fixed) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipEventDestroy(c->seqs_ev);
+    (void)hipStreamDestroy(c->own);
+    delete c;
+    return G2B_EDEVICE;
+  }
   int n_cu = 0;
   if (hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     n_cu = 0;
@@ -773,6 +837,25 @@ int g2b_attn_forward(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, vo
   one.k = (uint8_t *)kc;
   one.v = (uint8_t *)vc;
   return run_layers(c, nullptr, one, 1, pos, (int64_t)pos + 1, layer, 1, q, k, v, att, ctx_cap);
+}
+
+int g2b_attn_forward_noalloc(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, void *kc,
+                             void *vc, float *q, const float *k, const float *v) {
+  if (!c) return G2B_EINVAL;
+  if (!kc || !vc) return fail(c, G2B_ENOKV, "KV cache not allocated");
+  if (misaligned(kc) || misaligned(vc))
+    return fail(c, G2B_EINVAL, "KV caches must be 16-byte aligned");
+  if (ctx_cap < 1 || pos < 0 || pos >= ctx_cap)
+    return fail(c, G2B_EPOS, "pos=%d outside [0,%d)", pos, ctx_cap);
+  if (!c->fixed) return fail(c, G2B_EDEVICE, "no scratch address for device %d", c->device);
+  if (int rc = set_device(c)) return rc;
+  SeqDev one{};
+  one.pos = pos;
+  one.ctx_cap = ctx_cap;
+  one.k = (uint8_t *)kc;
+  one.v = (uint8_t *)vc;
+  return run_layers(c, nullptr, one, 1, pos, (int64_t)pos + 1, layer, 1, q, k, v, nullptr, 0,
+                    false, c->fixed, kFixedScratchBytes / sizeof(float));
 }
 
 int g2b_attn_forward_host(g2b_ctx *c, int32_t layer, int32_t pos, int32_t ctx_cap, void *kc,

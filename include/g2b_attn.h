@@ -190,6 +190,21 @@ int g2b_attn_forward(g2b_ctx *ctx, int32_t layer, int32_t pos, int32_t ctx_cap,
                      void *kcache, void *vcache, float *q, const float *k,
                      const float *v, float *att);
 
+/* The same call, allocating nothing: no counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Its scratch (the
+ * split partials, and the rotated q of shapes without a specialised kernel)
+ * is a fixed 2 MiB array in the library's device memory, one per GPU, held
+ * until the process ends; every call on a GPU shares that GPU's array, so
+ * calls that overlap on one GPU race.  It never uses the work-queue schedule
+ * (whose counters need clearing) and lengthens its splits until the partials
+ * fit; a shape whose one split does not fit is G2B_EUNSUP.  The RoPE table
+ * must already cover pos (g2b_kv_alloc of the cache extends it): G2B_EINVAL
+ * otherwise.  No weights output.  Asynchronous like g2b_attn_forward. */
+int g2b_attn_forward_noalloc(g2b_ctx *ctx, int32_t layer, int32_t pos, int32_t ctx_cap,
+                             void *kcache, void *vcache, float *q, const float *k,
+                             const float *v);
+
 /* Same, with q/k/v/att in HOST memory (the reference keeps them in m->buf):
  * copies in, runs, copies the output back over q, and returns when done. */
 int g2b_attn_forward_host(g2b_ctx *ctx, int32_t layer, int32_t pos, int32_t ctx_cap,
