@@ -33,6 +33,7 @@ and two units in float64).  rank 0 prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -144,6 +145,7 @@ class Workload:
         log(f"{name}: {desc}; n_seq={n_seq}, KV {kv_total / 1e9:.2f} GB")
         self.ctx = ctx = attn.Context(shape)
         ctx.tune(args.split, args.chunk, args.stage, args.piece)
+        ctx.tune_kernel(args.kernel)
         t0 = time.perf_counter()
         self.kvs = [ctx.kv_alloc(c) for c in self.caps]
         for i, (p, c) in enumerate(zip(poss, self.caps)):
@@ -180,13 +182,15 @@ class Workload:
         self.ctx.attn_layers(0, self.shape.n_layers, self.qw.ptr, self.kb.ptr, self.vb.ptr)
 
     def timed(self, step, steps, warmup):
-        """(event ms per step, host ms per step, decode-kernel ms summed, launches)."""
+        """(event ms per step, host ms per step, decode-kernel ms summed, launches).
+        The step time comes from a pass with nothing but the step on the
+        stream; the decode kernels' own durations from a second pass of the
+        same steps with a pair of events around every decode launch (which
+        would otherwise add their own gaps to the step)."""
         ctx = self.ctx
         for _ in range(warmup):
             step()
         ctx.sync()
-        ctx.profile(True)
-        ctx.profile_read()
         e0, e1 = hip.Event(), hip.Event()
         h0 = time.perf_counter()
         e0.record(ctx.stream)
@@ -195,6 +199,10 @@ class Workload:
         e1.record(ctx.stream)
         e1.synchronize()
         wall = time.perf_counter() - h0
+        ctx.profile(True)
+        ctx.profile_read()
+        for _ in range(steps):
+            step()
         dms, nlaunch = ctx.profile_read()
         ctx.profile(False)
         return e0.elapsed_ms(e1) / steps, wall / steps * 1e3, dms, nlaunch
@@ -206,6 +214,7 @@ class Workload:
         CPU baseline in both modes and the full-size parity sample.  Leaves
         the layer-serial outputs in qw."""
         ms, wall_ms, dms, dn = self.timed(self.step_layer_serial, steps, warmup)
+        sched = self.ctx.last_schedule()
         sb, L = self.bytes_per_step, self.shape.n_layers
         gbps = sb / (ms * 1e-3) / 1e9
         dec_ms = dms / max(dn, 1)
@@ -229,13 +238,14 @@ class Workload:
                "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
                "bytes_per_step": sb, "kv_fill_s": round(self.t_fill, 2),
                "step": "layer-serial: one g2b_attn_layers call per layer",
-               "roofline": roof}
+               "schedule": sched, "roofline": roof}
         if fused:
             fms, _, fdms, fdn = self.timed(self.step_fused, steps, 1)
             out["all_layers_one_call"] = {
                 "us_per_step": round(fms * 1e3, 2), "GBps": round(sb / (fms * 1e-3) / 1e9, 2),
                 "pct_hbm_peak": round(100 * sb / (fms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
-                "decode_kernel_avg_us": round(fdms / max(fdn, 1) * 1e3, 2)}
+                "decode_kernel_avg_us": round(fdms / max(fdn, 1) * 1e3, 2),
+                "schedule": self.ctx.last_schedule()}
             log(f"{self.name}: all layers in one call {fms * 1e3:.1f} us/step, "
                 f"{out['all_layers_one_call']['GBps']} GB/s")
         # the layer-serial outputs, for the parity sample
@@ -288,6 +298,9 @@ def main():
                          "2 register-pipelined chunks through LDS (0 = automatic)")
     ap.add_argument("--piece", type=int, default=0,
                     help="schedule: -1 static splits, >0 work-queue piece length (0 = automatic)")
+    ap.add_argument("--kernel", type=int, default=0, choices=(0, 1, 2, 3),
+                    help="decode kernel: 0 automatic, 1 k_layer only, 2 k_tiles where it "
+                         "applies, 3 spanned k_short wherever it applies")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="before timing, run one plain copy kernel of this many MiB (a "
                          "known-size reference for rocprofv3 byte counters)")
@@ -456,21 +469,32 @@ def model_leg(args):
     """A whole decode step on the device (g2b_model_forward, model_forward of
     l5_model.c:461-606) for a Qwen3-0.6B-shape model with random Q8_0 weights
     (28 layers, dim 1024, hidden 3072, 16/8 heads of 128, vocab 151936, tied
-    embeddings, QK-RMSNorm; 0.63 GB) written as a G2BX file, Q8_0 KV: decode
-    tokens per second at positions 8..8+K, next to the reference's own
-    model_forward (compiled reference, AVX2+OpenMP) on the same file, whose
-    first steps also check the device's logits."""
+    embeddings, QK-RMSNorm; 0.63 GB) written as a G2BX file, Q8_0 KV, in two
+    windows: positions 8..8+K (below 128: the attention is the single-span
+    short kernel) and positions from 4096 (the KV of positions 0..4095
+    filled with seeded rows on the device; the attention schedule the
+    automatic choice took is recorded).  Beside each, the reference's own
+    model_forward (compiled reference, AVX2+OpenMP) on the same file - for
+    the long window on the same KV bytes - whose first steps also check the
+    device's logits."""
     import tempfile
     from oracle import orc  # CPU baseline and checker only
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from helpers import F_QK_NORM, F_TIE_EMBD, random_model_slots, write_g2bx
 
     cfg = dict(dim=1024, hidden_dim=3072, n_layers=28, n_heads=16, n_kv_heads=8, vocab=151936,
-               seq_len=4096, head_dim=128, eps=1e-6, rope_theta=1e6)
+               seq_len=8192, head_dim=128, eps=1e-6, rope_theta=1e6)
     flags = F_QK_NORM | F_TIE_EMBD
     rng = np.random.default_rng(args.seed + 11)
+    P0 = 4096
     fd, path = tempfile.mkstemp(suffix=".g2bx")
     os.close(fd)
+    have_ref = orc.ref_lib("avx2") is not None
+
+    def rel_diff(dev, ref):
+        return max(float(np.abs(dev[i] - ref[i]).max() / max(1.0, np.abs(ref[i]).max()))
+                   for i in range(len(ref)))
+
     try:
         slots = random_model_slots(rng, cfg, flags, attn.T_Q8_0, attn.T_Q8_0, None)
         wbytes = sum(len(s[3]) for s in slots)
@@ -484,43 +508,76 @@ def model_leg(args):
             for i in range(8, 8 + K):
                 m.forward(toks[i], i)
             dt = (time.perf_counter() - t0) / K
+            # the long window: positions 0..P0-1 of every layer filled on the
+            # device (seeded N(0,1) rows through the append arithmetic)
+            kc, vc, cap = m.kv()
+            mctx = attn.lib().g2b_model_ctx(m.h)
+            rc = attn.lib().g2b_synth_fill_kv(mctx, kc, vc, cap, 0, cfg["n_layers"], 0, P0,
+                                              args.seed, 0, float("inf"))
+            if rc or attn.lib().g2b_sync(mctx):
+                raise RuntimeError(f"KV fill of the model failed ({rc})")
+            nbytes = attn.kv_bytes(attn.Shape(cfg["n_layers"], 16, 8, 128, 1e6,
+                                              attn.ARCH_QWEN3, True), cap)
+            kbytes = hip.copy_d2h(kc, np.uint8, nbytes) if have_ref else None
+            vbytes = hip.copy_d2h(vc, np.uint8, nbytes) if have_ref else None
+            ltoks = [int(t) for t in rng.integers(0, cfg["vocab"], 4 + K)]
+            lfirst = [m.forward(ltoks[i], P0 + i) for i in range(4)]
+            t0 = time.perf_counter()
+            for i in range(4, 4 + K):
+                m.forward(ltoks[i], P0 + i)
+            ldt = (time.perf_counter() - t0) / K
+            sched = (C.c_int32 * 6)()
+            attn.lib().g2b_ctx_last_schedule(mctx, sched)
+            lsched = {"kernel": attn.Context.KERNEL_NAMES.get(sched[0], "none"),
+                      "split_len": sched[1], "max_splits": sched[3], "workgroups": sched[4],
+                      "output_in_kernel": bool(sched[5])}
+            kv_cap = cap
         res = {"workload": "Qwen3-0.6B shape, random Q8_0 weights (tied embeddings, QK-RMSNorm), "
-                           "Q8_0 KV, batch 1, positions 8.." + str(8 + K - 1),
-               "ms_per_token": round(dt * 1e3, 3), "tokens_per_s": round(1 / dt, 1),
+                           "Q8_0 KV, batch 1",
                "weight_bytes": int(wbytes),
-               "weight_GBps": round(wbytes / dt / 1e9, 1),
-               # embedding, 5 per layer (four fused GEMVs and the attention: one
-               # split, no combine, at these positions), logits
-               "launches_per_token": cfg["n_layers"] * 5 + 2}
-        if orc.ref_lib("avx2") is not None:
-            def rel_diff(dev, ref):
-                return max(float(np.abs(dev[i] - ref[i]).max() / max(1.0, np.abs(ref[i]).max()))
-                           for i in range(len(ref)))
+               "short_context": {
+                   "positions": f"8..{8 + K - 1}", "attention": "k_short, one span",
+                   "ms_per_token": round(dt * 1e3, 3), "tokens_per_s": round(1 / dt, 1),
+                   "weight_GBps": round(wbytes / dt / 1e9, 1),
+                   # embedding, 5 per layer (four fused GEMVs and the attention),
+                   # logits
+                   "launches_per_token": cfg["n_layers"] * 5 + 2},
+               "long_context": {
+                   "positions": f"{P0}..{P0 + 3 + K}", "kv_positions_filled": P0,
+                   "attention_schedule": lsched,
+                   "ms_per_token": round(ldt * 1e3, 3), "tokens_per_s": round(1 / ldt, 1),
+                   # plus the combine launch per layer where the splits are not
+                   # merged in the decode kernel
+                   "launches_per_token": cfg["n_layers"] * (
+                       5 if lsched["output_in_kernel"] else 6) + 2}}
+        if have_ref:
             # per-token time of the reference: its token loop alone (the driver
-            # times it, without the file load and KV allocation), positions
-            # 0..7 - at least as short as the device's positions 8..8+K - after
-            # one untimed call that pages the file in and starts the OpenMP threads
+            # times it, without the file load and KV allocation), after one
+            # untimed call that pages the file in and starts the OpenMP threads
             orc.ref_model_forward(path, toks[:1], cfg["vocab"], True, 0)
             ref_q8, secs = orc.ref_model_forward(path, toks[:8], cfg["vocab"], True, 0,
                                                  timed=True)
-            ref_q8 = ref_q8[:5]
-            cdt = secs / 8
-            # parity with an F32 KV (no quantisation of the appended rows: fp32
-            # summation order only), and the Q8_0-KV figure beside it
             ref_f32 = orc.ref_model_forward(path, toks[:5], cfg["vocab"], False, 0)
             with attn.Model(path, kv_q8=False) as m32:
                 dev_f32 = [m32.forward(toks[i], i) for i in range(5)]
-            res.update({"cpu_tokens_per_s": round(1 / cdt, 2),
-                        "cpu_kind": "reference model_forward (AVX2, OpenMP)",
+            lref, lsecs = orc.ref_model_forward_kv(path, True, kv_cap, kbytes, vbytes, P0,
+                                                   ltoks[:4], cfg["vocab"])
+            res["short_context"].update({
+                "cpu_tokens_per_s": round(8 / secs, 2),
+                "max_rel_logit_diff_vs_reference_f32_kv": rel_diff(dev_f32, ref_f32),
+                "max_rel_logit_diff_vs_reference_q8_kv": rel_diff(first[:5], ref_q8[:5])})
+            res["long_context"].update({
+                "cpu_tokens_per_s": round(4 / lsecs, 2),
+                "max_rel_logit_diff_vs_reference_q8_kv": rel_diff(lfirst, lref)})
+            res.update({"cpu_kind": "reference model_forward (AVX2, OpenMP)",
                         "cpu_threads": orc.max_threads(),
-                        "max_rel_logit_diff_vs_reference_f32_kv": rel_diff(dev_f32, ref_f32),
-                        "max_rel_logit_diff_vs_reference_q8_kv": rel_diff(first[:5], ref_q8),
                         "note": "Q8_0 KV: appended rows can quantise one step apart where the "
                                 "two fp32 k/v differ in their last bits; the difference compounds "
                                 "over 28 layers (argmax unchanged)"})
-        log(f"model_forward: {res['ms_per_token']} ms/token ({res['tokens_per_s']} tokens/s, "
-            f"{res['weight_GBps']} GB/s of weights), cpu {res.get('cpu_tokens_per_s')} tokens/s, "
-            f"logits vs reference (F32 KV) {res.get('max_rel_logit_diff_vs_reference_f32_kv')}")
+        log(f"model_forward: {res['short_context']['ms_per_token']} ms/token at positions "
+            f"8.., {res['long_context']['ms_per_token']} ms/token at {P0}..; cpu "
+            f"{res['short_context'].get('cpu_tokens_per_s')} / "
+            f"{res['long_context'].get('cpu_tokens_per_s')} tokens/s")
         return res
     finally:
         os.unlink(path)

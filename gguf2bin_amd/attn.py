@@ -33,13 +33,14 @@ EXPORTS = [
     "g2b_model_kv_bytes", "g2b_clamp_ctx", "g2b_hbm_bytes", "g2b_auto_budget", "g2b_hbm_info",
     "g2b_matmul_row_bytes", "g2b_matmul", "g2b_matmul_host", "g2b_weights_upload",
     "g2b_weights_free", "g2b_g2bx_open", "g2b_g2bx_close", "g2b_g2bx_slot",
-    "g2b_model_load_g2bx", "g2b_model_free", "g2b_model_info", "g2b_model_ctx",
+    "g2b_model_load_g2bx", "g2b_model_free", "g2b_model_info", "g2b_model_ctx", "g2b_model_kv",
     "g2b_model_forward", "g2b_model_use_graph", "g2b_model_set_fused",
     "g2b_batch_begin", "g2b_attn_layers", "g2b_attn_forward", "g2b_attn_forward_host",
     "g2b_attn_forward_noalloc",
     "g2b_rope_table", "g2b_sync",
     "g2b_stream_seed", "g2b_synth_normal", "g2b_synth_fill_kv", "g2b_synth_copy",
     "g2b_ctx_profile", "g2b_ctx_profile_read", "g2b_ctx_tune", "g2b_ctx_tune_kernel",
+    "g2b_ctx_last_schedule",
 ]
 
 
@@ -139,6 +140,7 @@ def lib() -> C.CDLL:
             "g2b_model_info": ([vp, C.POINTER(_ModelCfg), C.POINTER(i32), C.POINTER(i32),
                                 C.POINTER(i32)], C.c_int),
             "g2b_model_ctx": ([vp], vp),
+            "g2b_model_kv": ([vp, C.POINTER(vp), C.POINTER(vp), C.POINTER(i32)], C.c_int),
             "g2b_model_forward": ([vp, i32, i32, fp], C.c_int),
             "g2b_model_use_graph": ([vp, i32], C.c_int),
             "g2b_model_set_fused": ([vp, i32], C.c_int),
@@ -167,6 +169,7 @@ def lib() -> C.CDLL:
             "g2b_ctx_profile": ([vp, i32], C.c_int),
             "g2b_ctx_tune": ([vp, i32, i32, i32, i32], C.c_int),
             "g2b_ctx_tune_kernel": ([vp, i32], C.c_int),
+            "g2b_ctx_last_schedule": ([vp, C.POINTER(C.c_int32)], C.c_int),
             "g2b_ctx_profile_read": ([vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)],
                                      C.c_int),
         }
@@ -239,6 +242,14 @@ class Model:
         if rc:
             raise G2BError(rc, f"g2b_model_forward: {strerror(rc)}")
         return out
+
+    def kv(self):
+        """(K cache, V cache, ctx_cap): the model's device caches."""
+        k, v, cap = C.c_void_p(), C.c_void_p(), C.c_int32()
+        rc = lib().g2b_model_kv(self.h, C.byref(k), C.byref(v), C.byref(cap))
+        if rc:
+            raise G2BError(rc, f"g2b_model_kv: {strerror(rc)}")
+        return k.value, v.value, cap.value
 
     def use_graph(self, on: bool):
         """Capture the step once and replay it (on), or launch every step
@@ -471,8 +482,18 @@ class Context:
         self._check(lib().g2b_ctx_tune(self.h, split_len, chunk, stage, piece), "g2b_ctx_tune")
 
     def tune_kernel(self, kernel: int):
-        """0 automatic, 1 k_layer only, 2 k_tiles where it applies."""
+        """0 automatic, 1 k_layer only, 2 k_tiles where it applies, 3 spanned k_short."""
         self._check(lib().g2b_ctx_tune_kernel(self.h, kernel), "g2b_ctx_tune_kernel")
+
+    KERNEL_NAMES = {1: "k_layer", 2: "k_tiles", 3: "k_short", 4: "k_decode_generic"}
+
+    def last_schedule(self) -> dict:
+        """The last decode call's schedule (g2b_ctx_last_schedule)."""
+        a = (C.c_int32 * 6)()
+        self._check(lib().g2b_ctx_last_schedule(self.h, a), "g2b_ctx_last_schedule")
+        return {"kernel": self.KERNEL_NAMES.get(a[0], "none"), "split_len": a[1],
+                "piece_len": a[2], "max_splits": a[3], "workgroups": a[4],
+                "output_in_kernel": bool(a[5])}
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

@@ -69,8 +69,13 @@ struct g2b_ctx {
   int32_t wq_dirty[2] = {0, 0};  // units of each set a launch may have left non-zero
   bool wq_reset = false;         // a launch failed after using the counters
   int32_t tune_stage = 0;      // -1: k_layer loads straight from HBM; 1, 2: staging mode
-  int32_t tune_kernel = 0;     // 0 automatic, 1 k_layer only, 2 k_tiles where it applies
+  int32_t tune_kernel = 0;     // 0 automatic, 1 k_layer only, 2 k_tiles, 3 spanned k_short
+  int32_t *span_ctr = nullptr; // k_short's span tickets (zero between launches)
+  size_t span_ctr_cap = 0;
   int32_t occ_tiles[2] = {0, 0};  // k_tiles workgroups per CU (static, work queue)
+
+  // the last decode call's schedule (g2b_ctx_last_schedule)
+  int32_t sched[G2B_SCHED_FIELDS] = {};
 
   // decode-launch timing (g2b_ctx_profile)
   bool prof = false;
@@ -93,6 +98,9 @@ struct g2b_ctx {
 // creation.
 constexpr size_t kFixedScratchBytes = (size_t)2 << 20;
 static __device__ __align__(256) float scratch[kFixedScratchBytes / sizeof(float)];
+// Its first kFixedCtrInts words are k_short's span counters: zero at load
+// (static storage) and left zero by every launch; nothing else uses them.
+constexpr size_t kFixedCtrInts = 1024;
 
 namespace {
 
@@ -233,19 +241,51 @@ int32_t tiles_slots(g2b_ctx *c, bool wq) {
   return std::max(1, c->n_cu) * std::max(1, occ);
 }
 
-// min_len: the shortest split worth a workgroup (its waves get a few
-// wave-steps or chunks each; shorter splits cost more in setup and partials
-// than they gain in parallelism).
-int32_t choose_split(const g2b_ctx *c, int64_t slots, int64_t total_pos, int32_t max_pos,
-                     int32_t n_layers, bool fast, int32_t min_len) {
-  const int64_t work = total_pos * (int64_t)n_layers;
-  int64_t sl = c->split_override > 0 ? c->split_override : (work + slots - 1) / slots;
-  if (c->split_override <= 0) sl = std::max<int64_t>(sl, min_len);
-  const int64_t min_for_cap = ((int64_t)max_pos + 1 + 511) / 512;
+// Positions per split of a static schedule.  min_len is the shortest split
+// worth a workgroup (its waves get a few wave-steps or chunks each; shorter
+// splits cost more in setup and partials than they gain).
+//
+// One sequence (every unit the same length): the launch's workgroups,
+// n_layers * ceil((max_pos+1)/len), fill the fewest whole rounds of `slots`
+// that the layers allow (one round for up to `slots` layers), with the
+// shortest splits that fit.  Measured on the single-sequence calls: a launch
+// a few workgroups past a round runs ~35% longer (c1, all layers: 90.8 us at
+// 252 workgroups of 256 slots, 123 us at 308) and many rounds of short
+// splits lose to one round of long ones (100 us at 924); the rule gives c1
+// 252 workgroups (92.7 us, was 109) and c2 504 of 512 (97.5 us, was 131).
+// Batches: the average work per slot, total_pos * n_layers / slots (ragged
+// lengths make whole-round counting moot; measured on the 64-sequence SmolLM2
+// F32 batch (c3), the round rule lost 20% layer-serial and 50% in one call).
+int32_t choose_split(const g2b_ctx *c, int64_t slots, int32_t n_seq, int64_t total_pos,
+                     int32_t max_pos, int32_t n_layers, bool fast, int32_t min_len) {
+  const int64_t hi = (int64_t)max_pos + 1;
+  const int64_t min_for_cap = (hi + 511) / 512;
+  int64_t sl;
+  if (c->split_override > 0) {
+    sl = c->split_override;
+  } else if (n_seq == 1) {
+    const int64_t lo = std::min<int64_t>(std::max<int64_t>(min_len, min_for_cap), hi);
+    const int64_t target = ((int64_t)n_layers + slots - 1) / slots * slots;
+    // the per-layer split count that fits, then the shortest length giving it
+    const int64_t per_layer = std::max<int64_t>(1, target / n_layers);
+    sl = std::max<int64_t>(lo, (hi + per_layer - 1) / per_layer);
+  } else {
+    sl = std::max<int64_t>((total_pos * (int64_t)n_layers + slots - 1) / slots, min_len);
+  }
   sl = std::max(sl, min_for_cap);
   if (!fast) sl = std::min<int64_t>(sl, kGenericMaxSplit);
-  sl = std::min<int64_t>(sl, (int64_t)max_pos + 1);
+  sl = std::min<int64_t>(sl, hi);
   return (int32_t)std::max<int64_t>(sl, 1);
+}
+
+void set_sched(g2b_ctx *c, int32_t kernel, int32_t split_len, int32_t piece_len,
+               int32_t max_splits, int64_t grid, bool direct) {
+  c->sched[0] = kernel;
+  c->sched[1] = split_len;
+  c->sched[2] = piece_len;
+  c->sched[3] = max_splits;
+  c->sched[4] = (int32_t)std::min<int64_t>(grid, INT32_MAX);
+  c->sched[5] = direct ? 1 : 0;
 }
 
 // With g2b_ctx_profile on: records the first of two timing events around
@@ -325,13 +365,84 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
 
-  // Short contexts (every pos < kShortMaxPos), no weights output: k_short,
-  // one workgroup per (KV head, sequence, layer), writes the output over q
-  // itself - no partials, no combine.  An explicit split length or
-  // work-queue piece (g2b_ctx_tune) keeps the split kernel.
-  if (fast && !att && max_pos < kShortMaxPos && c->split_override == 0 && c->tune_piece == 0 &&
-      short_available(c->sh)) {
+  // split partials per sequence and layer: at most 512 (k_combine stages a
+  // weight per partial), and n_seq of them within g2b_splits_per_layer_cap,
+  // the bound g2b_hbm_bytes budgets
+  int32_t splits_per_seq =
+      (int32_t)std::min<uint64_t>(512, g2b_splits_per_layer_cap(n_seq) / (uint64_t)n_seq);
+  // the fixed scratch: k_short's span counters (kFixedCtrInts, kept zero),
+  // the rotated q (generic path), then the partials
+  const size_t fixed_ctr = fixed ? kFixedCtrInts : 0;
+  const size_t fixed_qrot = fixed && !fast ? ((size_t)n_layers * n_seq * nq + 63) & ~(size_t)63 : 0;
+  if (fixed) {
+    const size_t per_split = (size_t)n_layers * n_seq * nh * (size_t)(kPartHead + hd);
+    const size_t used = fixed_ctr + fixed_qrot;
+    const size_t fit = fixed_floats > used ? (fixed_floats - used) / per_split : 0;
+    if (fit < 1)
+      return fail(c, G2B_EUNSUP, "one split's partials (%zu bytes) exceed the %zu-byte scratch",
+                  (used + per_split) * 4, fixed_floats * 4);
+    splits_per_seq = (int32_t)std::min<size_t>((size_t)splits_per_seq, fit);
+  }
+
+  // k_short, no weights output: one workgroup per (KV head, span of
+  // kShortMaxPos positions, sequence, layer).  Below kShortMaxPos positions
+  // it is a single span that writes the output over q itself.  Longer
+  // contexts take it (spans that merge their partials in the kernel, no
+  // combine launch) automatically when one layer of one sequence is asked
+  // for and its spans fit one workgroup per CU: the in-kernel merge saves
+  // the combine launch only while the spans run in a single round (c1, 17
+  // spans x 8 KV heads = 136 workgroups: 525.9 against 556.7 us per
+  // layer-serial step; c2, 65 x 8 = 520: 822 against 695; all 28 layers in
+  // one call 108.7 against 92.7 us).  g2b_ctx_tune_kernel(3) asks for it
+  // wherever it fits.  An explicit split length or work-queue piece
+  // (g2b_ctx_tune) keeps the split kernels.
+  const int32_t n_spans = max_pos / kShortMaxPos + 1;
+  const bool short_ok = fast && !att && c->split_override == 0 && c->tune_piece == 0 &&
+                        short_available(c->sh);
+  const bool spans_wanted =
+      c->tune_kernel == 3 ||
+      (c->tune_kernel == 0 && n_seq == 1 && n_layers == 1 &&
+       (int64_t)n_spans * c->shape.n_kv_heads <= (int64_t)std::max(1, c->n_cu));
+  const bool spans_fit = n_spans <= std::min<int32_t>(kShortMaxSpans, splits_per_seq) &&
+                         (!fixed || (size_t)n_layers * n_seq * c->shape.n_kv_heads <= fixed_ctr);
+  if (short_ok && (n_spans == 1 || (spans_wanted && spans_fit))) {
+    dp.max_splits = n_spans;
+    dp.span_ctr = nullptr;
+    if (n_spans > 1) {
+      const size_t ctrs = (size_t)n_layers * n_seq * c->shape.n_kv_heads;
+      if (fixed) {
+        dp.span_ctr = reinterpret_cast<int32_t *>(fixed);
+        dp.part = fixed + fixed_ctr;
+      } else {
+        const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)n_spans *
+                                   (size_t)(kPartHead + hd);
+        const size_t part_limit = (size_t)c->shape.n_layers *
+                                  (size_t)g2b_splits_per_layer_cap(n_seq) * nh *
+                                  (size_t)(kPartHead + hd);
+        if (int rc = grow(c, &c->part, &c->part_cap, part_floats, part_limit)) return rc;
+        if (ctrs > c->span_ctr_cap) {
+          // (counters are zero between launches: the last span of each
+          // (sequence, layer, KV head) resets its own)
+          G2B_HIP(c, hipStreamSynchronize(c->stream));
+          if (c->span_ctr) G2B_HIP(c, hipFree(c->span_ctr));
+          c->span_ctr = nullptr;
+          c->span_ctr_cap = 0;
+          const size_t cap = std::max<size_t>(ctrs, G2B_SPAN_CTR_MIN);
+          if (hipMalloc((void **)&c->span_ctr, cap * sizeof(int32_t)) != hipSuccess) {
+            c->span_ctr = nullptr;
+            (void)hipGetLastError();
+            return fail(c, G2B_ENOMEM, "span counters");
+          }
+          G2B_HIP(c, hipMemset(c->span_ctr, 0, cap * sizeof(int32_t)));
+          c->span_ctr_cap = cap;
+        }
+        dp.span_ctr = c->span_ctr;
+        dp.part = c->part;
+      }
+    }
     if (dry) return G2B_OK;
+    set_sched(c, G2B_KERNEL_SHORT, kShortMaxPos, 0, n_spans,
+              (int64_t)c->shape.n_kv_heads * n_spans * n_seq * n_layers, true);
     hipEvent_t ev1 = nullptr;
     if (int rc = prof_begin(c, &ev1)) return rc;
     G2B_HIP(c, launch_short(dp, n_layers, c->stream));
@@ -354,21 +465,6 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // the workgroups take the units in turn; otherwise static splits, sized
   // so the launch's workgroups form whole rounds.
   const int64_t n_units = (int64_t)n_seq * n_layers;
-  // split partials per sequence and layer: at most 512 (k_combine stages a
-  // weight per partial), and n_seq of them within g2b_splits_per_layer_cap,
-  // the bound g2b_hbm_bytes budgets
-  int32_t splits_per_seq =
-      (int32_t)std::min<uint64_t>(512, g2b_splits_per_layer_cap(n_seq) / (uint64_t)n_seq);
-  // the fixed scratch: rotated q (generic path) first, then the partials
-  const size_t fixed_qrot = fixed && !fast ? ((size_t)n_layers * n_seq * nq + 63) & ~(size_t)63 : 0;
-  if (fixed) {
-    const size_t per_split = (size_t)n_layers * n_seq * nh * (size_t)(kPartHead + hd);
-    const size_t fit = fixed_floats > fixed_qrot ? (fixed_floats - fixed_qrot) / per_split : 0;
-    if (fit < 1)
-      return fail(c, G2B_EUNSUP, "one split's partials (%zu bytes) exceed the %zu-byte scratch",
-                  (fixed_qrot + per_split) * 4, fixed_floats * 4);
-    splits_per_seq = (int32_t)std::min<size_t>((size_t)splits_per_seq, fit);
-  }
   const int64_t wq_slots = tiles                        ? tiles_slots(c, true)
                            : fast && dp.stage_mode != 0 ? slots_for(c, dp, true)
                                                          : 0;
@@ -428,14 +524,17 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
                             : tiles             ? 8 * kTilesRows
                             : dp.stage_rows > 0 ? kWavesPerSplit * 4 * dp.stage_rows
                                                 : kWavesPerSplit * 8 * decode_ppw(c->sh, dp.tune_chunk);
-    // Per-lane loads (stage_rows == 0): splits sized for ~0.7 of the resident
-    // workgroups - measured on the 64-sequence SmolLM2 F32 batch (c3):
-    // 1304 us per layer-serial step at 0.72 of a round against 1490 us at
-    // 0.9, 1559 us at 1.13 and 1458 us at 1.5 rounds
-    const int64_t split_slots = fast && dp.stage_rows == 0 ? slots * 7 / 10 : slots;
-    int32_t split_len =
-        choose_split(c, std::max<int64_t>(split_slots, 1), total_pos, max_pos, n_layers, fast,
-                     min_len);
+    // Per-lane loads (stage_rows == 0): for one sequence a round is one
+    // workgroup per CU (c1 all layers: 252 workgroups of 228 positions
+    // 92.7 us, 364 of 161 positions 109 us); for batches ~0.7 of the resident
+    // workgroups - measured on the 64-sequence SmolLM2 F32 batch (c3): 1304 us
+    // per layer-serial step at 0.72 of a round against 1490 us at 0.9,
+    // 1559 us at 1.13 and 1458 us at 1.5 rounds
+    const int64_t split_slots = !(fast && dp.stage_rows == 0) ? slots
+                                : n_seq == 1                 ? std::max(1, c->n_cu)
+                                                             : slots * 7 / 10;
+    int32_t split_len = choose_split(c, std::max<int64_t>(split_slots, 1), n_seq, total_pos,
+                                     max_pos, n_layers, fast, min_len);
     max_splits = (max_pos + 1 + split_len - 1) / split_len;
     if (max_splits > splits_per_seq) {  // lengthen the splits to stay within the budget
       split_len = (int32_t)(((int64_t)max_pos + splits_per_seq) / splits_per_seq);
@@ -454,8 +553,8 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              (size_t)(kPartHead + hd);
   if (fixed) {
-    dp.q_rot = fixed;
-    dp.part = fixed + fixed_qrot;
+    dp.q_rot = fixed + fixed_ctr;
+    dp.part = fixed + fixed_ctr + fixed_qrot;
   } else {
     const size_t part_limit = (size_t)c->shape.n_layers *
                               (size_t)g2b_splits_per_layer_cap(n_seq) * nh *
@@ -478,7 +577,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     ap.n_seq = n_seq;
     ap.layer0 = layer0;
     ap.q_in = q;
-    ap.q_rot = fixed ? fixed : c->qrot;
+    ap.q_rot = fixed ? fixed + fixed_ctr : c->qrot;
     ap.k_in = k;
     ap.v_in = v;
     ap.rope = c->rope;
@@ -495,6 +594,9 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   } else {
     G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
   }
+  set_sched(c, tiles ? G2B_KERNEL_TILES : used_fast ? G2B_KERNEL_LAYER : G2B_KERNEL_GENERIC,
+            dp.split_len, use_wq ? dp.piece_len : 0, max_splits,
+            use_wq ? slots : (int64_t)max_splits * n_seq * n_layers, direct && used_fast);
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
   if (!direct || !used_fast) G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {
@@ -626,6 +728,7 @@ int g2b_ctx_destroy(g2b_ctx *c) {
   if (c->qkn_w) (void)hipFree(c->qkn_w);
   if (c->qkn_on) (void)hipFree(c->qkn_on);
   if (c->wq) (void)hipFree(c->wq);
+  if (c->span_ctr) (void)hipFree(c->span_ctr);
   if (c->seqs_ev) (void)hipEventDestroy(c->seqs_ev);
   for (hipEvent_t e : c->prof_ev) (void)hipEventDestroy(e);
   if (c->own) (void)hipStreamDestroy(c->own);
@@ -1038,8 +1141,14 @@ int g2b_ctx_tune(g2b_ctx *c, int32_t split_len, int32_t chunk, int32_t stage, in
 }
 
 int g2b_ctx_tune_kernel(g2b_ctx *c, int32_t kernel) {
-  if (!c || kernel < 0 || kernel > 2) return G2B_EINVAL;
+  if (!c || kernel < 0 || kernel > 3) return G2B_EINVAL;
   c->tune_kernel = kernel;
+  return G2B_OK;
+}
+
+int g2b_ctx_last_schedule(const g2b_ctx *c, int32_t *out) {
+  if (!c || !out) return G2B_EINVAL;
+  for (int i = 0; i < G2B_SCHED_FIELDS; i++) out[i] = c->sched[i];
   return G2B_OK;
 }
 

@@ -120,6 +120,7 @@ struct DecodeParams {
   // k_combine runs - the value k_combine would give for one partial,
   // (float)((double)acc / (double)l).
   int32_t direct_out;
+  int32_t *span_ctr;  // k_short with several spans: [L][n_seq][n_kv_heads] tickets
 };
 constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte line each
 constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit
@@ -171,10 +172,15 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, boo
 hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s);
 // Whether a specialised decode kernel exists for this shape.
 bool decode_fast_available(const ShapeDev &sh);
-// Short contexts (every sequence's pos < kShortMaxPos, no weights output):
-// k_short does RoPE, append and attention with one workgroup per (KV head,
-// sequence, layer) and writes the output over q itself (no combine).
+// k_short (no weights output): RoPE, append and attention with one
+// workgroup per (KV head, span of kShortMaxPos positions, sequence, layer);
+// DecodeParams.max_splits = the call's spans, ceil((max pos + 1) /
+// kShortMaxPos), at most kShortMaxSpans.  A single span writes the output
+// over q itself; with several, the spans of a (sequence, layer, KV head)
+// write partials and the last to finish merges them (span_ctr: one zeroed
+// int32 per (layer of the call, sequence, KV head), left zero again).
 constexpr int kShortMaxPos = 128;
+constexpr int kShortMaxSpans = 512;
 bool short_available(const ShapeDev &sh);
 hipError_t launch_short(const DecodeParams &p, int n_layers, hipStream_t s);
 // Q8_0 KV with head_dim 128, 8 KV heads and 3 or 4 q heads per KV head, no

@@ -20,6 +20,9 @@
 /* Batch descriptor bytes per sequence (SeqDev), at least 64 descriptors. */
 #define G2B_SEQ_DESC_BYTES 32u
 #define G2B_SEQ_DESC_MIN 64u
+/* k_short's span counters: one int32 per (layer of a call, sequence, KV
+ * head), at least this many. */
+#define G2B_SPAN_CTR_MIN 1024u
 /* What one device allocation may take beyond its size (hipMalloc rounds
  * allocations up to pages; 2 MiB covers every size class). */
 #define G2B_ALLOC_GRAIN (2u << 20)

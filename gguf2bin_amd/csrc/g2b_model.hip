@@ -324,6 +324,14 @@ int g2b_model_use_graph(g2b_model *m, int32_t on) {
   return G2B_OK;
 }
 
+int g2b_model_kv(g2b_model *m, void **kcache, void **vcache, int32_t *ctx_cap) {
+  if (!m || !kcache || !vcache || !ctx_cap) return G2B_EINVAL;
+  *kcache = m->kc;
+  *vcache = m->vc;
+  *ctx_cap = m->ctx_cap;
+  return G2B_OK;
+}
+
 int g2b_model_set_fused(g2b_model *m, int32_t on) {
   if (!m) return G2B_EINVAL;
   if (m->fuse != (on != 0)) {

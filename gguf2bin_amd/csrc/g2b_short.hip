@@ -1,5 +1,5 @@
-// g2b_short.hip - k_short: decode attention of short contexts, one
-// workgroup per (KV head, sequence, layer).
+// g2b_short.hip - k_short: decode attention split by KV head and by spans
+// of 128 positions, one workgroup per (KV head, span, sequence, layer).
 //
 // Same work as k_layer for one (sequence, layer) - l5_model.c:505-516
 // (QK-RMSNorm, RoPE, kv_store of the new row) and :518-577 (scores over
@@ -30,6 +30,19 @@
 //      weights and written over q.
 // Scores are in the log2 domain (q . k * log2(e)/sqrt(hd)), so the weights
 // are exp2(s - max): the reference's softmax within fp32 rounding.
+//
+// Contexts longer than one span (up to 512 spans): workgroup (KV head, span)
+// takes positions [128*span, min(pos+1, 128*span+128)), and only the span
+// that holds pos appends the new row.  Instead of the output it writes its
+// G heads' partials (max m, sum l, unnormalised sums of the weighted V) to
+// the partial buffer with device-coherent stores, then takes a ticket from
+// the (sequence, layer, KV head)'s counter with an agent-scope atomic: the
+// span that draws the last ticket resets the counter to zero (so it is zero
+// before every launch without a clearing pass), merges the spans' partials of its
+// heads (weights exp2(m_s - M) with M the largest m, float64 sums, folded in
+// chunks of 16 spans with a running maximum) and writes the output over q.  The merges of different KV heads run on
+// different workgroups at once, and no second launch is needed.  The other
+// spans read q before they take their ticket, so the output may overwrite it.
 #include "g2b_internal.h"
 
 namespace g2b {
@@ -162,19 +175,29 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   __shared__ __align__(16) float xs[(kSMaxG + 2) * XS];
   __shared__ __align__(16) uint8_t rowk[Geo::HBP], rowv[Geo::HBP];
   __shared__ float sc[kSMaxG * kShortMaxPos];  // scores, then weights
+  // the four waves' V sums
   __shared__ __align__(16) float accs[4 * kSMaxG * HD];
-  __shared__ float inv[kSMaxG + 1], lsum[kSMaxG];
+  __shared__ float inv[kSMaxG + 1], lsum[kSMaxG], msh[kSMaxG];
+  __shared__ int32_t s_last;
 
-  const int kvh = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
-  const int layer = P.layer0 + li;
   const ShapeDev &sh = P.sh;
-  const int G = sh.n_heads / sh.n_kv_heads;
+  const int nkvh = sh.n_kv_heads;
+  const int kvh = (int)(blockIdx.x % (unsigned)nkvh), span = (int)(blockIdx.x / (unsigned)nkvh);
+  const int seq = blockIdx.y, li = blockIdx.z;
+  const int layer = P.layer0 + li;
+  const int G = sh.n_heads / nkvh;
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
   const int pos = sd.pos;
-  // (the host schedules this kernel only when every sequence's pos is below
-  // kShortMaxPos; a descriptor that breaks that leaves its output untouched
-  // rather than index past the score table)
-  if (pos < 0 || pos >= kShortMaxPos) return;
+  // positions [t0, t0 + n_here) of this span; the span of pos appends
+  const int t0 = span * kShortMaxPos;
+  if (pos < 0 || t0 > pos) return;  // (a shorter sequence of a ragged batch)
+  const int n_here = min(pos + 1 - t0, kShortMaxPos);
+  const bool owner = t0 + n_here == pos + 1;
+  const int nspans = pos / kShortMaxPos + 1;
+  // (the host sizes the partials and counters for max_splits spans; a
+  // descriptor beyond that leaves its output untouched rather than index
+  // past them)
+  if (nspans > 1 && (nspans > P.max_splits || !P.span_ctr)) return;
   const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
   const size_t nq = (size_t)sh.n_heads * HD, nkv = (size_t)sh.n_kv_heads * HD;
   float *qo = P.q_out + sidx * nq + (size_t)kvh * G * HD;  // q in; the output goes here
@@ -195,23 +218,23 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     const float *src = xh < G ? qo + xh * HD : (xh == G ? ki : vi);
     x4 = *reinterpret_cast<const float4 *>(src + 4 * xj);
   }
-  // Every KV load of the call is issued now, so that it is in flight during
-  // the setup: the K pieces of positions < pos (each thread one piece per
-  // round) and, per wave, the V elements of positions wave, wave + 4, ...
-  // below pos.  Positions at or past pos read row 0 instead (in bounds,
-  // never used), which keeps the loads unconditional.
+  // Every KV load of the span is issued now, so that it is in flight during
+  // the setup: the K pieces of its positions below pos (each thread one
+  // piece per round) and, per wave, the V elements of its positions
+  // t0 + wave, t0 + wave + 4, ... below pos.  Other slots read row 0 instead
+  // (in bounds, never used), which keeps the loads unconditional.
   const int b = t % NB;
   PieceRaw<FMT> kraw[RK];
 #pragma unroll
   for (int r = 0; r < RK; r++) {
-    const int tp = r * PPR + t / NB;
+    const int tp = t0 + r * PPR + t / NB;
     fetch_piece<FMT>(kb + (size_t)(tp < pos ? tp : 0) * row, b, kraw[r]);
   }
   const int e0 = lane * EPL;
   uint32_t vq[VI], vsb[VI];
 #pragma unroll
   for (int i = 0; i < VI; i++) {
-    const int tp = wave + 4 * i;
+    const int tp = t0 + wave + 4 * i;
     fetch_v<FMT, EPL>(vb + (size_t)(tp < pos ? tp : 0) * row, e0, vq[i], vsb[i]);
   }
   if (has_x) *reinterpret_cast<float4 *>(xs + xh * XS + 4 * xj) = x4;
@@ -261,9 +284,11 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   }
   __syncthreads();
 
-  // 4. the new row's slice: LDS copy, then the caches
+  // 4. the new row's slice (the span of pos only): LDS copy, then the caches
   const float *kr = xs + G * XS, *vr = xs + (G + 1) * XS;
-  if constexpr (FMT == 1) {
+  if (!owner) {
+    // nothing to append
+  } else if constexpr (FMT == 1) {
     if (t < 8 * NB) {  // blocks 0..NB-1 of k, then of v; four lanes each
       const int bq = t >> 2, part = t & 3;
       const bool is_k = bq < NB;
@@ -279,7 +304,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     }
   }
   __syncthreads();
-  {
+  if (owner) {
     constexpr int W = HB / 4;  // dwords of a slice (HB is a multiple of 4)
     const size_t off = (size_t)pos * row;
     for (int i = t; i < 2 * W; i += kSThreads) {
@@ -294,8 +319,8 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   const float qscale = P.qscale;
 #pragma unroll
   for (int r = 0; r < RK; r++) {
-    const int tp = r * PPR + t / NB;
-    if (tp <= pos) {  // (uniform over a position's NB lanes)
+    const int lp = r * PPR + t / NB, tp = t0 + lp;
+    if (lp < n_here) {  // (uniform over a position's NB lanes)
       PieceRaw<FMT> pr = kraw[r];
       if (tp == pos) fetch_piece<FMT>(rowk, b, pr);
       float k[32];
@@ -316,7 +341,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
           float s = ((a0 + a1) + (a2 + a3)) * d;
 #pragma unroll
           for (int o = 1; o < NB; o <<= 1) s += __shfl_xor(s, o);
-          if (b == 0) sc[g * kShortMaxPos + tp] = s * qscale;
+          if (b == 0) sc[g * kShortMaxPos + lp] = s * qscale;
         }
       }
     }
@@ -327,16 +352,19 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   if (wave < G) {
     float *s = sc + wave * kShortMaxPos;
     float m = kNegBig;
-    for (int i = lane; i <= pos; i += 64) m = fmaxf(m, s[i]);
+    for (int i = lane; i < n_here; i += 64) m = fmaxf(m, s[i]);
     m = wave_max(m);
     float l = 0.f;
-    for (int i = lane; i <= pos; i += 64) {
+    for (int i = lane; i < n_here; i += 64) {
       const float p = __builtin_amdgcn_exp2f(s[i] - m);
       s[i] = p;
       l += p;
     }
     l = wave_sum(l);
-    if (lane == 0) lsum[wave] = l;
+    if (lane == 0) {
+      lsum[wave] = l;
+      msh[wave] = m;
+    }
   }
   __syncthreads();
 
@@ -348,8 +376,8 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     for (int i = 0; i < EPL; i++) acc[g][i] = 0.f;
 #pragma unroll
   for (int i = 0; i < VI; i++) {
-    const int tp = wave + 4 * i;
-    if (tp <= pos) {
+    const int lp = wave + 4 * i, tp = t0 + lp;
+    if (lp < n_here) {
       uint32_t q = vq[i], sb = vsb[i];
       if (tp == pos) fetch_v<FMT, EPL>(rowv, e0, q, sb);
       float v[EPL];
@@ -357,7 +385,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
 #pragma unroll
       for (int g = 0; g < kSMaxG; g++) {
         if (g < G) {
-          const float p = sc[g * kShortMaxPos + tp];
+          const float p = sc[g * kShortMaxPos + lp];
 #pragma unroll
           for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, v[e], acc[g][e]);
         }
@@ -369,11 +397,110 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
 #pragma unroll
     for (int i = 0; i < EPL; i++) accs[(wave * kSMaxG + g) * HD + e0 + i] = acc[g][i];
   __syncthreads();
+  if (nspans == 1) {
+    for (int i = t; i < G * HD; i += kSThreads) {
+      const int g = i / HD, e = i - g * HD;
+      const float s = (accs[(0 * kSMaxG + g) * HD + e] + accs[(1 * kSMaxG + g) * HD + e]) +
+                      (accs[(2 * kSMaxG + g) * HD + e] + accs[(3 * kSMaxG + g) * HD + e]);
+      qo[g * HD + e] = s / lsum[g];
+    }
+    return;
+  }
+
+  // 8. several spans: this span's partials, a ticket, and the merge by the
+  // span that draws the last one
+  constexpr int PS = kPartHead + HD;
+  const size_t nh = (size_t)sh.n_heads, ms = (size_t)P.max_splits;
+  // partial (head kvh*G + g, slot s) of this (sequence, layer)
+  auto part_of = [&](int g, int sl) {
+    return P.part + ((sidx * nh + (size_t)(kvh * G + g)) * ms + (size_t)sl) * PS;
+  };
+  // The partials travel through device-coherent accesses: agent-scope
+  // atomic stores (write-through to the device's coherence point) that each
+  // thread waits for before the barrier, and agent-scope atomic loads in the
+  // merging span.  The ordering comes from the waits and the ticket; no
+  // L2-wide writeback or invalidation is needed (a release fence per wave
+  // cost more than the whole stream here).
   for (int i = t; i < G * HD; i += kSThreads) {
     const int g = i / HD, e = i - g * HD;
-    const float s = (accs[(0 * kSMaxG + g) * HD + e] + accs[(1 * kSMaxG + g) * HD + e]) +
+    float *pp = part_of(g, span);
+    const float a = (accs[(0 * kSMaxG + g) * HD + e] + accs[(1 * kSMaxG + g) * HD + e]) +
                     (accs[(2 * kSMaxG + g) * HD + e] + accs[(3 * kSMaxG + g) * HD + e]);
-    qo[g * HD + e] = s / lsum[g];
+    __hip_atomic_store(pp + kPartHead + e, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (e == 0) {
+      __hip_atomic_store(pp, msh[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pp + 1, lsum[g], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores are done
+  __syncthreads();
+  if (t == 0) {
+    int32_t *ctr = P.span_ctr + sidx * (size_t)nkvh + (size_t)kvh;
+    const int32_t ticket =
+        __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = ticket == nspans - 1;
+    if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // An online merge over chunks of MC spans: each thread folds in, per
+  // chunk, the (m, l) pairs and its elements' sums of MC spans, all loaded
+  // together (one round trip per chunk rather than a pass for the maxima
+  // and another for the sums): M' = max(M, m_s), weights exp2(m_s - M'),
+  // the running float64 sums scaled by exp2(M - M').
+  constexpr int MC = 16;
+  constexpr int EPT = (kSMaxG * HD + kSThreads - 1) / kSThreads;  // elements per thread
+  float M[EPT];
+  double Lw[EPT], O[EPT];
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    M[j] = kNegBig;
+    Lw[j] = 0.0;
+    O[j] = 0.0;
+  }
+  for (int c0 = 0; c0 < nspans; c0 += MC) {
+    const int nc = min(MC, nspans - c0);
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+      const int i = t + j * kSThreads;
+      if (i >= G * HD) break;
+      const int g = i / HD, e = i - g * HD;
+      uint64_t ml[MC];
+      float a[MC];
+#pragma unroll
+      for (int u = 0; u < MC; u++) {
+        if (u < nc) {
+          const float *pp = part_of(g, c0 + u);
+          ml[u] = __hip_atomic_load(reinterpret_cast<const uint64_t *>(pp), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+          a[u] = __hip_atomic_load(pp + kPartHead + e, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      float mx = M[j];
+#pragma unroll
+      for (int u = 0; u < MC; u++)
+        if (u < nc) mx = fmaxf(mx, __uint_as_float((uint32_t)ml[u]));
+      const double sc = (double)exp2f(M[j] - mx);
+      double lw = Lw[j] * sc, o = O[j] * sc;
+#pragma unroll
+      for (int u = 0; u < MC; u++) {
+        if (u < nc) {
+          const double w = (double)exp2f(__uint_as_float((uint32_t)ml[u]) - mx);
+          lw = fma((double)__uint_as_float((uint32_t)(ml[u] >> 32)), w, lw);
+          o = fma((double)a[u], w, o);
+        }
+      }
+      M[j] = mx;
+      Lw[j] = lw;
+      O[j] = o;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < EPT; j++) {
+    const int i = t + j * kSThreads;
+    if (i < G * HD) qo[i] = (float)(O[j] / Lw[j]);
   }
 }
 
@@ -384,8 +511,10 @@ bool short_available(const ShapeDev &sh) {
 }
 
 hipError_t launch_short(const DecodeParams &p, int n_layers, hipStream_t s) {
-  if (!short_available(p.sh) || n_layers < 1 || p.n_seq < 1) return hipErrorInvalidValue;
-  dim3 grid(p.sh.n_kv_heads, p.n_seq, n_layers);
+  if (!short_available(p.sh) || n_layers < 1 || p.n_seq < 1 || p.max_splits < 1 ||
+      p.max_splits > kShortMaxSpans || (p.max_splits > 1 && (!p.span_ctr || !p.part)))
+    return hipErrorInvalidValue;
+  dim3 grid(p.sh.n_kv_heads * p.max_splits, p.n_seq, n_layers);
   if (p.sh.kv_q8) {
     if (p.sh.head_dim == 128)
       hipLaunchKernelGGL((k_short<1, 128>), grid, dim3(kSThreads), 0, s, p);

@@ -27,9 +27,12 @@
 // Streaming: a workgroup stages tiles of 16 positions - the K and V rows of
 // 16 consecutive positions are two contiguous runs of 16 x row bytes - with
 // coalesced non-temporal 16-byte loads, the next tile's loads in registers
-// while the current tile is consumed from LDS.  Each wave owns two KV heads
-// of every tile, so the waves of a workgroup never merge states: each writes
-// the partials (or, with one split, the output) of its own heads.
+// while the current tile is consumed from LDS.  In LDS each row is padded by
+// 16 bytes: at the plain 1088-byte stride the 16 positions' operand reads
+// all fell on 2 of 32 banks (an 8-way conflict that made LDS the bound).
+// Each wave owns two KV heads of every tile, so the waves of a workgroup
+// never merge states: each writes the partials (or, with one split, the
+// output) of its own heads.
 //
 // Schedules are k_layer's: static splits (workgroup = split x sequence x
 // layer) or the work queue (pieces of a unit claimed per workgroup).  The
@@ -70,7 +73,7 @@ __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
   const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u) +
                        (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
-  const uint32_t tile = 2u * (uint32_t)kTileRows * sh.row_bytes;
+  const uint32_t tile = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
   TilesLds l;
   l.ra = ((pre > tile ? pre : tile) + 15u) & ~15u;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;
@@ -111,16 +114,36 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   const int nkv = P.sh.n_kv_heads * HD;
   const size_t nq = (size_t)n_heads * HD;
   const uint32_t row = P.sh.row_bytes;
+  const uint32_t lrow = row + 16u;  // LDS row stride of the staged tile
   const TilesLds ll = tiles_lds_layout(P.sh);
   float *qrot = reinterpret_cast<float *>(lds);
   float *kr = reinterpret_cast<float *>(lds + nq * 4);
   float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
   float *trq = reinterpret_cast<float *>(lds + nq * 4 + 2 * ((nkv * 4 + 15) & ~15u));
-  uint8_t *tk = lds, *tv = lds + (size_t)TP * row;  // the staged tile
+  uint8_t *tk = lds, *tv = lds + (size_t)TP * lrow;  // the staged tile
   uint8_t *rowk = lds + ll.ra, *rowv = rowk + ll.row_pad;
   float *scr = reinterpret_cast<float *>(lds + ll.scr);
   float *px = reinterpret_cast<float *>(lds + ll.px) + (size_t)wave * tiles_px_floats();
   float *pfac = px + KPW * NB * TP * 4;  // [kv][head] rescale factors
+
+  // LDS offsets of this thread's staged pieces tid, tid + 256, ... (piece p
+  // of a run is row p / (row/16), bytes 16 * (p % (row/16)) of it)
+  uint32_t soff[kTileLoads];
+  {
+    const uint32_t ppr = row / 16u;
+    uint32_t r = (uint32_t)tid / ppr, w = (uint32_t)tid % ppr;
+    const uint32_t dr = (uint32_t)kThreads / ppr, dw = (uint32_t)kThreads % ppr;
+#pragma unroll
+    for (int i = 0; i < kTileLoads; i++) {
+      soff[i] = r * lrow + 16u * w;
+      r += dr;
+      w += dw;
+      if (w >= ppr) {
+        w -= ppr;
+        r += 1;
+      }
+    }
+  }
 
   // lane roles: MFMA row / column (A row, B and C column = position) and
   // quarter (A/B k-quarter, C row group = q head of the group)
@@ -157,8 +180,8 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       for (int i = 0; i < kTileLoads; i++) {
         const uint32_t pc = (uint32_t)(kThreads * i + tid);
         if (pc < np) {
-          *reinterpret_cast<u32x4 *>(tk + 16u * pc) = rk[i];
-          *reinterpret_cast<u32x4 *>(tv + 16u * pc) = rv[i];
+          *reinterpret_cast<u32x4 *>(tk + soff[i]) = rk[i];
+          *reinterpret_cast<u32x4 *>(tv + soff[i]) = rv[i];
         }
       }
     };
@@ -213,12 +236,12 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     const uint32_t vsel = (voff & 2u) ? 0x05040302u : 0x03020100u;
     const uint32_t valn = voff & ~3u;
 
-    // One tile: rows [0, nrows) at K / V (row stride `row`), positions
-    // tpos0.. (rows past nrows read row 0 and are masked).
-    auto consume = [&](const uint8_t *K, const uint8_t *V, int nrows) {
+    // One tile: rows [0, nrows) at K / V, `stride` bytes apart (rows past
+    // nrows read row 0 and are masked).
+    auto consume = [&](const uint8_t *K, const uint8_t *V, int nrows, uint32_t stride) {
       const int rr = col < nrows ? col : 0;
-      const uint8_t *krow = K + (size_t)rr * row;
-      const uint8_t *vrow = V + (size_t)rr * row;
+      const uint8_t *krow = K + (size_t)rr * stride;
+      const uint8_t *vrow = V + (size_t)rr * stride;
       const bool valid = col < nrows && quarter < G;
       float s[KPW];
 #pragma unroll
@@ -292,7 +315,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       const float *pv = px + (vkv * NB + vblk) * TP * 4;
       auto vstep = [&](int t) {
         const float4 p4 = *reinterpret_cast<const float4 *>(pv + t * 4);
-        const uint32_t *w = reinterpret_cast<const uint32_t *>(V + (size_t)t * row + valn);
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(V + (size_t)t * stride + valn);
         const uint32_t x = __builtin_amdgcn_perm(w[1], w[0], vsel);
         const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
@@ -323,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
         __syncthreads();
         const int ns = ts + TP;
         if (ns < tend) issue(ns, min(TP, tend - ns));
-        consume(tk, tv, n);
+        consume(tk, tv, n, lrow);
         ts = ns;
       }
     } else {
@@ -361,13 +384,13 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
         }
         __syncthreads();
         if (npc < pm.npieces) issue(ns, min(TP, npe - ns));
-        consume(tk, tv, n);
+        consume(tk, tv, n, lrow);
         pc = npc;
         ts = ns;
         pe = npe;
       }
     }
-    if (owns_new) consume(rowk, rowv, 1);
+    if (owns_new) consume(rowk, rowv, 1, row);
 
     // The partials (or the output) of the wave's heads: the sums of each
     // head's 16 lanes; m is already shared by them.

@@ -54,6 +54,7 @@ static uint64_t grain(uint64_t b) {
  *   work-queue counters: two sets of max(n_layers*n_seq + 1, 256) lines;
  *   batch descriptors: max(n_seq, 64) of them;
  *   QK-RMSNorm weights and flags: n_layers x (2*head_dim + 1) words;
+ *   the spanned short kernel's counters: n_layers x n_seq x n_kv_heads words;
  *   the host entry point's staging: nq + 2*nkv + n_heads*ctx floats. */
 static uint64_t ctx_bytes(const g2b_shape *s, int32_t ctx, int32_t n_seq) {
   const uint64_t L = (uint64_t)s->n_layers, nh = (uint64_t)s->n_heads;
@@ -64,12 +65,14 @@ static uint64_t ctx_bytes(const g2b_shape *s, int32_t ctx, int32_t n_seq) {
   uint64_t wq_lines = L * ns + 1u;
   if (wq_lines < G2B_WQ_MIN_LINES) wq_lines = G2B_WQ_MIN_LINES;
   const uint64_t descs = ns > G2B_SEQ_DESC_MIN ? ns : G2B_SEQ_DESC_MIN;
+  uint64_t span_ctrs = L * ns * (uint64_t)s->n_kv_heads;
+  if (span_ctrs < G2B_SPAN_CTR_MIN) span_ctrs = G2B_SPAN_CTR_MIN;
   return grain(rope_pos * hd * 4u) +
          grain(L * g2b_splits_per_layer_cap(n_seq) * nh * (G2B_PART_HEAD + hd) * 4u) +
          grain(L * ns * nq * 4u) +
          grain(2u * wq_lines * G2B_WQ_LINE_BYTES) +
          grain(descs * G2B_SEQ_DESC_BYTES) +
-         grain(L * 2u * hd * 4u) + grain(L * 4u) +
+         grain(L * 2u * hd * 4u) + grain(L * 4u) + grain(span_ctrs * 4u) +
          grain((nq + 2u * nkv + nh * (uint64_t)ctx) * 4u);
 }
 

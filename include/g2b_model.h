@@ -84,6 +84,11 @@ int g2b_model_info(const g2b_model *m, g2b_model_cfg *cfg, int32_t *arch, int32_
                    int32_t *ctx);
 /* The attention context the model runs on (stream, tuning, errors). */
 g2b_ctx *g2b_model_ctx(g2b_model *m);
+/* The model's K and V caches (device, [n_layers][ctx_cap][row] each, in the
+ * model's KV mode) and their capacity: what the reference's Model exposes as
+ * kcache/vcache or kcq/vcq and ctx (include/g2b.h:82-85), e.g. to fill or
+ * read a context with g2b_synth_fill_kv / g2b_kv_read. */
+int g2b_model_kv(g2b_model *m, void **kcache, void **vcache, int32_t *ctx_cap);
 
 /* model_forward (l5_model.c:461-606) on the device for `token` at `pos`:
  * embedding row, then per layer rmsnorm, Q/K/V GEMVs, the decode-attention

@@ -57,11 +57,34 @@ int g2b_synth_copy(g2b_ctx *ctx, void *dst, const void *src, uint64_t nbytes);
  * workgroup per KV head) unless split_len > 0 or piece != 0 is set. */
 int g2b_ctx_tune(g2b_ctx *ctx, int32_t split_len, int32_t chunk, int32_t stage, int32_t piece);
 
-/* Decode kernel choice: 0 automatic (k_tiles - K scores on the int8 matrix
- * cores - for Q8_0 KV with head_dim 128, 8 KV heads and 3-4 q heads per KV
- * head when neither the weights output, a chunk nor a stage other than 2 is
- * asked for; else k_layer), 1 k_layer only, 2 as 0. */
+/* Decode kernel choice.  0 automatic: one layer of a single sequence longer
+ * than 128 positions whose spans of 128 positions times the KV heads fit one
+ * workgroup per CU runs k_short over those spans, which merge their partials
+ * in the kernel; k_tiles (K scores on the int8 matrix cores) for
+ * Q8_0 KV with head_dim 128, 8 KV heads and 3-4 q heads per KV head when
+ * neither the weights output, a chunk nor a stage other than 2 is asked
+ * for; else k_layer.  1: k_layer (no k_tiles, no spans).  2: k_tiles where it
+ * applies, no spans.  3: spans wherever they apply (any batch), else as 0.
+ * Contexts below 128 positions take the single-span k_short in every mode
+ * unless g2b_ctx_tune sets a split length or piece. */
 int g2b_ctx_tune_kernel(g2b_ctx *ctx, int32_t kernel);
+
+/* The schedule of the last decode call that launched (g2b_attn_layers,
+ * g2b_attn_forward and their variants), into out[G2B_SCHED_FIELDS]:
+ *   [0] kernel: G2B_KERNEL_LAYER, _TILES, _SHORT or _GENERIC,
+ *   [1] positions per split (k_short: per span; 0 under the work queue),
+ *   [2] work-queue piece length (0: static splits or spans),
+ *   [3] partial slots per (sequence, layer) (splits, spans or queue slots),
+ *   [4] workgroups launched,
+ *   [5] 1 when the decode kernel wrote the output itself (no combine launch,
+ *       or spans merged in the kernel).
+ * All zero before the first call. */
+#define G2B_SCHED_FIELDS 6
+#define G2B_KERNEL_LAYER 1
+#define G2B_KERNEL_TILES 2
+#define G2B_KERNEL_SHORT 3
+#define G2B_KERNEL_GENERIC 4
+int g2b_ctx_last_schedule(const g2b_ctx *ctx, int32_t *out);
 
 /* Kernel timing with HIP events on the context's stream: while enabled,
  * every decode-kernel launch is bracketed by two events.  _read waits for

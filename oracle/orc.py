@@ -400,6 +400,31 @@ def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
     return (out, secs.value) if timed else out
 
 
+def ref_model_forward_kv(path: str, kv_q8: bool, ctx: int, kbytes: np.ndarray,
+                         vbytes: np.ndarray, pos0: int, tokens, vocab: int):
+    """The compiled reference's model_forward over tokens at positions
+    pos0.. of a G2BX file whose KV positions [0, pos0) are the given cache
+    bytes ([n_layers][ctx][row] each, ctx the model's effective context):
+    (logits [n][vocab], seconds of the token loop)."""
+    L = ref_lib("avx2")
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    fn = L.ref_model_forward_g2bx_kv
+    fn.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_void_p, C.c_void_p, C.c_int,
+                   C.c_void_p, C.c_int, C.c_void_p, C.POINTER(C.c_double)]
+    fn.restype = C.c_int
+    tok = np.ascontiguousarray(tokens, np.int32)
+    kb = np.ascontiguousarray(kbytes, np.uint8)
+    vb = np.ascontiguousarray(vbytes, np.uint8)
+    out = np.zeros((len(tok), vocab), np.float32)
+    secs = C.c_double(0.0)
+    rc = fn(path.encode(), 1 if kv_q8 else 0, ctx, ctx, kb.ctypes.data, vb.ctypes.data, pos0,
+            tok.ctypes.data, len(tok), out.ctypes.data, C.byref(secs))
+    if rc:
+        raise RuntimeError(f"reference forward failed ({rc})")
+    return out, secs.value
+
+
 def random_weights(rng: np.random.Generator, t: int, n: int, d: int) -> np.ndarray:
     """d rows of random blocks: fp16 scales in [2^-10, 2^-4), int8 quants in
     [-128, 127] (Q8_0) or nibbles (Q4_0); N(0,1) floats for F32."""

@@ -267,3 +267,34 @@ int ref_model_forward_g2bx(const char *path, int kv_q8, int ctx, const i32 *toke
   model_free(&m);
   return 0;
 }
+
+/* model_forward over tokens at positions pos0..pos0+n-1 of a G2BX file whose
+ * KV positions [0, pos0) are given as bytes (kbytes, vbytes: the K and V
+ * caches [n_layers][ctx][row] in the mode kv_q8 selects, ctx = the model's
+ * effective context after model_set_ctx(ctx), which must equal cap): the
+ * reference's own decode step at a long context, without a prefill through
+ * pos0 forwards.  Logits of every step into out[n][vocab]; secs (may be NULL)
+ * receives the wall time of the token loop alone (CLOCK_MONOTONIC). */
+int ref_model_forward_g2bx_kv(const char *path, int kv_q8, int ctx, int cap, const u8 *kbytes,
+                              const u8 *vbytes, int pos0, const i32 *tokens, int n, f32 *out,
+                              double *secs) {
+  Model m;
+  if (model_load_g2bx(path, &m)) return -1;
+  if (kv_q8) m.flags |= F_KV_Q8;
+  if (model_set_ctx(&m, ctx > 0 ? ctx : m.c.seq_len) || m.ctx != cap) {
+    model_free(&m);
+    return -2;
+  }
+  const i32 nkv = m.c.n_kv_heads * m.c.head_dim;
+  const size_t row = kv_q8 ? kv_q8_rowsize(nkv) : (size_t)nkv * sizeof(f32);
+  const size_t nbytes = (size_t)m.c.n_layers * (size_t)m.ctx * row;
+  memcpy(kv_q8 ? (void *)m.kcq : (void *)m.kcache, kbytes, nbytes);
+  memcpy(kv_q8 ? (void *)m.vcq : (void *)m.vcache, vbytes, nbytes);
+  struct timespec t0, t1;
+  clock_gettime(CLOCK_MONOTONIC, &t0);
+  for (int i = 0; i < n; i++) model_forward(&m, tokens[i], pos0 + i, out + (size_t)i * m.c.vocab);
+  clock_gettime(CLOCK_MONOTONIC, &t1);
+  if (secs) *secs = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+  model_free(&m);
+  return 0;
+}

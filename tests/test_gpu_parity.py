@@ -192,7 +192,7 @@ MODES = {
 
 
 def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, norms=None,
-                   setup=None, tune=None, misalign=0, kernel=0):
+                   setup=None, tune=None, misalign=0, kernel=0, sched=None):
     """n_seq ragged sequences, all layers: device (one fused call or layer by
     layer) against the oracle, sequence by sequence.  tune: None or the
     g2b_ctx_tune arguments for the context.  norms: None, or
@@ -201,7 +201,8 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
     its inputs with them, and they are set on the context unless setup(ctx)
     is given to do that itself.  misalign: byte offset of q, k and v in their
     device buffers (not a multiple of 16: the generic kernels run).  kernel:
-    g2b_ctx_tune_kernel (0 automatic, 1 k_layer only)."""
+    g2b_ctx_tune_kernel (0 automatic, 1 k_layer only).  sched: None or a
+    dict that receives the last call's schedule (g2b_ctx_last_schedule)."""
     n_seq, nL = len(caps), o.n_layers
     rng_seed = seed * 1000
     qn, kn, eps = norms if norms else (None, None, 1e-6)
@@ -256,6 +257,8 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
                     ctx.attn_layers(L, 1, qd.ptr + off_q, kd.ptr + off_k, vd.ptr + off_k,
                                     (att.ptr + off_a) if att else None, stride)
             ctx.sync()
+            if sched is not None:
+                sched.update(ctx.last_schedule())
             out = qd.download(np.float32, q.size, base).reshape(q.shape)
             w = (att.download(np.float32, nL * n_seq * o.n_heads * stride)
                  .reshape(nL, n_seq, o.n_heads, stride) if att else None)
