@@ -23,7 +23,7 @@ Bytes per step are algorithmic, as BASELINE states them:
 Every config (the headline, then c1, c2, c3, c5 under all_configs) reports
 the same block: the layer-serial step, its dominant decode kernel against
 the HBM roofline (HIP-event launch time; HBM traffic from the committed
-rocprofv3 summary profiles/traffic_<config>.json), the all-layers call, the
+rocprofv3 summary profiles/traffic_<kernel>_<config>.json), the all-layers call, the
 CPU baseline - the C99 oracle (a restatement of the reference path, built
 with the reference flags) on the same KV bytes and inputs, mode A one thread
 over sequences in turn, mode B OpenMP over sequences - and a full-size
@@ -106,11 +106,12 @@ def launch_bytes(s: attn.Shape, poss, layers_per_launch: int) -> int:
     return step_bytes(s, poss) // s.n_layers * layers_per_launch
 
 
-def load_traffic(workload: str):
-    """HBM bytes per launch of the workload's dominant decode kernel, measured
-    with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by a copy kernel
-    of known size, when that summary has been committed under profiles/."""
-    p = os.path.join(ROOT, "profiles", f"traffic_{workload}.json")
+def load_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of the workload's decode kernel, measured with
+    rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by a copy kernel of
+    known size, when that summary (profiles/traffic_<kernel>_<workload>.json)
+    has been committed."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{kernel}_{workload}.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -223,8 +224,8 @@ class Workload:
         log(f"{self.name}: layer-serial {ms * 1e3:.1f} us/step (host {wall_ms * 1e3:.1f}), "
             f"{gbps:.1f} GB/s, {100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak; decode kernel "
             f"{dn} launches, avg {dec_ms * 1e3:.2f} us, {dec_gbps:.1f} GB/s")
-        traffic = load_traffic(self.name)
-        roof = {"bound": "hbm", "kernel": traffic.get("kernel") if traffic else "decode kernel",
+        traffic = load_traffic(self.name, sched["kernel"])
+        roof = {"bound": "hbm", "kernel": traffic.get("kernel") if traffic else sched["kernel"],
                 "achieved": round(dec_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": per_launch,
                 "avg_launch_us": round(dec_ms * 1e3, 3),

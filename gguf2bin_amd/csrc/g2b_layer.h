@@ -347,7 +347,8 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
 // n_kv_heads + 1) floats holding q and k transposed in float4 groups -
 // elements 4i..4i+3 of head H at float4 [i][H] - so each head's sum reads
 // 16-byte pieces without bank conflicts; dig (DIG) reuses tr once the sums
-// are done: dig_stride<CD>() dwords per chunk, chunk h * (hd / CD) + c.
+// are done, or is digp where the caller gives it (outside qrot, kr and vr):
+// dig_stride<CD>() dwords per chunk, chunk h * (hd / CD) + c.
 template <int CD>
 constexpr int dig_stride() {
   return (3 * (CD / 4) + 1 + 3) & ~3;  // three planes, the unit, 16-byte rows
@@ -358,7 +359,8 @@ __device__ inline void visit_setup(const ShapeDev &sh, const SeqDev &sd, int lay
                                    const float *qi, const float *ki, const float *vi,
                                    const float *rope, const NormDev &norm, float qscale,
                                    float *qrot, float *kr, float *vr, uint8_t *rowk,
-                                   uint8_t *rowv, float *scr, float *tr) {
+                                   uint8_t *rowv, float *scr, float *tr,
+                                   uint32_t *digp = nullptr) {
   constexpr int half = HD / 2;
   constexpr int gph = half / 4;  // rope groups per head
   static_assert(half % 4 == 0, "four pairs per group");
@@ -499,7 +501,7 @@ __device__ inline void visit_setup(const ShapeDev &sh, const SeqDev &sd, int lay
     // elements k*CD/4 .. (k+1)*CD/4 - 1; the chunk maximum over the quarter's
     // four lanes (consecutive threads)
     constexpr int QE = CD / 4;
-    uint32_t *dig = reinterpret_cast<uint32_t *>(tr);
+    uint32_t *dig = digp ? digp : reinterpret_cast<uint32_t *>(tr);
     const int nch = nh * (HD / CD);
     for (int it = threadIdx.x; it < 4 * nch; it += kThreads) {
       const int ch = it >> 2, k = it & 3;

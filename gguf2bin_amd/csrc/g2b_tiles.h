@@ -56,25 +56,34 @@ __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
   return g >= 3 && g <= 4;
 }
 
-// k_tiles' dynamic LDS: [0, ra) is the setup's scratch (rotated q, new k and
-// v, the transposed copy for the QK-RMSNorm sums, then the digit planes) and,
-// once every wave holds its q operands, the staged tile (K rows, then V
-// rows); then the new K and V rows, the setup's norm factors and inputs, and
-// each wave's exchange of p * v_scale ([kv][block][position][head]) and
-// rescale factors ([kv][head]).
+// k_tiles' dynamic LDS: [0, ra) is the setup's scratch and, once every wave
+// holds its q operands, the staged tile (K rows, then V rows); then the new K
+// and V rows, the setup's norm factors, and each wave's exchange of
+// p * v_scale ([kv][block][position][head]) and rescale factors ([kv][head]).
+// The setup's scratch: rotated q at 0, the new k after it, the digit planes
+// after that and the new v last; the transposed copy for the QK-RMSNorm sums
+// lies over q, k and the digit planes, which are written only after the sums
+// (the v copy is written before them, so it stays clear).  ~50 KB for
+// Llama-3-8B's heads: LDS would hold three workgroups per CU; the registers
+// (~240 per lane under the work queue) hold two.
 struct TilesLds {
-  uint32_t ra, row_pad, scr, px, total;
+  uint32_t kr, dig, vr, ra, row_pad, scr, px, total;
 };
 __host__ __device__ inline uint32_t tiles_px_floats() {
   return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTileRows * 4 + kTilesKvPerWave * 4);
 }
 __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
-  const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
-  const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u) +
-                       (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
-  const uint32_t tile = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
+  const uint32_t nkv4 = ((uint32_t)(sh.n_kv_heads * sh.head_dim) * 4u + 15u) & ~15u;
+  const uint32_t digb = (uint32_t)(sh.n_heads * (sh.head_dim / 32) * dig_stride<32>()) * 4u;
+  const uint32_t trb = (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
   TilesLds l;
+  l.kr = nq * 4u;
+  l.dig = l.kr + nkv4;
+  const uint32_t dig_end = l.dig + digb;
+  l.vr = ((dig_end > trb ? dig_end : trb) + 15u) & ~15u;
+  const uint32_t pre = l.vr + nkv4;
+  const uint32_t tile = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
   l.ra = ((pre > tile ? pre : tile) + 15u) & ~15u;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;
   l.scr = l.ra + 2u * l.row_pad;
@@ -117,9 +126,10 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   const uint32_t lrow = row + 16u;  // LDS row stride of the staged tile
   const TilesLds ll = tiles_lds_layout(P.sh);
   float *qrot = reinterpret_cast<float *>(lds);
-  float *kr = reinterpret_cast<float *>(lds + nq * 4);
-  float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
-  float *trq = reinterpret_cast<float *>(lds + nq * 4 + 2 * ((nkv * 4 + 15) & ~15u));
+  float *kr = reinterpret_cast<float *>(lds + ll.kr);
+  float *vr = reinterpret_cast<float *>(lds + ll.vr);
+  float *trq = reinterpret_cast<float *>(lds);  // the norm sums' transposed copy
+  uint32_t *digs = reinterpret_cast<uint32_t *>(lds + ll.dig);
   uint8_t *tk = lds, *tv = lds + (size_t)TP * lrow;  // the staged tile
   uint8_t *rowk = lds + ll.ra, *rowv = rowk + ll.row_pad;
   float *scr = reinterpret_cast<float *>(lds + ll.scr);
@@ -192,14 +202,14 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     // Q8_0 blocks) and the owner's append, all in LDS
     visit_setup<HD, 32, true>(P.sh, sd, layer, owns_new, P.q_in + sidx * nq, P.k_in + sidx * nkv,
                               P.v_in + sidx * nkv, P.rope, P.norm, P.qscale, qrot, kr, vr, rowk,
-                              rowv, scr, trq);
+                              rowv, scr, trq, digs);
     // A operands: digit plane (col & 3) of head (col >> 2), bytes
     // 8*quarter .. of block b; and the C lanes' units 2^(e-22) of
     // (head quarter, block b)
     uint64_t qa[KPW][NB];
     float un[KPW][NB];
     {
-      const uint32_t *dig = reinterpret_cast<const uint32_t *>(trq);
+      const uint32_t *dig = digs;
       constexpr int DS = dig_stride<32>();
       const int ah = col >> 2, ap = col & 3;
 #pragma unroll
