@@ -56,18 +56,18 @@ __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
   return g >= 3 && g <= 4;
 }
 
-// k_tiles' dynamic LDS: [0, ra) is the setup's scratch and, once every wave
-// holds its q operands, the staged tile (K rows, then V rows); then the new K
-// and V rows, the setup's norm factors, and each wave's exchange of
+// k_tiles' dynamic LDS: two tile buffers (each the K rows, then the V rows,
+// of 16 positions at a padded stride), then each wave's exchange of
 // p * v_scale ([kv][block][position][head]) and rescale factors ([kv][head]).
-// The setup's scratch: rotated q at 0, the new k after it, the digit planes
-// after that and the new v last; the transposed copy for the QK-RMSNorm sums
-// lies over q, k and the digit planes, which are written only after the sums
-// (the v copy is written before them, so it stays clear).  ~50 KB for
-// Llama-3-8B's heads: LDS would hold three workgroups per CU; the registers
-// (~240 per lane under the work queue) hold two.
+// The setup's scratch lies over the tile buffers: rotated q at 0, the new k
+// after it, the digit planes after that and the new v, then the new K and V
+// rows and the norm factors; the transposed copy for the QK-RMSNorm sums lies
+// over q, k and the digit planes, which are written only after the sums (the
+// v copy is written before them, so it stays clear).  The new rows are
+// consumed before the first tile is staged.  ~77 KB for Llama-3-8B's heads:
+// two workgroups per CU, as the registers allow.
 struct TilesLds {
-  uint32_t kr, dig, vr, ra, row_pad, scr, px, total;
+  uint32_t kr, dig, vr, rows, row_pad, scr, tb, px, total;
 };
 __host__ __device__ inline uint32_t tiles_px_floats() {
   return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTileRows * 4 + kTilesKvPerWave * 4);
@@ -82,14 +82,15 @@ __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   l.dig = l.kr + nkv4;
   const uint32_t dig_end = l.dig + digb;
   l.vr = ((dig_end > trb ? dig_end : trb) + 15u) & ~15u;
-  const uint32_t pre = l.vr + nkv4;
-  const uint32_t tile = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
-  l.ra = ((pre > tile ? pre : tile) + 15u) & ~15u;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;
-  l.scr = l.ra + 2u * l.row_pad;
+  l.rows = l.vr + nkv4;
+  l.scr = l.rows + 2u * l.row_pad;
   const uint32_t scr_floats =
       (uint32_t)(((sh.n_heads + sh.n_kv_heads + 3) & ~3) + 3 * sh.head_dim);
-  l.px = (l.scr + scr_floats * 4u + 15u) & ~15u;
+  const uint32_t scr_end = l.scr + scr_floats * 4u;
+  l.tb = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
+  const uint32_t bufs = 2u * l.tb;
+  l.px = ((scr_end > bufs ? scr_end : bufs) + 15u) & ~15u;
   l.total = l.px + (uint32_t)kWavesPerSplit * tiles_px_floats() * 4u;
   return l;
 }
@@ -115,7 +116,7 @@ template <int G, bool WQ>
 __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   constexpr int HD = kTilesHd, NB = HD / 32, KPW = kTilesKvPerWave, TP = kTileRows;
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ int32_t s_bcast, s_piece;
+  __shared__ int32_t s_bcast, s_pub[2];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -130,8 +131,8 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   float *vr = reinterpret_cast<float *>(lds + ll.vr);
   float *trq = reinterpret_cast<float *>(lds);  // the norm sums' transposed copy
   uint32_t *digs = reinterpret_cast<uint32_t *>(lds + ll.dig);
-  uint8_t *tk = lds, *tv = lds + (size_t)TP * lrow;  // the staged tile
-  uint8_t *rowk = lds + ll.ra, *rowv = rowk + ll.row_pad;
+  uint8_t *const buf0 = lds, *const buf1 = lds + ll.tb;  // the staged tiles
+  uint8_t *rowk = lds + ll.rows, *rowv = rowk + ll.row_pad;
   float *scr = reinterpret_cast<float *>(lds + ll.scr);
   float *px = reinterpret_cast<float *>(lds + ll.px) + (size_t)wave * tiles_px_floats();
   float *pfac = px + KPW * NB * TP * 4;  // [kv][head] rescale factors
@@ -184,8 +185,9 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
         }
       }
     };
-    auto stash = [&](int n) {
+    auto stash = [&](uint8_t *buf, int n) {
       const uint32_t np = (uint32_t)n * row / 16u;
+      uint8_t *tk = buf, *tv = buf + (size_t)TP * lrow;
 #pragma unroll
       for (int i = 0; i < kTileLoads; i++) {
         const uint32_t pc = (uint32_t)(kThreads * i + tid);
@@ -348,59 +350,105 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
+    // The owner's new row first: it sits in the setup's scratch, which the
+    // tiles overwrite.
+    if (owns_new) consume(rowk, rowv, 1, row);
+
+    // Two tile buffers: while the waves consume one, each thread writes its
+    // share of the next tile (loaded into registers one tile earlier) into
+    // the other and issues the loads of the tile after; one workgroup barrier
+    // per tile then both publishes the next tile and frees the current one.
+    int cn = 0;  // rows of the staged tile (0: none)
     if constexpr (!WQ) {
-      for (int ts = t0; ts < tend;) {
-        const int n = min(TP, tend - ts);
-        __syncthreads();  // the previous tile (or the setup's scratch) is no longer read
-        stash(n);
+      // (the first tile's loads were issued before the setup)
+      __syncthreads();  // every wave holds its operands and took the new row
+      int ts = t0;
+      if (ts < tend) {
+        cn = min(TP, tend - ts);
+        stash(buf0, cn);
+        if (ts + TP < tend) issue(ts + TP, min(TP, tend - ts - TP));
+      }
+      __syncthreads();
+      for (int i = 0; cn > 0; i++) {
+        uint8_t *cur = (i & 1) ? buf1 : buf0, *nxt = (i & 1) ? buf0 : buf1;
+        consume(cur, cur + (size_t)TP * lrow, cn, lrow);
+        ts += TP;
+        cn = ts < tend ? min(TP, tend - ts) : 0;
+        if (cn > 0) {
+          stash(nxt, cn);
+          if (ts + TP < tend) issue(ts + TP, min(TP, tend - ts - TP));
+        }
         __syncthreads();
-        const int ns = ts + TP;
-        if (ns < tend) issue(ns, min(TP, tend - ns));
-        consume(tk, tv, n, lrow);
-        ts = ns;
       }
     } else {
-      // Pieces of [0, tend) claimed per workgroup from ctr[0]; thread 0
-      // keeps one claim in flight and publishes it at the piece switch.
-      // (the first claim travels in s_bcast, which the unit loop does not
-      // touch during a visit, so thread 0 may write s_piece in the first
-      // trip while others still read it)
+      // Pieces of [0, tend) claimed per workgroup from ctr[0].  Thread 0
+      // keeps one claim ahead: when a piece starts (its first tile is
+      // issued) it publishes the claim it holds in s_pub[k & 1] (k: the
+      // piece's index in this visit) and claims again; the waves read that
+      // slot when piece k runs out, at least one barrier later, and it is
+      // written again only when piece k + 2 starts, a barrier after they
+      // all read it.  (The first claim travels in s_bcast, which the unit
+      // loop does not touch during a visit.)
       const PieceMap pm = piece_map(tend, P.piece_big, P.piece_len);
       int32_t pn = 0;
       if (tid == 0) {
         s_bcast = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-      __syncthreads();
-      int pc = __builtin_amdgcn_readfirstlane(s_bcast);
-      int ts = 0, pe = 0;
-      if (pc < pm.npieces) {
-        piece_range(pm, pc, tend, ts, pe);
-        issue(ts, min(TP, pe - ts));
-      }
-      while (pc < pm.npieces) {
-        const int n = min(TP, pe - ts);
-        const bool last = ts + TP >= pe;  // last tile of the piece
-        if (last && tid == 0) {
-          s_piece = pn;
+      __syncthreads();  // the claim; every wave holds its operands and took the new row
+      int k = 0, nx = 0, pe = 0;  // the piece being issued, its next tile, its end
+      bool live = false;          // a piece is being issued
+      auto start_piece = [&](int pc) {
+        piece_range(pm, pc, tend, nx, pe);
+        if (tid == 0) {
+          s_pub[k & 1] = pn;
           pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __syncthreads();  // the previous tile is no longer read; s_piece is published
-        stash(n);
-        int ns = ts + TP, npe = pe, npc = pc;
-        if (last) {
-          npc = s_piece;
-          if (npc < pm.npieces) piece_range(pm, npc, tend, ns, npe);
+        live = true;
+      };
+      // the next tile to issue (ts, n rows), or n = 0 when the pieces ran out
+      auto next_tile = [&](int &ts, int &n) {
+        if (live && nx >= pe) {
+          const int npc = __builtin_amdgcn_readfirstlane(s_pub[k & 1]);
+          k++;
+          live = false;
+          if (npc < pm.npieces) start_piece(npc);
+        }
+        if (!live) {
+          n = 0;
+          return;
+        }
+        ts = nx;
+        n = min(TP, pe - nx);
+        nx += n;
+      };
+      const int pc0 = __builtin_amdgcn_readfirstlane(s_bcast);
+      int its = 0, in = 0;  // the tile in registers
+      if (pc0 < pm.npieces) {
+        start_piece(pc0);
+        next_tile(its, in);
+        issue(its, in);
+      }
+      __syncthreads();  // the first piece's successor is published
+      if (in > 0) {
+        cn = in;
+        stash(buf0, cn);
+        next_tile(its, in);
+        if (in > 0) issue(its, in);
+      }
+      __syncthreads();
+      for (int i = 0; cn > 0; i++) {
+        uint8_t *cur = (i & 1) ? buf1 : buf0, *nxt = (i & 1) ? buf0 : buf1;
+        consume(cur, cur + (size_t)TP * lrow, cn, lrow);
+        cn = in;
+        if (cn > 0) {
+          stash(nxt, cn);
+          next_tile(its, in);
+          if (in > 0) issue(its, in);
         }
         __syncthreads();
-        if (npc < pm.npieces) issue(ns, min(TP, npe - ns));
-        consume(tk, tv, n, lrow);
-        pc = npc;
-        ts = ns;
-        pe = npe;
       }
     }
-    if (owns_new) consume(rowk, rowv, 1, row);
 
     // The partials (or the output) of the wave's heads: the sums of each
     // head's 16 lanes; m is already shared by them.
