@@ -112,6 +112,9 @@ struct DecodeParams {
   int32_t *wq;
   int32_t wq_set, wq_cap, wq_zero_units;
   int32_t wq_grid;      // workgroups of the launch
+  // wq_grid entries: the first unit of each workgroup (null: workgroup g
+  // starts at unit g % n_units).  Every unit is some workgroup's first.
+  const int32_t *home;
   int32_t piece_len;    // positions per small claimed piece (a multiple of stage_rows)
   int32_t piece_big;    // positions per big piece (a multiple of piece_len)
   int32_t n_layers_call;

@@ -23,6 +23,9 @@
 /* k_short's span counters: one int32 per (layer of a call, sequence, KV
  * head), at least this many. */
 #define G2B_SPAN_CTR_MIN 1024u
+/* Work-queue home units: one int32 per workgroup of a launch, at most this
+ * many (the resident workgroups of a device: 256 CUs x 8 workgroups, twice). */
+#define G2B_HOME_ENTRIES 4096u
 /* What one device allocation may take beyond its size (hipMalloc rounds
  * allocations up to pages; 2 MiB covers every size class). */
 #define G2B_ALLOC_GRAIN (2u << 20)

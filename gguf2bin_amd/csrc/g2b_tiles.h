@@ -500,7 +500,8 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   } else {
     const int n_units = P.n_seq * P.n_layers_call;
     int32_t *const wq = P.wq + (size_t)P.wq_set * (size_t)P.wq_cap * kWqStride;
-    int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x % (unsigned)n_units));
+    int unit = __builtin_amdgcn_readfirstlane(
+        P.home ? P.home[blockIdx.x] : (int)(blockIdx.x % (unsigned)n_units));
     uint32_t probe = blockIdx.x * 2654435761u;
     int32_t *const fresh = wq + (size_t)n_units * kWqStride;
     bool fresh_left = (int)gridDim.x < n_units;

@@ -55,6 +55,7 @@ static uint64_t grain(uint64_t b) {
  *   batch descriptors: max(n_seq, 64) of them;
  *   QK-RMSNorm weights and flags: n_layers x (2*head_dim + 1) words;
  *   the spanned short kernel's counters: n_layers x n_seq x n_kv_heads words;
+ *   the work queue's home units: G2B_HOME_ENTRIES words;
  *   the host entry point's staging: nq + 2*nkv + n_heads*ctx floats. */
 static uint64_t ctx_bytes(const g2b_shape *s, int32_t ctx, int32_t n_seq) {
   const uint64_t L = (uint64_t)s->n_layers, nh = (uint64_t)s->n_heads;
@@ -73,6 +74,7 @@ static uint64_t ctx_bytes(const g2b_shape *s, int32_t ctx, int32_t n_seq) {
          grain(2u * wq_lines * G2B_WQ_LINE_BYTES) +
          grain(descs * G2B_SEQ_DESC_BYTES) +
          grain(L * 2u * hd * 4u) + grain(L * 4u) + grain(span_ctrs * 4u) +
+         grain((uint64_t)G2B_HOME_ENTRIES * 4u) +
          grain((nq + 2u * nkv + nh * (uint64_t)ctx) * 4u);
 }
 
