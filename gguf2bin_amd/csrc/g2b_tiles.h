@@ -259,7 +259,11 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
 #pragma unroll
       for (int kk = 0; kk < KPW; kk++) {
         const int kvg = wave * KPW + kk;
-        float sc = 0.f;
+        // the KV head's four blocks: operands first, then the MFMAs in pairs
+        // into separate accumulators (so they issue back to back), then the
+        // sums in block order
+        uint64_t bop[NB];
+        float ks[NB];
 #pragma unroll
         for (int b = 0; b < NB; b++) {
           const uint32_t blk = (uint32_t)(kvg * NB + b);
@@ -267,15 +271,26 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
           const uint32_t *w = reinterpret_cast<const uint32_t *>(krow + (off & ~3u));
           const uint32_t sel = (off & 2u) ? 0x05040302u : 0x03020100u;
           const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
-          const uint64_t bop = (uint64_t)__builtin_amdgcn_perm(w1, w0, sel) |
-                               ((uint64_t)__builtin_amdgcn_perm(w2, w1, sel) << 32);
-          const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-              (long)qa[kk][b], (long)bop, i32x4{0, 0, 0, 0}, 0, 0, 0);
+          bop[b] = (uint64_t)__builtin_amdgcn_perm(w1, w0, sel) |
+                   ((uint64_t)__builtin_amdgcn_perm(w2, w1, sel) << 32);
           const uint32_t sw = *reinterpret_cast<const uint32_t *>(krow + ((34u * blk) & ~3u));
-          const float ks = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
-          // |c2| <= 32*128*127, so c2*256 + c1 fits in int32
-          const float part = fmaf((float)(c[2] * 256 + c[1]), 256.f, (float)c[0]);
-          sc = fmaf(part, ks * un[kk][b], sc);
+          ks[b] = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
+        }
+        float sc = 0.f;
+#pragma unroll
+        for (int b0 = 0; b0 < NB; b0 += 2) {
+          // two at a time (four accumulators would cost the second wave per SIMD)
+          i32x4 c[2];
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+            c[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)qa[kk][b0 + j], (long)bop[b0 + j],
+                                                         i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            // |c2| <= 32*128*127, so c2*256 + c1 fits in int32
+            const float part = fmaf((float)(c[j][2] * 256 + c[j][1]), 256.f, (float)c[j][0]);
+            sc = fmaf(part, ks[b0 + j] * un[kk][b0 + j], sc);
+          }
         }
         s[kk] = valid ? sc : -INFINITY;
       }
