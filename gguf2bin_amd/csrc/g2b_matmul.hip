@@ -31,6 +31,7 @@ constexpr int kGemvUnroll = 4;  // steps whose loads are in flight together
 constexpr int kGemvGroup = 8;   // blocks per lane in flight (x in LDS or the cache)
 constexpr int kGemvMinSteps = 8;            // wave-steps per wave, where there are enough
 constexpr int kGemvMaxXLds = 64 * 1024;     // x staged in LDS up to this many bytes
+constexpr int kGemvMmaMinRows = 32768;      // k_gemv_mma for Q4_0 matrices of this many rows
 
 template <typename T>
 __device__ __forceinline__ T nt_load(const void *p) {
@@ -341,6 +342,167 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
   }
 }
 
+// Q8_0 / Q4_0 rows of nb = 16 * BPL blocks (BPL even) on the int8 matrix
+// cores, for the plain product (no prologue, one segment); dispatched for
+// Q4_0 with 1024-element rows (launch_gemv).  v_mfma_i32_4x4x4_16b_i8 computes,
+// in each of its 16 groups of four lanes, D[l][i] += dot4(A[4*(l/4) + i],
+// B[l]) (the lane layout checked on the device): lane l = 4*g + r takes row
+// r of the wave-step's four rows and blocks g*BPL .. g*BPL + BPL - 1 of it,
+// so the four lanes of a group read the same block of four rows; B lane l =
+// four of its row's quants, A lane 4*g + i = digit plane i of the same four
+// elements of x.  x is held as four signed int8 digit planes of a 31-bit
+// fixed point relative to each block's largest |x| (m = rint(x * 2^(30-e)),
+// 2^(e-1) <= max|x| < 2^e; m = d0 + 256 d1 + 65536 d2 + 2^24 d3), so the
+// eight MFMAs of a block give exact int32 plane sums; the block's sum is
+// ((D3*256 + D2)*256 + D1)*256 + D0 in fp32, times the block's fp16 scale
+// and 2^(e-30), and the lane's blocks and then the row's 16 lanes are summed
+// in fp32.  x's rounding (2^-31 of its block maximum) is far below fp32's, so
+// outlier channels cost nothing.  Q4_0 quants go in as their nibbles (0..15)
+// with the -8 folded in as 8 x the block's digit sums.  Against the VALU path
+// (a convert and an FMA per weight) this is ~0.5 VALU operations per weight.
+template <int FMT, int BPL>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
+  extern __shared__ float xs[];  // the digit planes of x
+  constexpr int BB = FMT == 1 ? 34 : 18;
+  constexpr int NB = 16 * BPL;
+  constexpr int NW = BPL * BB / 4;  // dwords of a lane's span (BPL even)
+  // wave-steps in flight: about 72 registers of weights
+  constexpr int UN = 72 / NW >= kGemvUnroll ? kGemvUnroll : (72 / NW >= 1 ? 72 / NW : 1);
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+  const int r = lane & 3, g = lane >> 2;
+  // LDS: digit planes [block][plane][chunk] (a dword = one plane of four
+  // elements), per block 1 (or NaN) and its exponent e, and the blocks'
+  // per-plane digit sums
+  uint32_t *dig = reinterpret_cast<uint32_t *>(xs);
+  float *units = reinterpret_cast<float *>(dig + NB * 32);
+  int32_t *exps = reinterpret_cast<int32_t *>(units + NB);
+  int32_t *dsum = exps + NB;
+  const int stride = P.n_waves;
+  for (int s0 = gw, trip = 0;; s0 += stride * UN, trip++) {
+    // this trip's spans: UN wave-steps of four rows, each lane its row's
+    // BPL blocks (dword loads; a row's 16 lanes cover it, so its lines are
+    // fetched once and shared through the cache)
+    uint32_t wvs[UN][NW];
+    int row[UN];
+    bool ok[UN];
+#pragma unroll
+    for (int u = 0; u < UN; u++) {
+      const int st = s0 + u * stride;
+      row[u] = st * 4 + r;
+      ok[u] = st < P.steps && row[u] < P.d;
+      const uint32_t *src =
+          reinterpret_cast<const uint32_t *>(P.w + (size_t)(ok[u] ? row[u] : 0) * P.row_bytes +
+                                             g * (BPL * BB));
+#pragma unroll
+      for (int i = 0; i < NW; i++) wvs[u][i] = ok[u] ? src[i] : 0u;
+    }
+    if (trip == 0) {
+      // x into digit planes, while the weights load
+      for (int it = threadIdx.x; it < NB * 8; it += kGemvThreads) {
+        const int b = it >> 3, j = it & 7;  // chunk j: elements 4j .. 4j+3
+        const float4 v = *reinterpret_cast<const float4 *>(P.x + 32 * b + 4 * j);
+        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        mx = fmaxf(mx, __shfl_xor(mx, 1));
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = fmaxf(mx, __shfl_xor(mx, 4));
+        int e = 0;
+        (void)frexpf(mx, &e);
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        uint32_t pl[4] = {0u, 0u, 0u, 0u};
+        int ps[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          int m = (int)rintf(ldexpf(xv[k], 30 - e));  // |m| <= 2^30, exact scaling
+          int d[4];
+#pragma unroll
+          for (int q = 0; q < 3; q++) {
+            d[q] = ((m + 128) & 255) - 128;
+            m = (m - d[q]) >> 8;
+          }
+          d[3] = m;
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            pl[q] |= ((uint32_t)d[q] & 0xFFu) << (8 * k);
+            ps[q] += d[q];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          dig[(b * 4 + q) * 8 + j] = pl[q];
+          int t = ps[q];
+          t += __shfl_xor(t, 1);
+          t += __shfl_xor(t, 2);
+          t += __shfl_xor(t, 4);
+          ps[q] = t;
+        }
+        if (j == 0) {
+          // the block's exponent, and 1 (NaN for a non-finite x: the rows'
+          // sums then are NaN)
+          exps[b] = e;
+          units[b] = (mx <= 3.402823466e38f) ? 1.f : __int_as_float(0x7fc00000);
+#pragma unroll
+          for (int q = 0; q < 4; q++) dsum[b * 4 + q] = ps[q];
+        }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < UN; u++) {
+      const uint32_t *wv = wvs[u];
+      float acc = 0.f;
+#pragma unroll
+      for (int k = 0; k < BPL; k++) {
+        const int b = g * BPL + k;
+        const int o = k * BB;  // the block's first byte in the span (o + 2: quants)
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        v4i dd = {0, 0, 0, 0};
+        // quant word j of the block: bytes o + 2 + 4j .. (o is even)
+        auto qword = [&](int jw) -> uint32_t {
+          const int byte = o + 2 + 4 * jw;
+          const int wi = byte >> 2;
+          return (byte & 2) ? __builtin_amdgcn_perm(wv[wi + 1], wv[wi], 0x05040302u) : wv[wi];
+        };
+        // A: plane r of the block's eight chunks
+        const uint4 a03 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8);
+        const uint4 a47 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8 + 4);
+        const uint32_t av[8] = {a03.x, a03.y, a03.z, a03.w, a47.x, a47.y, a47.z, a47.w};
+        if constexpr (FMT == 1) {
+#pragma unroll
+          for (int jw = 0; jw < 8; jw++)
+            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)qword(jw), dd, 0, 0, 0);
+        } else {
+#pragma unroll
+          for (int jw = 0; jw < 4; jw++) {
+            const uint32_t w = qword(jw);
+            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)(w & 0x0F0F0F0Fu), dd, 0, 0,
+                                                   0);
+            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[4 + jw], (int)((w >> 4) & 0x0F0F0F0Fu),
+                                                   dd, 0, 0, 0);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; q++) dd[q] -= 8 * dsum[b * 4 + q];
+        }
+        // |D3| <= 32*128*64, so D3*256 + D2 fits in int32
+        const float t = (float)(dd[3] * 256 + dd[2]);
+        const float sum = fmaf(fmaf(t, 256.f, (float)dd[1]), 256.f, (float)dd[0]);
+        const uint32_t sw = wv[o >> 2];
+        const float scl = half_bits_to_f32_hw((o & 2) ? (sw >> 16) : (sw & 0xFFFFu));
+        // times the scale, then 2^(e-30) (ldexp: no overflow or early
+        // underflow for blocks of very large or very small x)
+        acc += ldexpf(sum * scl, exps[b] - 30) * units[b];
+      }
+      // the row's 16 lanes (lanes r, r + 4, ..., r + 60)
+      acc += __shfl_xor(acc, 4);
+      acc += __shfl_xor(acc, 8);
+      acc += __shfl_xor(acc, 16);
+      acc += __shfl_xor(acc, 32);
+      if (ok[u] && g == 0) P.out[row[u]] = acc;
+    }
+    if (s0 + stride * UN >= P.steps) break;
+  }
+}
+
 // Q8_0 / Q4_0 rows of more than 128 blocks: the workgroup's four waves
 // split each row's blocks in quarters (a quarter of at most 128 blocks, so
 // every lane keeps the x of its KB <= 2 blocks in registers) and add their
@@ -503,6 +665,22 @@ hipError_t launch_split_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t 
   return hipGetLastError();
 }
 
+// k_gemv_mma<2, 2> (Q4_0, 1024-element rows): resident workgroups per CU,
+// queried once.
+int occ_mma_q4(size_t lds) {
+  static int cached = 0;
+  if (cached <= 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_mma<2, 2>, kGemvThreads, lds) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    cached = std::max(1, n);
+  }
+  return cached;
+}
+
 template <int FMT>
 hipError_t launch_split(const GemvParams &p, int lpr, int kb, dim3 grid, hipStream_t s) {
   // a quarter of more than 128 blocks is more than 32: LPR is 64
@@ -564,6 +742,26 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
     p.n_waves = wgs * waves_per_wg;
     return fmt == 1 ? launch_split<1>(p, 64, kb, dim3(wgs), s)
                     : launch_split<2>(p, 64, kb, dim3(wgs), s);
+  }
+  // The int8 matrix cores (k_gemv_mma) where they pay: plain (unfused) Q4_0
+  // products of 1024-element rows, at least kGemvMmaMinRows of them (the lm
+  // head: 18.7 against 26.2 us), x 16-byte and the weights 4-byte aligned.  Measured slower
+  // elsewhere (its per-lane dword loads; same box): Q8_0 lm head 34.4 against
+  // 31.1 us, Q4_0 4096 x 14336 29.6 against 13.8 us, 4096-row matrices
+  // 4.7-5.0 against 4.4 us (the digit prologue of every workgroup); a variant
+  // staging four rows per wave through LDS with 16-byte loads was slower still.
+  if (fmt == 2 && !fused && p.x_vec4 && p.nb == 32 && p.d >= kGemvMmaMinRows &&
+      ((uintptr_t)p.w & 3u) == 0) {
+    p.steps = (p.d + 3) / 4;
+    const size_t lds = (size_t)p.nb * (32u * 4u + 4u + 4u + 16u);
+    const int occ = occ_mma_q4(lds);
+    const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
+                                        std::min(p.steps, n_cu * 4)),
+                               n_cu * std::max(1, occ) * waves_per_wg);
+    const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
+    p.n_waves = wgs * waves_per_wg;
+    hipLaunchKernelGGL((k_gemv_mma<2, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    return hipGetLastError();
   }
   int lpr = 1;
   while (lpr < p.nb && lpr < 64) lpr *= 2;

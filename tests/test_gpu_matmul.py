@@ -122,3 +122,37 @@ def test_matmul_lm_head_full_size(gpu_device, t):
         finally:
             ctx.weights_free(wd)
     check(out, x, w, t, n, d, "lm head")
+
+
+@pytest.mark.parametrize("case", ["normal", "outlier", "zero_blocks", "tiny", "huge"])
+def test_q4_matrix_core_path(gpu_device, case):
+    """Plain Q4_0 products of 1024-element rows with at least 32768 rows run
+    on the int8 matrix cores (x as four int8 digit planes of a 31-bit fixed
+    point per block): the same bar as every GEMV, with x that stresses the
+    digits - one channel 3e4 x the others, whole blocks of zeros, x near the
+    bottom of the normal range (1e-36) and near the top (1e35)."""
+    n, d, t = 1024, 40000, orc.T_Q4_0
+    rng = np.random.default_rng(4321)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    if case == "outlier":
+        x[37] = np.float32(3e4)
+    elif case == "zero_blocks":
+        x[64:160] = 0
+        x[1000:] = 0
+    elif case == "tiny":
+        x = (x * np.float32(1e-36)).astype(np.float32)
+    elif case == "huge":
+        x = (x * np.float32(1e30)).astype(np.float32)
+    print(f"[gemv] q4 matrix cores {case}", flush=True)
+    with attn.Context(SHAPE) as ctx:
+        wd = ctx.weights_upload(w)
+        try:
+            xd = hip.to_device(x)
+            od = hip.DeviceBuffer(d * 4)
+            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+            ctx.sync()
+            out = od.download(np.float32, d)
+        finally:
+            ctx.weights_free(wd)
+    check(out, x, w, t, n, d, f"q4 matrix cores {case}")
