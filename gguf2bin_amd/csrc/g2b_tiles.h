@@ -24,18 +24,23 @@
 // p * v_scale for its block from a per-wave LDS exchange and does 4 x G FMAs
 // per position.
 //
-// Streaming: a workgroup stages tiles of 16 positions - the K and V rows of
-// 16 consecutive positions are two contiguous runs of 16 x row bytes - with
-// coalesced non-temporal 16-byte loads, the next tile's loads in registers
-// while the current tile is consumed from LDS.  In LDS each row is padded by
-// 16 bytes: at the plain 1088-byte stride the 16 positions' operand reads
-// all fell on 2 of 32 banks (an 8-way conflict that made LDS the bound).
+// Streaming: a workgroup streams tiles of 16 positions - the K and V rows of
+// 16 consecutive positions are two contiguous runs of 16 x 1088 bytes - from
+// HBM straight into one of two LDS tile buffers (buffer_load_dwordx4 ... lds,
+// non-temporal, 36 loads of 1 KiB per tile, nine per wave): tile i+1 is
+// issued into the other buffer right after the workgroup barrier that opens
+// tile i and lands while tile i is consumed.  In LDS each 1088-byte row is
+// padded to 1104 bytes (a 16-byte slot no load writes): at the plain stride
+// the 16 positions' operand reads all fell on 2 of 32 banks (an 8-way
+// conflict that made LDS the bound).
 // Each wave owns two KV heads of every tile, so the waves of a workgroup
 // never merge states: each writes the partials (or, with one split, the
 // output) of its own heads.
 //
 // Schedules are k_layer's: static splits (workgroup = split x sequence x
-// layer) or the work queue (pieces of a unit claimed per workgroup).  The
+// layer) or the work queue (pieces of a unit claimed per workgroup by wave 0,
+// which hands each tile's first row and row count to the waves through LDS
+// one tile ahead).  The
 // setup (QK-RMSNorm, RoPE, digit planes, the owner's append) is k_layer's
 // visit_setup; the owner consumes its new row from LDS.
 #pragma once
@@ -46,28 +51,43 @@ namespace g2b {
 constexpr int kTileRows = kTilesRows;  // positions per tile (the MFMA's 16 columns)
 constexpr int kTilesKvPerWave = 2;
 constexpr int kTilesHd = 128;
+// A tile tensor (16 K or V rows) in LDS: rows of 68 16-byte slots of data
+// and one of padding.
+constexpr int kTilesRowSlots = 69;
+constexpr uint32_t kTilesLdsRow = 16u * kTilesRowSlots;
+constexpr int kTilesSlots = kTileRows * kTilesRowSlots;   // per tensor
+constexpr int kTilesLoadsT = (kTilesSlots + 63) / 64;     // 1 KiB loads per tensor
+constexpr int kTilesLoads = 2 * kTilesLoadsT;             // per tile
+constexpr int kTilesWaveLoads = kTilesLoads / kWavesPerSplit;  // wave w: loads w, w + 4, ...
+static_assert(kTilesLoads % kWavesPerSplit == 0, "the same loads per wave");
+constexpr uint32_t kTilesTensorBytes = (uint32_t)kTilesSlots * 16u;
+constexpr uint32_t kTilesTileBytes = 2u * kTilesTensorBytes;
 
 // Shapes k_tiles serves.
 __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
   if (!sh.kv_q8 || sh.head_dim != kTilesHd) return false;
   if (sh.n_kv_heads != kWavesPerSplit * kTilesKvPerWave) return false;
+  if (sh.row_bytes != 16u * (kTilesRowSlots - 1)) return false;
   if (sh.n_heads % sh.n_kv_heads) return false;
   const int g = sh.n_heads / sh.n_kv_heads;
   return g >= 3 && g <= 4;
 }
 
-// k_tiles' dynamic LDS: two tile buffers (each the K rows, then the V rows,
-// of 16 positions at a padded stride), then each wave's exchange of
-// p * v_scale ([kv][block][position][head]) and rescale factors ([kv][head]).
-// The setup's scratch lies over the tile buffers: rotated q at 0, the new k
-// after it, the digit planes after that and the new v, then the new K and V
-// rows and the norm factors; the transposed copy for the QK-RMSNorm sums lies
-// over q, k and the digit planes, which are written only after the sums (the
-// v copy is written before them, so it stays clear).  The new rows are
-// consumed before the first tile is staged.  ~77 KB for Llama-3-8B's heads:
-// two workgroups per CU, as the registers allow.
+// k_tiles' dynamic LDS: tile buffer 0, each wave's exchange of p * v_scale
+// ([kv][block][position][head]) and rescale factors ([kv][head]), tile
+// buffer 1.  The setup's scratch starts at the exchange and lies over it and
+// buffer 1 (never over buffer 0, whose loads the static schedule issues
+// before the setup): rotated q at 0, the new k after it, the digit planes
+// after that and the new v, then the new K and V rows and the norm factors;
+// the transposed copy for the QK-RMSNorm sums lies over q, k and the digit
+// planes, which are written only after the sums (the v copy is written before
+// them, so it stays clear).  The exchange overlaps only q and k, dead by the
+// time the owner consumes its new row; buffer 1 is loaded after a barrier
+// that follows that.  ~77 KiB for Llama-3-8B's heads: two workgroups per CU.
 struct TilesLds {
-  uint32_t kr, dig, vr, rows, row_pad, scr, tb, px, total;
+  uint32_t scr0;                              // the setup scratch (absolute)
+  uint32_t kr, dig, vr, rows, row_pad, scr;  // (relative to scr0)
+  uint32_t px, buf1, total;                   // (absolute)
 };
 __host__ __device__ inline uint32_t tiles_px_floats() {
   return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTileRows * 4 + kTilesKvPerWave * 4);
@@ -88,10 +108,11 @@ __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   const uint32_t scr_floats =
       (uint32_t)(((sh.n_heads + sh.n_kv_heads + 3) & ~3) + 3 * sh.head_dim);
   const uint32_t scr_end = l.scr + scr_floats * 4u;
-  l.tb = 2u * (uint32_t)kTileRows * (sh.row_bytes + 16u);
-  const uint32_t bufs = 2u * l.tb;
-  l.px = ((scr_end > bufs ? scr_end : bufs) + 15u) & ~15u;
-  l.total = l.px + (uint32_t)kWavesPerSplit * tiles_px_floats() * 4u;
+  l.px = kTilesTileBytes;
+  l.scr0 = l.px;
+  l.buf1 = l.px + (uint32_t)kWavesPerSplit * tiles_px_floats() * 4u;
+  const uint32_t end = l.buf1 + kTilesTileBytes;
+  l.total = end > l.scr0 + scr_end ? end : ((l.scr0 + scr_end + 15u) & ~15u);
   return l;
 }
 
@@ -107,16 +128,69 @@ __device__ __forceinline__ float group_max(float x) {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
-// Staged tile loads per thread and tensor (a tile of 16 rows of up to 1088
-// bytes is at most 1088 16-byte pieces over 256 threads).
-constexpr int kTileLoads = 5;
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family devices: data
+// format 32 bits, the rest zero (untyped loads move the bytes as they are;
+// the range check is offset < the resource's byte count).
+constexpr int32_t kBufferRsrcWord3 = 0x00020000;
+
+// The tile loads and the work-queue claims are issued through inline
+// assembly, so that the compiler's wait-count bookkeeping does not see them:
+// the compiler waits for every LDS DMA before any LDS read (which would
+// serialise each tile's loads with the consumption of the one before), and
+// loads or claims issued on some loop paths and not others made it wait for
+// everything (vmcnt(0)) inside the consume phase.  The kernel waits for them
+// itself: one s_waitcnt vmcnt(0) per tile, before the barrier that opens it.
+//
+// 16 bytes per lane from buffer resource rsrc at byte voff into LDS at
+// lds_addr + 16 * lane, non-temporal (M0 holds the LDS address).
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+// Lane 0 adds 1 to *ctr (agent scope: global_atomic_add ... sc0, as the
+// compiler issues a relaxed agent-scope fetch_add) and finds the old value in
+// its lane of the result once the atomic completes: the caller reads it
+// (readlane 0) only after an s_waitcnt that covers it.  The other lanes are
+// masked off inside the statement.
+__device__ __forceinline__ int32_t claim_lane0(int32_t *ctr) {
+  int32_t r;
+  uint64_t save;
+  asm volatile(
+      "s_mov_b64 %1, exec\n\t"
+      "s_mov_b64 exec, 1\n\t"
+      "global_atomic_add %0, %2, %3, off sc0\n\t"
+      "s_mov_b64 exec, %1"
+      : "=&v"(r), "=&s"(save)
+      : "v"(ctr), "v"(1)
+      : "memory");
+  return r;
+}
+// The raw buffer resource of `bytes` bytes at p (p the same in every lane).
+__device__ __forceinline__ i32x4 raw_rsrc(const uint8_t *p, uint32_t bytes) {
+  const uint64_t u = (uint64_t)(uintptr_t)p;
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32)) & 0xFFFF;
+  r.z = (int)bytes;
+  r.w = kBufferRsrcWord3;
+  return r;
+}
+// The LDS address of p (a pointer into __shared__ memory).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// Every vector memory operation of this wave has completed.
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // G: q heads per KV head (3 or 4).  WQ: work-queue schedule.
 template <int G, bool WQ>
 __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   constexpr int HD = kTilesHd, NB = HD / 32, KPW = kTilesKvPerWave, TP = kTileRows;
   extern __shared__ __align__(16) uint8_t lds[];
-  __shared__ int32_t s_bcast, s_pub[2];
+  __shared__ int32_t s_bcast;
+  __shared__ int32_t s_desc[2][2];  // work queue: tile t's (first row, rows) at [t & 1]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -124,36 +198,33 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   const int nkv = P.sh.n_kv_heads * HD;
   const size_t nq = (size_t)n_heads * HD;
   const uint32_t row = P.sh.row_bytes;
-  const uint32_t lrow = row + 16u;  // LDS row stride of the staged tile
   const TilesLds ll = tiles_lds_layout(P.sh);
-  float *qrot = reinterpret_cast<float *>(lds);
-  float *kr = reinterpret_cast<float *>(lds + ll.kr);
-  float *vr = reinterpret_cast<float *>(lds + ll.vr);
-  float *trq = reinterpret_cast<float *>(lds);  // the norm sums' transposed copy
-  uint32_t *digs = reinterpret_cast<uint32_t *>(lds + ll.dig);
-  uint8_t *const buf0 = lds, *const buf1 = lds + ll.tb;  // the staged tiles
-  uint8_t *rowk = lds + ll.rows, *rowv = rowk + ll.row_pad;
-  float *scr = reinterpret_cast<float *>(lds + ll.scr);
+  uint8_t *const sb = lds + ll.scr0;
+  float *qrot = reinterpret_cast<float *>(sb);
+  float *kr = reinterpret_cast<float *>(sb + ll.kr);
+  float *vr = reinterpret_cast<float *>(sb + ll.vr);
+  float *trq = reinterpret_cast<float *>(sb);  // the norm sums' transposed copy
+  uint32_t *digs = reinterpret_cast<uint32_t *>(sb + ll.dig);
+  uint8_t *rowk = sb + ll.rows, *rowv = rowk + ll.row_pad;
+  float *scr = reinterpret_cast<float *>(sb + ll.scr);
   float *px = reinterpret_cast<float *>(lds + ll.px) + (size_t)wave * tiles_px_floats();
   float *pfac = px + KPW * NB * TP * 4;  // [kv][head] rescale factors
+  auto buf = [&](int k) { return lds + (k ? ll.buf1 : 0u); };
 
-  // LDS offsets of this thread's staged pieces tid, tid + 256, ... (piece p
-  // of a run is row p / (row/16), bytes 16 * (p % (row/16)) of it)
-  uint32_t soff[kTileLoads];
-  {
-    const uint32_t ppr = row / 16u;
-    uint32_t r = (uint32_t)tid / ppr, w = (uint32_t)tid % ppr;
-    const uint32_t dr = (uint32_t)kThreads / ppr, dw = (uint32_t)kThreads % ppr;
+  // This wave's tile loads u: load j = wave + 4u of the tile, tensor j / 18
+  // (K, V), slots 64 (j % 18) + lane of it; slot s is row s / 69, bytes
+  // 16 (s % 69) of it, and slot 68 of a row is padding (lane off).
+  // Loop-invariant registers: a load's offset register must not be
+  // rewritten while the load is in flight.
+  uint32_t goff[kTilesWaveLoads];
+  uint32_t gon = 0u;  // bit u: this lane takes part in load u
 #pragma unroll
-    for (int i = 0; i < kTileLoads; i++) {
-      soff[i] = r * lrow + 16u * w;
-      r += dr;
-      w += dw;
-      if (w >= ppr) {
-        w -= ppr;
-        r += 1;
-      }
-    }
+  for (int u = 0; u < kTilesWaveLoads; u++) {
+    const int j = wave + kWavesPerSplit * u;
+    const int sl = 64 * (j % kTilesLoadsT) + lane;
+    const int r = sl / kTilesRowSlots, c = sl - r * kTilesRowSlots;
+    goff[u] = (uint32_t)r * row + 16u * (uint32_t)c;
+    if (sl < kTilesSlots && c < kTilesRowSlots - 1) gon |= 1u << u;
   }
 
   // lane roles: MFMA row / column (A row, B and C column = position) and
@@ -164,41 +235,42 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
 
   auto visit = [&](const SeqDev &sd, int seq, int li, int t0, int tend, bool owns_new,
                    int pslot, int32_t *ctr) {
+    // (the workgroup's positions: scalar registers)
+    t0 = __builtin_amdgcn_readfirstlane(t0);
+    tend = __builtin_amdgcn_readfirstlane(tend);
     const int layer = P.layer0 + li;
     const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
     const uint8_t *kb = sd.k + ((size_t)layer * (size_t)sd.ctx_cap) * row;
     const uint8_t *vb = sd.v + ((size_t)layer * (size_t)sd.ctx_cap) * row;
-    u32x4 rk[kTileLoads], rv[kTileLoads];
-    // loads of the tile of n rows at ts: thread tid takes pieces tid,
-    // tid + 256, ... of the K run and of the V run
-    auto issue = [&](int ts, int n) {
-      const uint32_t np = (uint32_t)n * row / 16u;
-      const uint8_t *gk = kb + (size_t)ts * row + 16u * (uint32_t)tid;
-      const uint8_t *gv = vb + (size_t)ts * row + 16u * (uint32_t)tid;
+    // This wave's loads of the tile of n rows at ts into buffer k.  Slots of
+    // rows at or past n load the run's first bytes instead (never read), so
+    // that every load keeps its lanes.
+    auto issue = [&](int k, int ts, int n) {
+      const size_t base = (size_t)ts * row;
+      const uint32_t span = (uint32_t)TP * row;
+      const i32x4 rk = raw_rsrc(kb + base, span), rv = raw_rsrc(vb + base, span);
+      const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr(buf(k)));
+      const uint32_t lim = (uint32_t)n * row;
 #pragma unroll
-      for (int i = 0; i < kTileLoads; i++) {
-        if ((uint32_t)(kThreads * i + tid) < np) {
-          rk[i] = __builtin_nontemporal_load(
-              (const __attribute__((address_space(1))) u32x4 *)(gk + 16u * kThreads * i));
-          rv[i] = __builtin_nontemporal_load(
-              (const __attribute__((address_space(1))) u32x4 *)(gv + 16u * kThreads * i));
-        }
+      for (int u = 0; u < kTilesWaveLoads; u++) {
+        const int j = wave + kWavesPerSplit * u;
+        const bool is_v = j >= kTilesLoadsT;
+        const uint32_t dst = la + (is_v ? kTilesTensorBytes : 0u) +
+                             1024u * (uint32_t)(is_v ? j - kTilesLoadsT : j);
+        if ((gon >> u) & 1u) dma16(is_v ? rv : rk, dst, goff[u] < lim ? goff[u] : 0u);
       }
     };
-    auto stash = [&](uint8_t *buf, int n) {
-      const uint32_t np = (uint32_t)n * row / 16u;
-      uint8_t *tk = buf, *tv = buf + (size_t)TP * lrow;
-#pragma unroll
-      for (int i = 0; i < kTileLoads; i++) {
-        const uint32_t pc = (uint32_t)(kThreads * i + tid);
-        if (pc < np) {
-          *reinterpret_cast<u32x4 *>(tk + soff[i]) = rk[i];
-          *reinterpret_cast<u32x4 *>(tv + soff[i]) = rv[i];
-        }
-      }
-    };
+    const int ntiles = t0 < tend ? (tend - t0 + TP - 1) / TP : 0;  // static schedule
+    auto static_rows = [&](int t) { return t < ntiles ? min(TP, tend - (t0 + TP * t)) : 0; };
     // Static schedule: the first tile is in flight during the setup.
-    if (!WQ && t0 < tend) issue(t0, min(TP, tend - t0));
+    if (!WQ && ntiles > 0) issue(0, t0, static_rows(0));
+    // Work queue: wave 0 claims the visit's first two pieces (first, pend),
+    // in flight during the setup.
+    int32_t first = 0, pend = 0;
+    if (WQ && wave == 0) {
+      first = claim_lane0(ctr);
+      pend = claim_lane0(ctr);
+    }
 
     // [QK-RMSNorm,] RoPE, the digit planes of q (32-element chunks = the
     // Q8_0 blocks) and the owner's append, all in LDS
@@ -358,111 +430,82 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       } else {
         for (int t = 0; t < nrows; t++) vstep(t);
       }
-      // (px is written again only after these reads: the next tile's K
-      // phase follows a workgroup barrier)
+      // (px is written again only after these reads: the wave's next K
+      // phase)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    // The owner's new row first: it sits in the setup's scratch, which the
-    // tiles overwrite.
-    if (owns_new) consume(rowk, rowv, 1, row);
-
-    // Two tile buffers: while the waves consume one, each thread writes its
-    // share of the next tile (loaded into registers one tile earlier) into
-    // the other and issues the loads of the tile after; one workgroup barrier
-    // per tile then both publishes the next tile and frees the current one.
-    int cn = 0;  // rows of the staged tile (0: none)
-    if constexpr (!WQ) {
-      // (the first tile's loads were issued before the setup)
-      __syncthreads();  // every wave holds its operands and took the new row
-      int ts = t0;
-      if (ts < tend) {
-        cn = min(TP, tend - ts);
-        stash(buf0, cn);
-        if (ts + TP < tend) issue(ts + TP, min(TP, tend - ts - TP));
-      }
-      __syncthreads();
-      for (int i = 0; cn > 0; i++) {
-        uint8_t *cur = (i & 1) ? buf1 : buf0, *nxt = (i & 1) ? buf0 : buf1;
-        consume(cur, cur + (size_t)TP * lrow, cn, lrow);
-        ts += TP;
-        cn = ts < tend ? min(TP, tend - ts) : 0;
-        if (cn > 0) {
-          stash(nxt, cn);
-          if (ts + TP < tend) issue(ts + TP, min(TP, tend - ts - TP));
-        }
-        __syncthreads();
-      }
-    } else {
-      // Pieces of [0, tend) claimed per workgroup from ctr[0].  Thread 0
-      // keeps one claim ahead: when a piece starts (its first tile is
-      // issued) it publishes the claim it holds in s_pub[k & 1] (k: the
-      // piece's index in this visit) and claims again; the waves read that
-      // slot when piece k runs out, at least one barrier later, and it is
-      // written again only when piece k + 2 starts, a barrier after they
-      // all read it.  (The first claim travels in s_bcast, which the unit
-      // loop does not touch during a visit.)
-      const PieceMap pm = piece_map(tend, P.piece_big, P.piece_len);
-      int32_t pn = 0;
-      if (tid == 0) {
-        s_bcast = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __syncthreads();  // the claim; every wave holds its operands and took the new row
-      int k = 0, nx = 0, pe = 0;  // the piece being issued, its next tile, its end
-      bool live = false;          // a piece is being issued
-      auto start_piece = [&](int pc) {
+    // Work queue: wave 0 turns claimed pieces of [0, tend) into tiles, one
+    // tile ahead of the issue.  A claim is issued when a piece starts and
+    // read when it runs out, at a later tile: after the wait for all of the
+    // wave's loads that opens every tile.
+    const PieceMap pm = piece_map(WQ ? tend : 0, P.piece_big, P.piece_len);
+    int nx = 0, pe = 0;  // the piece being cut: next row, end
+    bool live = false;
+    auto take_piece = [&](int pc) {
+      live = pc >= 0 && pc < pm.npieces;
+      if (live) {
         piece_range(pm, pc, tend, nx, pe);
-        if (tid == 0) {
-          s_pub[k & 1] = pn;
-          pn = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        live = true;
-      };
-      // the next tile to issue (ts, n rows), or n = 0 when the pieces ran out
-      auto next_tile = [&](int &ts, int &n) {
-        if (live && nx >= pe) {
-          const int npc = __builtin_amdgcn_readfirstlane(s_pub[k & 1]);
-          k++;
-          live = false;
-          if (npc < pm.npieces) start_piece(npc);
-        }
-        if (!live) {
-          n = 0;
-          return;
-        }
+        nx = __builtin_amdgcn_readfirstlane(nx);
+        pe = __builtin_amdgcn_readfirstlane(pe);
+      }
+    };
+    auto publish = [&](int t) {  // (wave 0) tile t's descriptor, for all
+      if (live && nx >= pe) {
+        take_piece(__builtin_amdgcn_readlane(pend, 0));
+        if (live) pend = claim_lane0(ctr);
+      }
+      int ts = 0, n = 0;
+      if (live) {
         ts = nx;
-        n = min(TP, pe - nx);
+        n = __builtin_amdgcn_readfirstlane(min(TP, pe - nx));
         nx += n;
-      };
-      const int pc0 = __builtin_amdgcn_readfirstlane(s_bcast);
-      int its = 0, in = 0;  // the tile in registers
-      if (pc0 < pm.npieces) {
-        start_piece(pc0);
-        next_tile(its, in);
-        issue(its, in);
       }
-      __syncthreads();  // the first piece's successor is published
-      if (in > 0) {
-        cn = in;
-        stash(buf0, cn);
-        next_tile(its, in);
-        if (in > 0) issue(its, in);
+      if (lane == 0) {
+        s_desc[t & 1][0] = ts;
+        s_desc[t & 1][1] = n;
       }
+    };
+    auto desc = [&](int t, int &ts, int &n) {
+      if constexpr (WQ) {
+        ts = __builtin_amdgcn_readfirstlane(s_desc[t & 1][0]);
+        n = __builtin_amdgcn_readfirstlane(s_desc[t & 1][1]);
+      } else {
+        ts = __builtin_amdgcn_readfirstlane(t0 + TP * t);
+        n = __builtin_amdgcn_readfirstlane(static_rows(t));
+      }
+    };
+    if constexpr (WQ) {
+      if (wave == 0) {
+        wait_vm0();  // the first two claims (nothing else of this wave is in flight)
+        take_piece(__builtin_amdgcn_readlane(first, 0));
+        publish(0);
+        publish(1);
+      }
+    }
+
+    // The owner's new row first: it sits in the setup's scratch, which
+    // buffer 1 overlaps.
+    if (owns_new) consume(rowk, rowv, 1, row);
+    __syncthreads();  // operands held, new row taken, descriptors published
+
+    int ts = 0, n0 = 0;  // rows of tile i
+    desc(0, ts, n0);
+    if (WQ && n0 > 0) issue(0, ts, n0);  // (static: issued before the setup)
+    for (int i = 0; n0 > 0; i++) {
+      // this wave's loads of tile i are done; after the barrier everyone's
+      // are, and everyone is done with tile i-1, whose buffer takes tile i+1
+      wait_vm0();
       __syncthreads();
-      for (int i = 0; cn > 0; i++) {
-        uint8_t *cur = (i & 1) ? buf1 : buf0, *nxt = (i & 1) ? buf0 : buf1;
-        consume(cur, cur + (size_t)TP * lrow, cn, lrow);
-        cn = in;
-        if (cn > 0) {
-          stash(nxt, cn);
-          next_tile(its, in);
-          if (in > 0) issue(its, in);
-        }
-        __syncthreads();
-      }
+      int n1 = 0;
+      desc(i + 1, ts, n1);
+      if (n1 > 0) issue((i + 1) & 1, ts, n1);
+      if (WQ && wave == 0) publish(i + 2);
+      uint8_t *cur = buf(i & 1);
+      consume(cur, cur + kTilesTensorBytes, n0, kTilesLdsRow);
+      n0 = n1;
     }
 
     // The partials (or the output) of the wave's heads: the sums of each
