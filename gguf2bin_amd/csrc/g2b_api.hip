@@ -543,7 +543,19 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   const bool use_wq = !fixed && fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
                        wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
-  const int64_t slots = use_wq ? wq_slots : tiles ? tiles_slots(c, false) : slots_for(c, dp, false);
+  // k_layer's work queue pulls its chunks straight into LDS (mode 1): 1-2%
+  // faster than register staging on the batched configs, while a single
+  // sequence's static splits, bound by latency, keep register staging.
+  if (use_wq && !tiles && c->tune_stage == 0 && dp.stage_mode == kDefaultStageMode) {
+    const int32_t r1 = decode_stage_rows(c->sh, dp.tune_chunk, 1);
+    if (r1 > 0) {
+      dp.stage_mode = 1;
+      dp.stage_rows = r1;
+    }
+  }
+  const int64_t slots = use_wq ? (tiles ? wq_slots : slots_for(c, dp, true))
+                        : tiles ? tiles_slots(c, false)
+                                : slots_for(c, dp, false);
   int32_t max_splits;
   if (use_wq) {
     const int64_t wq_lines = n_units + 1;  // the units and the next-unit counter

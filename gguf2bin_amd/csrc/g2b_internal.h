@@ -46,8 +46,14 @@ __host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
 // setup inputs (the q and k norm weights, the cos/sin row of pos).  After the stream, the wave
 // merge of the partials ([wave][head][kPartHead + head_dim] floats) reuses
 // everything from 0.
+// Rows the staging regions of layer_lds_layout hold per wave and tensor:
+// mode 2 one chunk (the next one waits in registers), mode 1 two (the next
+// one is loaded straight into LDS), mode 0 none.
+__host__ __device__ inline int32_t layer_stage_rows(int32_t mode, int32_t stage_rows) {
+  return mode == 1 ? 2 * stage_rows : mode ? stage_rows : 0;
+}
 struct LdsLayout {
-  uint32_t rows, row_pad, total;
+  uint32_t pre, rows, row_pad, total;  // pre: the setup's bytes at 0
 };
 __host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
@@ -58,6 +64,7 @@ __host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_
   const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)sh.n_heads *
                          (uint32_t)(kPartHead + sh.head_dim) * 4u;
   LdsLayout l;
+  l.pre = pre;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;
   l.rows = pre > stage ? pre : stage;
   const uint32_t need =

@@ -71,6 +71,70 @@ __device__ __forceinline__ T gload(const uint8_t *p) {
 constexpr int kAuxNT = 2;
 // s_waitcnt operand (gfx9 encoding): vmcnt = 0, expcnt and lgkmcnt not waited.
 constexpr int kWaitVmcnt0 = 0x0F70;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family devices: data
+// format 32 bits, the rest zero (untyped loads move the bytes as they are;
+// the range check is offset < the resource's byte count).
+constexpr int32_t kBufferRsrcWord3 = 0x00020000;
+
+// Streamed chunks go straight into LDS and work-queue claims return
+// through inline assembly, so that the compiler's wait-count bookkeeping
+// does not see them: it waits for every LDS DMA before any LDS read (which
+// would serialise each chunk's loads with the consumption of the one before),
+// and loads or claims issued on some loop paths and not others made it wait
+// for everything (vmcnt(0)) inside the consume phase.  The kernels wait for
+// them themselves, with s_waitcnt vmcnt(0) before each chunk is read.
+//
+// 16 bytes per lane from buffer resource rsrc at byte voff into LDS at
+// lds_addr + 16 * lane, non-temporal (M0 holds the LDS address).
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(lds_addr), "v"(voff), "s"(rsrc)
+               : "memory");
+}
+// Lane 0 adds 1 to *ctr (agent scope: global_atomic_add ... sc0, as the
+// compiler issues a relaxed agent-scope fetch_add) and finds the old value in
+// its lane of the result once the atomic completes: the caller reads it
+// (readlane 0) only after an s_waitcnt that covers it.  The other lanes are
+// masked off inside the statement.
+__device__ __forceinline__ int32_t claim_lane0(int32_t *ctr) {
+  int32_t r;
+  uint64_t save;
+  asm volatile(
+      "s_mov_b64 %1, exec\n\t"
+      "s_mov_b64 exec, 1\n\t"
+      "global_atomic_add %0, %2, %3, off sc0\n\t"
+      "s_mov_b64 exec, %1"
+      : "=&v"(r), "=&s"(save)
+      : "v"(ctr), "v"(1)
+      : "memory");
+  return r;
+}
+// The raw buffer resource of `bytes` bytes at p (p the same in every lane).
+__device__ __forceinline__ i32x4 raw_rsrc(const uint8_t *p, uint32_t bytes) {
+  const uint64_t u = (uint64_t)(uintptr_t)p;
+  i32x4 r;
+  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32)) & 0xFFFF;
+  r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+  r.w = kBufferRsrcWord3;
+  return r;
+}
+// The LDS address of p (a pointer into __shared__ memory).
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+// Every vector memory operation of this wave has completed.
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); }
+// The same wait, with a and b (results of claim_lane0) passed through it:
+// the compiler cannot tell that such a register is still being written, and
+// would otherwise be free to read it before the wait.
+__device__ __forceinline__ void wait_vm0_claims(int32_t &a, int32_t &b) {
+  asm volatile("s_waitcnt vmcnt(0)" : "+v"(a), "+v"(b) : : "memory");
+}
+
 // Online softmax: how far (log2 units) a score may exceed the reference
 // before the accumulators are rescaled.
 constexpr float kRescaleSlack = 8.f;
@@ -644,7 +708,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   // LDS: rotated q (nq floats), rotated new k and new v (nkv floats each) at 0 - with
   // STG, the waves' staging regions overlap them once q is in registers -
   // then the new K and V rows and the QK-RMSNorm scratch (n_heads floats).
-  const LdsLayout ll = layer_lds_layout(P.sh, STG ? P.stage_rows : 0);
+  const LdsLayout ll = layer_lds_layout(P.sh, layer_stage_rows(STG, P.stage_rows));
   float *qrot = reinterpret_cast<float *>(lds);
   float *kr = reinterpret_cast<float *>(lds + nq * 4);
   float *vr = reinterpret_cast<float *>(lds + nq * 4 + ((nkv * 4 + 15) & ~15u));
@@ -700,10 +764,39 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         C::load(vv[u], vb + off, lo);
       }
     };
+    // LDS DMA staging (STG 1): two regions per wave and tensor, region 0 of
+    // every wave in the upper half of the staging area and region 1 in the
+    // lower half, where the setup's scratch lies (so that a static
+    // schedule's first chunk can land in region 0 during the setup when the
+    // scratch fits the lower half).  Chunk cs0 of nrows rows goes straight
+    // into region k (buffer_load_dwordx4 ... lds, non-temporal) once the
+    // wave's reads of that region are done.
+    [[maybe_unused]] const uint32_t cbytes = (uint32_t)P.stage_rows * (uint32_t)row;
+    [[maybe_unused]] auto region = [&](int k) {
+      return lds + (size_t)((k ? 0 : kWavesPerSplit) + wave) * 2 * cbytes;
+    };
+    [[maybe_unused]] auto dma_chunk = [&](int k, int cs0, int nrows) {
+      const uint32_t np = (uint32_t)nrows * (uint32_t)row / 16u;  // 16-byte pieces
+      const size_t base = (size_t)cs0 * row;
+      const i32x4 rk = raw_rsrc(kb + base, np * 16u), rv = raw_rsrc(vb + base, np * 16u);
+      const uint32_t la = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr(region(k)));
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region's reads are done
+      for (uint32_t i = 0; 64u * i < np; i++) {
+        if (64u * i + (uint32_t)lane < np) {
+          dma16(rk, la + 1024u * i, 16u * (64u * i + (uint32_t)lane));
+          dma16(rv, la + cbytes + 1024u * i, 16u * (64u * i + (uint32_t)lane));
+        }
+      }
+    };
+    [[maybe_unused]] const bool early = ll.pre <= (uint32_t)kWavesPerSplit * 2u * cbytes;
     // Static schedule: the wave's first chunk or trip is in flight during
     // the setup.
     if constexpr (STG == 2 && !WQ) {
       if (t0 + wave * P.stage_rows < tend) issue(t0 + wave * P.stage_rows);
+    }
+    if constexpr (STG == 1 && !WQ) {
+      if (early && t0 + wave * P.stage_rows < tend)
+        dma_chunk(0, t0 + wave * P.stage_rows, min(P.stage_rows, tend - t0 - wave * P.stage_rows));
     }
     if constexpr (STG == 0) {
       if (t0 + wave * PPW < tend) fetch(t0 + wave * PPW, ka, va);
@@ -903,7 +996,6 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       // HBM byte fetched once, by one lane, non-temporal); then every lane
       // reads its blocks from there.
       const int R = P.stage_rows;
-      const uint32_t cbytes = (uint32_t)R * (uint32_t)row;
       uint8_t *sk = lds + (size_t)wave * 2 * cbytes, *sv = sk + cbytes;
       const int steps = R / PPW;
       // U wave-steps of the chunk from LDS; rows past nrows (and idle lanes)
@@ -952,38 +1044,59 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         return v;
       };
       if constexpr (STG == 1) {
-        auto dma_chunk = [&](int cs0, int nrows) {
-          const uint32_t np = (uint32_t)nrows * (uint32_t)row / 16u;  // 16-byte pieces
-          const uint8_t *gk = kb + (size_t)cs0 * row + 16u * (uint32_t)lane;
-          const uint8_t *gv = vb + (size_t)cs0 * row + 16u * (uint32_t)lane;
-          for (uint32_t i = 0; 64u * i < np; i++) {
-            if (64u * i + (uint32_t)lane < np) {
-              __builtin_amdgcn_global_load_lds(
-                  (const __attribute__((address_space(1))) void *)(gk + 1024u * i),
-                  (__attribute__((address_space(3))) void *)(sk + 1024u * i), 16, 0, kAuxNT);
-              __builtin_amdgcn_global_load_lds(
-                  (const __attribute__((address_space(1))) void *)(gv + 1024u * i),
-                  (__attribute__((address_space(3))) void *)(sv + 1024u * i), 16, 0, kAuxNT);
-            }
-          }
-          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the chunk is in LDS
+        // Chunk c+1 goes into the wave's other region while chunk c is
+        // consumed; each wave waits for its own loads only (s_waitcnt
+        // vmcnt(0) opens every chunk: nothing else of the wave is then in
+        // flight).
+        auto consume_region = [&](int k, int cs0, int nrows) {
+          sk = region(k);
+          sv = sk + cbytes;
           consume_chunk(cs0, nrows);
-          // The next chunk's loads overwrite this region only after every
-          // value read from it above has been used (data dependence orders them).
         };
         if constexpr (!WQ) {
-          for (int cs0 = t0 + wave * R; cs0 < tend; cs0 += cstride)
-            dma_chunk(cs0, min(R, tend - cs0));
+          int cs0 = t0 + wave * R;
+          if (!early && cs0 < tend) dma_chunk(0, cs0, min(R, tend - cs0));
+          for (int k = 0; cs0 < tend; k ^= 1, cs0 += cstride) {
+            wait_vm0();
+            const int ns = cs0 + cstride;
+            if (ns < tend) dma_chunk(k ^ 1, ns, min(R, tend - ns));
+            consume_region(k, cs0, min(R, tend - cs0));
+          }
         } else {
-          int pc = __builtin_amdgcn_readfirstlane(claim_async());
-          int32_t pn1 = claim_async(), pn2 = claim_async();
-          while (pc < npieces) {
-            int ps, pe;
-            piece_range(pm, pc, tend, ps, pe);
-            for (int cs0 = ps; cs0 < pe; cs0 += R) dma_chunk(cs0, min(R, pe - cs0));
-            pc = __builtin_amdgcn_readfirstlane(pn1);
-            pn1 = pn2;
-            if (pc < npieces) pn2 = claim_async();
+          // this wave's pieces: a claim (lane 0, in assembly) is issued when
+          // a piece starts and read when it runs out - at a later chunk, so
+          // after a wait for all of the wave's loads
+          int32_t c0 = claim_lane0(ctr);
+          int32_t pend = claim_lane0(ctr);
+          wait_vm0_claims(c0, pend);
+          int pc = __builtin_amdgcn_readlane(c0, 0);
+          int cs0 = 0, ce = 0;
+          bool live = pc >= 0 && pc < npieces;
+          if (live) {
+            piece_range(pm, pc, tend, cs0, ce);
+            cs0 = __builtin_amdgcn_readfirstlane(cs0);
+            ce = __builtin_amdgcn_readfirstlane(ce);
+            dma_chunk(0, cs0, min(R, ce - cs0));
+          }
+          for (int k = 0; live; k ^= 1) {
+            wait_vm0_claims(pend, c0);
+            int ns = cs0 + R, nce = ce;
+            bool nlive = true;
+            if (ns >= ce) {  // next piece
+              const int nc = __builtin_amdgcn_readlane(pend, 0);
+              nlive = nc >= 0 && nc < npieces;
+              if (nlive) {
+                piece_range(pm, nc, tend, ns, nce);
+                ns = __builtin_amdgcn_readfirstlane(ns);
+                nce = __builtin_amdgcn_readfirstlane(nce);
+                pend = claim_lane0(ctr);
+              }
+            }
+            if (nlive) dma_chunk(k ^ 1, ns, min(R, nce - ns));
+            consume_region(k, cs0, min(R, ce - cs0));
+            live = nlive;
+            cs0 = ns;
+            ce = nce;
           }
         }
       } else {
@@ -1231,7 +1344,7 @@ static inline size_t layer_lds_bytes(const ShapeDev &sh, int32_t stage_rows) {
 template <int FMT, int HD, int CD, int G, int U, int STG, bool WQ>
 static hipError_t launch_fast_s(const DecodeParams &p, int n_layers, hipStream_t s) {
   const dim3 grid = WQ ? dim3(p.wq_grid) : dim3(p.max_splits, p.n_seq, n_layers);
-  const size_t lds = layer_lds_bytes(p.sh, STG ? p.stage_rows : 0);
+  const size_t lds = layer_lds_bytes(p.sh, layer_stage_rows(STG, p.stage_rows));
   if (p.att)
     hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG, WQ>), grid, dim3(kThreads), lds, s, p);
   else
@@ -1275,7 +1388,7 @@ static int occupancy_of(const ShapeDev &sh, int32_t stage_rows) {
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_layer<FMT, HD, CD, G, 2, false, STG, WQ>,
                                                    kThreads,
-                                                   layer_lds_bytes(sh, STG ? stage_rows : 0)) !=
+                                                   layer_lds_bytes(sh, layer_stage_rows(STG, stage_rows))) !=
       hipSuccess) {
     (void)hipGetLastError();
     return 1;

@@ -126,64 +126,6 @@ __device__ __forceinline__ float group_max(float x) {
   return x;
 }
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-
-// Word 3 of a raw (stride 0) buffer resource on gfx9-family devices: data
-// format 32 bits, the rest zero (untyped loads move the bytes as they are;
-// the range check is offset < the resource's byte count).
-constexpr int32_t kBufferRsrcWord3 = 0x00020000;
-
-// The tile loads and the work-queue claims are issued through inline
-// assembly, so that the compiler's wait-count bookkeeping does not see them:
-// the compiler waits for every LDS DMA before any LDS read (which would
-// serialise each tile's loads with the consumption of the one before), and
-// loads or claims issued on some loop paths and not others made it wait for
-// everything (vmcnt(0)) inside the consume phase.  The kernel waits for them
-// itself: one s_waitcnt vmcnt(0) per tile, before the barrier that opens it.
-//
-// 16 bytes per lane from buffer resource rsrc at byte voff into LDS at
-// lds_addr + 16 * lane, non-temporal (M0 holds the LDS address).
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
-               :
-               : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory");
-}
-// Lane 0 adds 1 to *ctr (agent scope: global_atomic_add ... sc0, as the
-// compiler issues a relaxed agent-scope fetch_add) and finds the old value in
-// its lane of the result once the atomic completes: the caller reads it
-// (readlane 0) only after an s_waitcnt that covers it.  The other lanes are
-// masked off inside the statement.
-__device__ __forceinline__ int32_t claim_lane0(int32_t *ctr) {
-  int32_t r;
-  uint64_t save;
-  asm volatile(
-      "s_mov_b64 %1, exec\n\t"
-      "s_mov_b64 exec, 1\n\t"
-      "global_atomic_add %0, %2, %3, off sc0\n\t"
-      "s_mov_b64 exec, %1"
-      : "=&v"(r), "=&s"(save)
-      : "v"(ctr), "v"(1)
-      : "memory");
-  return r;
-}
-// The raw buffer resource of `bytes` bytes at p (p the same in every lane).
-__device__ __forceinline__ i32x4 raw_rsrc(const uint8_t *p, uint32_t bytes) {
-  const uint64_t u = (uint64_t)(uintptr_t)p;
-  i32x4 r;
-  r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)u);
-  r.y = __builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32)) & 0xFFFF;
-  r.z = (int)bytes;
-  r.w = kBufferRsrcWord3;
-  return r;
-}
-// The LDS address of p (a pointer into __shared__ memory).
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-// Every vector memory operation of this wave has completed.
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // G: q heads per KV head (3 or 4).  WQ: work-queue schedule.
 template <int G, bool WQ>
 __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
@@ -479,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     };
     if constexpr (WQ) {
       if (wave == 0) {
-        wait_vm0();  // the first two claims (nothing else of this wave is in flight)
+        wait_vm0_claims(first, pend);  // (nothing else of this wave is in flight)
         take_piece(__builtin_amdgcn_readlane(first, 0));
         publish(0);
         publish(1);
@@ -497,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     for (int i = 0; n0 > 0; i++) {
       // this wave's loads of tile i are done; after the barrier everyone's
       // are, and everyone is done with tile i-1, whose buffer takes tile i+1
-      wait_vm0();
+      wait_vm0_claims(pend, first);
       __syncthreads();
       int n1 = 0;
       desc(i + 1, ts, n1);

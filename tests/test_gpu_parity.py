@@ -179,7 +179,8 @@ SHAPES = {
 
 # Schedules of the decode call: (all layers in one call?, g2b_ctx_tune arguments
 # (split_len, chunk, stage, piece)).  "wq" forces the work queue (piece > 0),
-# "static" forces static splits, "dma" / "direct" the other KV row paths.
+# "static" forces static splits, "dma" / "dma_wq" the KV rows loaded straight
+# into LDS (static splits, work queue), "direct" per-lane loads.
 MODES = {
     "fused": (True, None),
     "layers": (False, None),
@@ -187,6 +188,7 @@ MODES = {
     "wq_fused": (True, (0, 0, 2, 8)),
     "static": (False, (0, 0, 2, -1)),
     "dma": (True, (0, 0, 1, -1)),
+    "dma_wq": (False, (0, 0, 1, 1)),
     "direct": (False, (0, 0, -1, -1)),
 }
 
