@@ -105,6 +105,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
 constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 2048;
 constexpr int kCombineFewParts = 32;  // up to this many partials: one wave per head
+constexpr int kCombineRowLoads = 24;  // rows held per thread on the one-round path
 
 __device__ inline float block_max_f(float x, float *red) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
@@ -130,7 +131,7 @@ __device__ inline double block_sum_d(double x, double *red) {
 
 __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, float *q_out) {
   __shared__ float w[kCombineMaxParts];
-  __shared__ double part_sum[kCombineThreads];
+  __shared__ double part_sum[4 * kCombineThreads];
   __shared__ double red[kCombineThreads / 64];
   const int h = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
@@ -155,6 +156,65 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
   const float *base =
       P.part + (sidx * nh + h) * (size_t)P.max_splits * pstr;
   const int tid = threadIdx.x;
+
+  // One round of loads where the rows fit the registers (up to
+  // kCombineRowLoads float4s of partial rows per thread): every (m, l) pair
+  // and every accumulator row is requested before any of them is used, so
+  // the merge waits for memory once (a few hundred partials, e.g. a single
+  // long sequence's splits, were ~6 us of dependent rounds).
+  const int tpr = HD / 4, GRP = (HD & 3) == 0 && tpr <= kCombineThreads ? kCombineThreads / tpr : 0;
+  if (GRP > 0 && np >= 1 && np <= GRP * kCombineRowLoads && np <= kCombineThreads) {
+    const int grp = tid / tpr, q = tid - grp * tpr;
+    // (every load is unconditional - a partial past np reads the last one
+    // and gets no weight - so that they are all in flight together: a
+    // conditional load waits for itself before the branches join)
+    float2 ml = *reinterpret_cast<const float2 *>(base + (size_t)min(tid, np - 1) * pstr);
+    if (tid >= np) ml = make_float2(kNegBig, 0.f);
+    float4 v[kCombineRowLoads];
+    const float *a = base + kPartHead + 4 * (grp < GRP ? q : 0);
+#pragma unroll
+    for (int u = 0; u < kCombineRowLoads; u++) {
+      const int p = min(grp + GRP * u, np - 1);
+      v[u] = *reinterpret_cast<const float4 *>(a + (size_t)p * pstr);
+    }
+    const float M = block_max_f(ml.x, reinterpret_cast<float *>(red));
+    double lsum = 0.0;
+    if (tid < np) {
+      const float wp = exp2f(ml.x - M);
+      w[tid] = wp;
+      lsum = (double)ml.y * (double)wp;
+    }
+    const double L = block_sum_d(lsum, red);  // (its barriers also publish w)
+    double o[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int u = 0; u < kCombineRowLoads; u++) {
+      const int p = grp + GRP * u;
+      if (grp < GRP && p < np) {
+        const double wp = (double)w[p];
+        o[0] = fma((double)v[u].x, wp, o[0]);
+        o[1] = fma((double)v[u].y, wp, o[1]);
+        o[2] = fma((double)v[u].z, wp, o[2]);
+        o[3] = fma((double)v[u].w, wp, o[3]);
+      }
+    }
+    double *gs = part_sum;  // [group][HD], GRP * HD <= 4 * kCombineThreads
+    __syncthreads();
+    if (grp < GRP)
+      for (int j = 0; j < 4; j++) gs[grp * HD + 4 * q + j] = o[j];
+    __syncthreads();
+    float *out = q_out + sidx * (size_t)(nh * HD) + (size_t)h * HD;
+    for (int d = tid; d < HD; d += kCombineThreads) {
+      double sum = 0.0;
+      for (int g = 0; g < GRP; g++) sum += gs[g * HD + d];
+      out[d] = (float)(sum / L);
+    }
+    if (P.att) {
+      float *at = P.att + (sidx * nh + h) * (size_t)P.att_stride;
+      for (int t = tid; t < npos; t += blockDim.x)
+        at[t] = (float)(exp2((double)at[t] - (double)M) / L);
+    }
+    return;
+  }
 
   float mx = kNegBig;
   for (int p = tid; p < np; p += blockDim.x) mx = fmaxf(mx, base[p * pstr]);
