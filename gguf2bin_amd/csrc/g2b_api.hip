@@ -428,11 +428,15 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
   // Staging pays for Q8_0 rows, whose per-lane block windows overlap; F32
-  // rows are read by the lanes in whole, disjoint 64-byte runs already.
-  dp.stage_mode = c->tune_stage < 0   ? 0
-                  : c->tune_stage > 0 ? c->tune_stage
-                  : c->shape.kv_q8    ? kDefaultStageMode
-                                      : 0;
+  // rows are read by the lanes in whole, disjoint 64-byte runs already.  One
+  // layer of one sequence is bound by latency, not bytes: per-lane loads,
+  // whose first trip is in flight during the setup (c2, 8193 positions:
+  // 545 us per layer-serial step against 580 us for staged chunks).
+  const bool one_unit = n_seq == 1 && n_layers == 1;
+  dp.stage_mode = c->tune_stage < 0          ? 0
+                  : c->tune_stage > 0        ? c->tune_stage
+                  : c->shape.kv_q8 && !one_unit ? kDefaultStageMode
+                                                : 0;
   dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
@@ -460,21 +464,16 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // kShortMaxPos positions, sequence, layer).  Below kShortMaxPos positions
   // it is a single span that writes the output over q itself.  Longer
   // contexts take it (spans that merge their partials in the kernel, no
-  // combine launch) automatically when one layer of one sequence is asked
-  // for and its spans fit one workgroup per CU: the in-kernel merge saves
-  // the combine launch only while the spans run in a single round (c1, 17
-  // spans x 8 KV heads = 136 workgroups: 525.9 against 556.7 us per
-  // layer-serial step; c2, 65 x 8 = 520: 822 against 695; all 28 layers in
-  // one call 108.7 against 92.7 us).  g2b_ctx_tune_kernel(3) asks for it
-  // wherever it fits.  An explicit split length or work-queue piece
-  // (g2b_ctx_tune) keeps the split kernels.
+  // combine launch) only when g2b_ctx_tune_kernel(3) asks for it: one layer
+  // of one sequence runs faster on k_layer's short static splits and the
+  // one-round combine (c1, 17 spans x 8 KV heads = 136 workgroups: 525.9 us
+  // per layer-serial step against 459 us; c2, 65 x 8 = 520: 822 against
+  // 545; all 28 layers in one call 108.7 against 92.7 us).  An explicit
+  // split length or work-queue piece (g2b_ctx_tune) keeps the split kernels.
   const int32_t n_spans = max_pos / kShortMaxPos + 1;
   const bool short_ok = fast && !att && c->split_override == 0 && c->tune_piece == 0 &&
                         short_available(c->sh);
-  const bool spans_wanted =
-      c->tune_kernel == 3 ||
-      (c->tune_kernel == 0 && n_seq == 1 && n_layers == 1 &&
-       (int64_t)n_spans * c->shape.n_kv_heads <= (int64_t)std::max(1, c->n_cu));
+  const bool spans_wanted = c->tune_kernel == 3;
   const bool spans_fit = n_spans <= std::min<int32_t>(kShortMaxSpans, splits_per_seq) &&
                          (!fixed || (size_t)n_layers * n_seq * c->shape.n_kv_heads <= fixed_ctr);
   if (short_ok && (n_spans == 1 || (spans_wanted && spans_fit))) {
@@ -608,22 +607,36 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     if (d_seqs && d_seqs == c->d_seqs && c->h_seqs && cap == hipStreamCaptureStatusNone)
       if (int rc = wq_home_table(c, n_seq, n_layers, slots, &dp.home)) return rc;
   } else {
-    // (measured: four staged chunks or eight per-lane wave-steps per wave)
+    // (measured: four staged chunks or eight per-lane wave-steps per wave, four
+    // for one layer of one sequence)
+    const int32_t ppw = decode_ppw(c->sh, dp.tune_chunk);
     const int32_t min_len = !fast                ? 64
                             : tiles             ? 8 * kTilesRows
                             : dp.stage_rows > 0 ? kWavesPerSplit * 4 * dp.stage_rows
-                                                : kWavesPerSplit * 8 * decode_ppw(c->sh, dp.tune_chunk);
+                            : one_unit          ? kWavesPerSplit * 4 * ppw
+                                                : kWavesPerSplit * 8 * ppw;
     // Per-lane loads (stage_rows == 0): for one sequence a round is one
     // workgroup per CU (c1 all layers: 252 workgroups of 228 positions
-    // 92.7 us, 364 of 161 positions 109 us); for batches ~0.7 of the resident
-    // workgroups - measured on the 64-sequence SmolLM2 F32 batch (c3): 1304 us
-    // per layer-serial step at 0.72 of a round against 1490 us at 0.9,
-    // 1559 us at 1.13 and 1458 us at 1.5 rounds
+    // 92.7 us, 364 of 161 positions 109 us), and one layer of it takes half
+    // of that (fewer partials for the combine; c1, 2049 positions: 459 us per
+    // layer-serial step at 129 splits, 487 at 147, 507 at 171 and 522 at 228;
+    // c2, 8193 positions: 545 at 129, 561 at 249); for batches ~0.7 of the
+    // resident workgroups - measured on the 64-sequence SmolLM2 F32 batch
+    // (c3): 1304 us per layer-serial step at 0.72 of a round against 1490 us
+    // at 0.9, 1559 us at 1.13 and 1458 us at 1.5 rounds
     const int64_t split_slots = !(fast && dp.stage_rows == 0) ? slots
+                                : one_unit                   ? std::max(1, c->n_cu / 2)
                                 : n_seq == 1                 ? std::max(1, c->n_cu)
                                                              : slots * 7 / 10;
     int32_t split_len = choose_split(c, std::max<int64_t>(split_slots, 1), n_seq, total_pos,
                                      max_pos, n_layers, fast, min_len);
+    if (fast && one_unit && dp.stage_rows == 0 && c->split_override == 0) {
+      // whole trips (two wave-steps) for every wave: a wave with one more
+      // trip than the others waits one more round trip (c1: 489 us per
+      // layer-serial step at 17 positions per split, 459 at 16)
+      const int32_t trip = kWavesPerSplit * 2 * ppw;
+      split_len = std::max(min_len, split_len / trip * trip);
+    }
     max_splits = (max_pos + 1 + split_len - 1) / split_len;
     if (max_splits > splits_per_seq) {  // lengthen the splits to stay within the budget
       split_len = (int32_t)(((int64_t)max_pos + splits_per_seq) / splits_per_seq);

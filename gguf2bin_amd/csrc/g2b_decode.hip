@@ -105,7 +105,7 @@ __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
 constexpr int kCombineThreads = 256;
 constexpr int kCombineMaxParts = 2048;
 constexpr int kCombineFewParts = 32;  // up to this many partials: one wave per head
-constexpr int kCombineRowLoads = 24;  // rows held per thread on the one-round path
+constexpr int kCombineRowLoads = 32;  // rows held per thread on the one-round path
 
 __device__ inline float block_max_f(float x, float *red) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));

@@ -50,6 +50,24 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// x of lane ^ S (S = 32 or 16) through gfx950's lane swaps, on the VALU (no
+// LDS traffic).  With both operands x, v_permlane32_swap leaves lanes 0-31 of
+// its second result holding lanes 32-63 of x and lanes 32-63 of its first
+// result holding lanes 0-31; v_permlane16_swap does the same for each pair of
+// 16-lane rows.
+template <int S>
+__device__ __forceinline__ float lanes_xor(float x) {
+  static_assert(S == 32 || S == 16, "swap distance");
+  const uint32_t u = __float_as_uint(x);
+  if constexpr (S == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  }
+}
+
 __device__ __forceinline__ float i8f(uint32_t w, int byte) {
   return (float)(int8_t)(uint8_t)(w >> (8 * byte));
 }
@@ -1177,25 +1195,47 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
     }
 
-    // Fold the PPW position slots of the wave into slot 0.  Every lane takes
-    // part in the shuffles, but only slot-0 lanes update their state, so the
-    // state read from slot k is always slot k's own.
-    const bool gather = slot == 0;
-    for (int k = 1; k < PPW; k++) {
-      const int src = (lane + k * LPP) & 63;
+    // Fold the PPW position slots of the wave into slot 0.  Slots of 32 or
+    // 16 lanes: a butterfly through the lane swaps, every lane merging its
+    // state with lane ^ 32's (then lane ^ 16's), so all lanes end with the
+    // wave's state.  Otherwise every lane takes part in LDS shuffles, but only
+    // slot-0 lanes update their state, so the state read from slot k is always
+    // slot k's own.
+    auto fold_xor = [&](auto dist) {
+      constexpr int S = decltype(dist)::value;
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        const float m2 = __shfl(m[i], src);
-        const float l2 = __shfl(l[i], src);
+        const float m2 = lanes_xor<S>(m[i]);
+        const float l2 = lanes_xor<S>(l[i]);
         const float M = fmaxf(m[i], m2);
         const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
-        l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
+        l[i] = l[i] * f1 + l2 * f2;
 #pragma unroll
-        for (int j = 0; j < CD; j++) {
-          const float a2 = __shfl(acc[i][j], src);
-          acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
+        for (int j = 0; j < CD; j++) acc[i][j] = acc[i][j] * f1 + lanes_xor<S>(acc[i][j]) * f2;
+        m[i] = M;
+      }
+    };
+    if (LPP == 32 || LPP == 16) {
+      fold_xor(std::integral_constant<int, 32>{});
+      if (LPP == 16) fold_xor(std::integral_constant<int, 16>{});
+    } else {
+      const bool gather = slot == 0;
+      for (int k = 1; k < PPW; k++) {
+        const int src = (lane + k * LPP) & 63;
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+          const float m2 = __shfl(m[i], src);
+          const float l2 = __shfl(l[i], src);
+          const float M = fmaxf(m[i], m2);
+          const float f1 = exp2f(m[i] - M), f2 = exp2f(m2 - M);
+          l[i] = gather ? l[i] * f1 + l2 * f2 : l[i];
+#pragma unroll
+          for (int j = 0; j < CD; j++) {
+            const float a2 = __shfl(acc[i][j], src);
+            acc[i][j] = gather ? acc[i][j] * f1 + a2 * f2 : acc[i][j];
+          }
+          m[i] = gather ? M : m[i];
         }
-        m[i] = gather ? M : m[i];
       }
     }
     // Merge the four waves' states in LDS (the rows and q there are no

@@ -66,14 +66,19 @@ def test_long_single_sequence(gpu_device, q8):
 
 @pytest.mark.parametrize("q8", [True, False])
 def test_automatic_choice(gpu_device, q8):
-    """The automatic choice for one layer of one sequence whose spans fit one
-    workgroup per CU (2049 positions: 17 spans x 8 KV heads) is k_short; the
-    outputs against the oracle."""
+    """Spans are taken only when asked for: the automatic choice for one layer
+    of one sequence past 128 positions (2049: 17 spans) is k_layer's static
+    splits, at least four per-lane wave-steps per wave, and the combine; below
+    128 positions it is a single span writing the output itself.  Outputs
+    against the oracle."""
     o = orc.Shape(1, 16, 8, 128, 1e6, orc.ARCH_QWEN3, q8)
     print(f"[spans] automatic q8={q8}", flush=True)
     sched = {}
     run_batch_case(o, [2049], [2048], seed=17, fused=False, want_att=False, sched=sched)
-    assert sched["kernel"] == "k_short" and sched["max_splits"] == 17, sched
+    assert sched["kernel"] == "k_layer" and sched["max_splits"] > 1, sched
+    assert not sched["output_in_kernel"], sched
+    run_batch_case(o, [128], [127], seed=18, fused=False, want_att=False, sched=sched)
+    assert sched["kernel"] == "k_short" and sched["max_splits"] == 1, sched
     assert sched["output_in_kernel"], sched
 
 
