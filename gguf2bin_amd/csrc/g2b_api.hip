@@ -286,6 +286,34 @@ int32_t choose_split(const g2b_ctx *c, int64_t slots, int32_t n_seq, int64_t tot
   return (int32_t)std::max<int64_t>(sl, 1);
 }
 
+// Zeroes device memory before anything on the context's stream can read it:
+// the stream is non-blocking, so a hipMemset on the null stream would not be
+// ordered before its launches.
+int zero_device(g2b_ctx *c, void *p, size_t bytes) {
+  G2B_HIP(c, hipMemsetAsync(p, 0, bytes, c->stream));
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  return G2B_OK;
+}
+
+// At least n of k_short's span tickets, zero between launches (the last span
+// of each (sequence, layer, KV head) resets its own).
+int span_counters(g2b_ctx *c, size_t n) {
+  if (n <= c->span_ctr_cap) return G2B_OK;
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  if (c->span_ctr) G2B_HIP(c, hipFree(c->span_ctr));
+  c->span_ctr = nullptr;
+  c->span_ctr_cap = 0;
+  const size_t cap = std::max<size_t>(n, G2B_SPAN_CTR_MIN);
+  if (hipMalloc((void **)&c->span_ctr, cap * sizeof(int32_t)) != hipSuccess) {
+    c->span_ctr = nullptr;
+    (void)hipGetLastError();
+    return fail(c, G2B_ENOMEM, "span counters");
+  }
+  c->span_ctr_cap = cap;
+  if (int rc = zero_device(c, c->span_ctr, cap * sizeof(int32_t))) return rc;
+  return G2B_OK;
+}
+
 void set_sched(g2b_ctx *c, int32_t kernel, int32_t split_len, int32_t piece_len,
                int32_t max_splits, int64_t grid, bool direct) {
   c->sched[0] = kernel;
@@ -491,22 +519,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
                                   (size_t)g2b_splits_per_layer_cap(n_seq) * nh *
                                   (size_t)(kPartHead + hd);
         if (int rc = grow(c, &c->part, &c->part_cap, part_floats, part_limit)) return rc;
-        if (ctrs > c->span_ctr_cap) {
-          // (counters are zero between launches: the last span of each
-          // (sequence, layer, KV head) resets its own)
-          G2B_HIP(c, hipStreamSynchronize(c->stream));
-          if (c->span_ctr) G2B_HIP(c, hipFree(c->span_ctr));
-          c->span_ctr = nullptr;
-          c->span_ctr_cap = 0;
-          const size_t cap = std::max<size_t>(ctrs, G2B_SPAN_CTR_MIN);
-          if (hipMalloc((void **)&c->span_ctr, cap * sizeof(int32_t)) != hipSuccess) {
-            c->span_ctr = nullptr;
-            (void)hipGetLastError();
-            return fail(c, G2B_ENOMEM, "span counters");
-          }
-          G2B_HIP(c, hipMemset(c->span_ctr, 0, cap * sizeof(int32_t)));
-          c->span_ctr_cap = cap;
-        }
+        if (int rc = span_counters(c, ctrs)) return rc;
         dp.span_ctr = c->span_ctr;
         dp.part = c->part;
       }
@@ -651,6 +664,7 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // one split per unit: the decode kernel writes the output, no combine
   const bool direct = fast && !use_wq && max_splits == 1 && !att;
   dp.direct_out = direct ? 1 : 0;
+
 
   const size_t part_floats = (size_t)n_layers * n_seq * nh * (size_t)max_splits *
                              (size_t)(kPartHead + hd);
@@ -860,7 +874,7 @@ int g2b_kv_alloc(g2b_ctx *c, int32_t ctx_cap, void **kc, void **vc) {
     if (k) (void)hipFree(k);
     return fail(c, G2B_ENOMEM, "KV allocation of 2 x %zu bytes failed", bytes);
   }
-  if (hipMemset(k, 0, bytes) != hipSuccess || hipMemset(v, 0, bytes) != hipSuccess) {
+  if (zero_device(c, k, bytes) != G2B_OK || zero_device(c, v, bytes) != G2B_OK) {
     (void)hipFree(k);
     (void)hipFree(v);
     return fail(c, G2B_EDEVICE, "KV memset failed");
@@ -945,7 +959,7 @@ int g2b_set_qk_norm(g2b_ctx *c, int32_t layer, const float *q_norm, const float 
       return fail(c, G2B_ENOMEM, "QK-norm weights");
     }
     c->qkn_on_h.assign((size_t)L, 0);
-    G2B_HIP(c, hipMemset(c->qkn_on, 0, (size_t)L * sizeof(int32_t)));
+    if (int rc = zero_device(c, c->qkn_on, (size_t)L * sizeof(int32_t))) return rc;
   }
   // Calls already queued may read the weights: let them finish first.
   G2B_HIP(c, hipStreamSynchronize(c->stream));

@@ -320,6 +320,52 @@ def test_static_splits_without_weights(gpu_device, name):
     run_batch_case(o, [1, 20, 33], [0, 19, 32], seed=33, fused=True, want_att=False, tune=tune)
 
 
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("norm", [False, True])
+def test_stepping_across_splits(gpu_device, q8, norm):
+    """A decode loop: one layer stepped one position per call from 120 to 200
+    on one context, each call appending its row (k_short below 128, then
+    k_layer's splits and the combine as their count grows; the first of
+    those calls allocates the context's buffers), every step against the
+    oracle; 8 query heads, 4 KV heads, head_dim 128, with and without
+    QK-RMSNorm."""
+    o = orc.Shape(1, 8, 4, 128, 1e6, orc.ARCH_QWEN3, q8)
+    cap, eps = 256, 1e-6
+    rng = np.random.default_rng(7 + 2 * int(q8) + int(norm))
+    qn = (1 + 0.25 * rng.standard_normal(o.head_dim)).astype(np.float32) if norm else None
+    kn = (1 + 0.25 * rng.standard_normal(o.head_dim)).astype(np.float32) if norm else None
+    print(f"[stepping] q8={q8} norm={norm}", flush=True)
+    with attn.Context(ashape(o)) as ctx:
+        if norm:
+            ctx.set_qk_norm(0, qn, kn, eps)
+        kc, vc = ctx.kv_alloc(cap)
+        host = orc.alloc_kv(o, cap)
+        try:
+            kp = rng.standard_normal((120, o.nkv)).astype(np.float32)
+            vp = rng.standard_normal((120, o.nkv)).astype(np.float32)
+            kd, vd = hip.to_device(kp), hip.to_device(vp)
+            ctx.kv_append_rows(kc, vc, cap, 0, 0, 120, kd.ptr, vd.ptr)
+            ctx.sync()
+            orc.kv_prefill(o, cap, 0, 0, host[0], host[1],
+                           normed(kp, kn, o.n_kv_heads, o.head_dim, eps), vp)
+            for pos in range(120, 200):
+                q = rng.standard_normal(o.nq).astype(np.float32)
+                k = rng.standard_normal(o.nkv).astype(np.float32)
+                v = rng.standard_normal(o.nkv).astype(np.float32)
+                qd, kk, vv = hip.to_device(q), hip.to_device(k), hip.to_device(v)
+                ctx.attn_forward(0, pos, cap, kc, vc, qd.ptr, kk.ptr, vv.ptr)
+                ctx.sync()
+                out = qd.download(np.float32, q.size)
+                ql = normed(q, qn, o.n_heads, o.head_dim, eps)
+                kl = normed(k, kn, o.n_kv_heads, o.head_dim, eps)
+                ref, _ = orc.attn_layer(o, cap, 0, pos, host[0], host[1], ql, kl, v)
+                ex, _ = exact_attention(o, cap, 0, pos, host[0], host[1], ql)
+                check_out(out, ref, ex)
+        finally:
+            ctx.kv_free(kc, vc)
+
+
+
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3"])
 def test_unaligned_qkv_take_generic_kernels(gpu_device, name):
     """q/k/v that are not 16-byte aligned (the fast kernel reads 16-byte
