@@ -45,7 +45,7 @@ __host__ __device__ inline int32_t stage_rows_of(uint32_t row_bytes,
 // floats (rounded up to 4) of QK-RMSNorm factors and 3 * head_dim floats of
 // setup inputs (the q and k norm weights, the cos/sin row of pos).  After the stream, the wave
 // merge of the partials ([wave][head][kPartHead + head_dim] floats) reuses
-// everything from 0.
+// everything from 0 (merge_states states per wave).
 // Rows the staging regions of layer_lds_layout hold per wave and tensor:
 // mode 2 one chunk (the next one waits in registers), mode 1 two (the next
 // one is loaded straight into LDS), mode 0 none.
@@ -55,14 +55,27 @@ __host__ __device__ inline int32_t layer_stage_rows(int32_t mode, int32_t stage_
 struct LdsLayout {
   uint32_t pre, rows, row_pad, total;  // pre: the setup's bytes at 0
 };
-__host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows) {
+// k_layer's position slots per wave that go to the LDS merge as they are
+// (1: folded inside the wave first), for lpp lanes per position.  Slots of 32
+// or 16 lanes fold through lane swaps; other widths of up to kLdsFoldMax
+// slots per wave skip the in-wave fold (a chain of LDS shuffles) and merge
+// with the other waves' states in LDS.
+constexpr int kLdsFoldMax = 8;
+__host__ __device__ inline int layer_merge_states(int lpp) {
+  const int ppw = lpp >= 1 && lpp <= 64 ? 64 / lpp : 1;
+  return (lpp == 32 || lpp == 16 || ppw <= 1 || ppw > kLdsFoldMax) ? 1 : ppw;
+}
+// merge_states: layer_merge_states of the variant (the merge area holds that
+// many states per wave).
+__host__ __device__ inline LdsLayout layer_lds_layout(const ShapeDev &sh, int32_t stage_rows,
+                                                      int32_t merge_states = 1) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
   const uint32_t nkv = (uint32_t)(sh.n_kv_heads * sh.head_dim);
   const uint32_t pre = nq * 4u + 2u * ((nkv * 4u + 15u) & ~15u) +
                        (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
   const uint32_t stage = (uint32_t)kWavesPerSplit * 2u * (uint32_t)stage_rows * sh.row_bytes;
-  const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)sh.n_heads *
-                         (uint32_t)(kPartHead + sh.head_dim) * 4u;
+  const uint32_t merge = (uint32_t)kWavesPerSplit * (uint32_t)merge_states *
+                         (uint32_t)sh.n_heads * (uint32_t)(kPartHead + sh.head_dim) * 4u;
   LdsLayout l;
   l.pre = pre;
   l.row_pad = (sh.row_bytes + 15u) & ~15u;

@@ -1215,10 +1215,11 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         m[i] = M;
       }
     };
+    const int S = layer_merge_states(LPP);  // slots kept apart for the LDS merge
     if (LPP == 32 || LPP == 16) {
       fold_xor(std::integral_constant<int, 32>{});
       if (LPP == 16) fold_xor(std::integral_constant<int, 16>{});
-    } else {
+    } else if (S == 1) {
       const bool gather = slot == 0;
       for (int k = 1; k < PPW; k++) {
         const int src = (lane + k * LPP) & 63;
@@ -1240,14 +1241,16 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     }
     // Merge the four waves' states in LDS (the rows and q there are no
     // longer read once every wave is past this barrier) and write one
-    // partial per head.  LDS: [wave][head][kPartHead + HD] floats.
+    // partial per head.  LDS: [wave][slot][head][kPartHead + HD] floats, S
+    // slots per wave (1 when the wave folded them).
     constexpr int pstr = kPartHead + HD;
     __syncthreads();
     float *ws = reinterpret_cast<float *>(lds);
-    if (slot == 0) {
+    if (S > 1 ? lane_on : slot == 0) {
+      const int st = wave * S + (S > 1 ? slot : 0);
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        float *pw = ws + ((size_t)wave * n_heads + (size_t)(g * G + i)) * pstr;
+        float *pw = ws + ((size_t)st * n_heads + (size_t)(g * G + i)) * pstr;
         if (c == 0) {
           pw[0] = m[i];
           pw[1] = l[i];
@@ -1261,16 +1264,15 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     __syncthreads();
     // (four elements of one head per thread and step)
     const size_t wstr = (size_t)n_heads * pstr;
+    const int NW = kWavesPerSplit * S;
     for (int e4 = threadIdx.x; e4 < n_heads * (HD / 4); e4 += blockDim.x) {
       const int h = e4 / (HD / 4), d = 4 * (e4 - h * (HD / 4));
       const float *pw = ws + (size_t)h * pstr;
       float M = pw[0];
-#pragma unroll
-      for (int w = 1; w < kWavesPerSplit; w++) M = fmaxf(M, pw[w * wstr]);
+      for (int w = 1; w < NW; w++) M = fmaxf(M, pw[w * wstr]);
       float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
       float lsum = 0.f;
-#pragma unroll
-      for (int w = 0; w < kWavesPerSplit; w++) {
+      for (int w = 0; w < NW; w++) {
         const float f = exp2f(pw[w * wstr] - M);
         const float4 a = *reinterpret_cast<const float4 *>(pw + w * wstr + kPartHead + d);
         o.x = fmaf(a.x, f, o.x);
@@ -1377,14 +1379,16 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
 
 // ---------------------------------------------------------------- launchers
 
+// (CD elements per lane: the variant's merge states)
+template <int HD, int CD>
 static inline size_t layer_lds_bytes(const ShapeDev &sh, int32_t stage_rows) {
-  return layer_lds_layout(sh, stage_rows).total;
+  return layer_lds_layout(sh, stage_rows, layer_merge_states(sh.n_kv_heads * (HD / CD))).total;
 }
 
 template <int FMT, int HD, int CD, int G, int U, int STG, bool WQ>
 static hipError_t launch_fast_s(const DecodeParams &p, int n_layers, hipStream_t s) {
   const dim3 grid = WQ ? dim3(p.wq_grid) : dim3(p.max_splits, p.n_seq, n_layers);
-  const size_t lds = layer_lds_bytes(p.sh, layer_stage_rows(STG, p.stage_rows));
+  const size_t lds = layer_lds_bytes<HD, CD>(p.sh, layer_stage_rows(STG, p.stage_rows));
   if (p.att)
     hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG, WQ>), grid, dim3(kThreads), lds, s, p);
   else
@@ -1428,7 +1432,7 @@ static int occupancy_of(const ShapeDev &sh, int32_t stage_rows) {
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_layer<FMT, HD, CD, G, 2, false, STG, WQ>,
                                                    kThreads,
-                                                   layer_lds_bytes(sh, layer_stage_rows(STG, stage_rows))) !=
+                                                   layer_lds_bytes<HD, CD>(sh, layer_stage_rows(STG, stage_rows))) !=
       hipSuccess) {
     (void)hipGetLastError();
     return 1;
