@@ -455,16 +455,20 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
-  // Staging pays for Q8_0 rows, whose per-lane block windows overlap; F32
-  // rows are read by the lanes in whole, disjoint 64-byte runs already.  One
-  // layer of one sequence is bound by latency, not bytes: per-lane loads,
-  // whose first trip is in flight during the setup (c2, 8193 positions:
-  // 545 us per layer-serial step against 580 us for staged chunks).
+  // Staging pays for Q8_0 rows, whose per-lane block windows overlap, and
+  // for F32 rows in calls over several layers (staged F32 rows lie
+  // transposed in LDS; c3 all layers 601 against 720 us, c1 85.4 against
+  // 94.9), while one layer of F32 rows streams faster through per-lane loads
+  // (c3 layer-serial 1067 against 1179 us).  One layer of one sequence is
+  // bound by latency, not bytes: per-lane loads, whose first trip is in
+  // flight during the setup (c2, 8193 positions: 545 us per layer-serial
+  // step against 580 us for staged chunks).
   const bool one_unit = n_seq == 1 && n_layers == 1;
-  dp.stage_mode = c->tune_stage < 0          ? 0
-                  : c->tune_stage > 0        ? c->tune_stage
-                  : c->shape.kv_q8 && !one_unit ? kDefaultStageMode
-                                                : 0;
+  dp.stage_mode = c->tune_stage < 0                        ? 0
+                  : c->tune_stage > 0                      ? c->tune_stage
+                  : c->shape.kv_q8 ? (one_unit ? 0 : kDefaultStageMode)
+                  : n_layers > 1                           ? kDefaultStageMode
+                                                           : 0;
   dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
@@ -552,9 +556,11 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   const int64_t wq_slots = tiles                        ? tiles_slots(c, true)
                            : fast && dp.stage_mode != 0 ? slots_for(c, dp, true)
                                                          : 0;
+  // (F32 rows: static splits unless a piece is asked for - c3 all layers
+  // 601 us static against 659 us through the work queue)
   const bool use_wq = !fixed && fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
-                       wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit);
+                       (c->shape.kv_q8 && wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit));
   // k_layer's work queue pulls its chunks straight into LDS (mode 1): 1-2%
   // faster than register staging on the batched configs, while a single
   // sequence's static splits, bound by latency, keep register staging.

@@ -167,16 +167,34 @@ struct LaneOff {
 template <int FMT, int CD>
 struct Codec;
 
+// F32 rows staged in LDS lie transposed within each row: the 16-byte quarter
+// q of lane r (row bytes 64r + 16q) at piece q * lpp + r, lpp = lanes per
+// position = row bytes / 64.  A position's lanes then read consecutive pieces
+// (reading their own 64-byte runs, every fourth lane would hit the same LDS
+// banks).  Piece indices count from the start of a chunk of whole rows.
+__device__ __forceinline__ uint32_t f32_lds_piece(uint32_t g, uint32_t lpp) {
+  const uint32_t P = 4u * lpp, rw = g / P, rem = g - rw * P;
+  return rw * P + (rem & 3u) * lpp + (rem >> 2);  // global piece g -> LDS piece
+}
+__device__ __forceinline__ uint32_t f32_global_piece(uint32_t p, uint32_t lpp) {
+  const uint32_t P = 4u * lpp, rw = p / P, rem = p - rw * P, q = rem / lpp;
+  return rw * P + 4u * (rem - q * lpp) + q;  // LDS piece p -> global piece
+}
+
 // ---- F32 rows: 16 contiguous floats, four 16-byte loads ----
 template <>
 struct Codec<0, 16> {
   struct Raw {
     f32x4 x[4];
   };
-  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+  // o0: the lane's bytes in a row; in a staged (transposed) row its first
+  // quarter at o2 = 16r, the next ones o1 = 16 * lpp apart.
+  static __device__ __forceinline__ LaneOff offsets(int elem0, int lpp) {
     LaneOff o;
     o.o0 = (uint32_t)elem0 * 4u;
-    o.o1 = o.o2 = o.sel = o.sshift = 0;
+    o.o1 = 16u * (uint32_t)lpp;
+    o.o2 = (uint32_t)elem0;
+    o.sel = o.sshift = 0;
     return o;
   }
   // Default cache policy: each of the four loads touches every cache line of
@@ -186,7 +204,14 @@ struct Codec<0, 16> {
 #pragma unroll
     for (int i = 0; i < 4; i++) r.x[i] = gload<f32x4>(row + o.o0 + 16 * i);
   }
+  // a staged row (transposed)
   static __device__ __forceinline__ void load_lds(Raw &r, const uint8_t *row, const LaneOff &o) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      r.x[i] = *reinterpret_cast<const f32x4 *>(row + o.o2 + (uint32_t)i * o.o1);
+  }
+  // a row as the cache holds it, in LDS (the new row)
+  static __device__ __forceinline__ void load_row(Raw &r, const uint8_t *row, const LaneOff &o) {
     const float *p = reinterpret_cast<const float *>(row + o.o0);
 #pragma unroll
     for (int i = 0; i < 4; i++) r.x[i] = f32x4{p[4 * i], p[4 * i + 1], p[4 * i + 2], p[4 * i + 3]};
@@ -214,7 +239,7 @@ struct Codec<1, 32> {
     u32x4 a, b;
     uint32_t c;
   };
-  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+  static __device__ __forceinline__ LaneOff offsets(int elem0, int) {
     const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u;
     LaneOff o;
     o.o0 = (34u * b) & ~3u;
@@ -234,6 +259,9 @@ struct Codec<1, 32> {
     r.a = u32x4{p[0], p[1], p[2], p[3]};
     r.b = u32x4{p[4], p[5], p[6], p[7]};
     r.c = p[8];
+  }
+  static __device__ __forceinline__ void load_row(Raw &r, const uint8_t *row, const LaneOff &o) {
+    load_lds(r, row, o);
   }
   // the 32 int8 quants as 8 aligned dwords, and the block scale
   static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[8], float &scale,
@@ -256,7 +284,7 @@ struct Codec<1, 16> {
     u32x4 a;
     uint32_t c;
   };
-  static __device__ __forceinline__ LaneOff offsets(int elem0) {
+  static __device__ __forceinline__ LaneOff offsets(int elem0, int) {
     const uint32_t b = (uint32_t)elem0 >> 5, odd = b & 1u, h = ((uint32_t)elem0 >> 4) & 1u;
     const uint32_t qstart = 34u * b + 2u + 16u * h;
     LaneOff o;
@@ -277,6 +305,9 @@ struct Codec<1, 16> {
     const uint32_t *p = reinterpret_cast<const uint32_t *>(row + o.o1);
     r.a = u32x4{p[0], p[1], p[2], p[3]};
     r.c = *reinterpret_cast<const uint32_t *>(row + o.o2);
+  }
+  static __device__ __forceinline__ void load_row(Raw &r, const uint8_t *row, const LaneOff &o) {
+    load_lds(r, row, o);
   }
   static __device__ __forceinline__ void quants(const Raw &r, uint32_t (&w)[4], float &scale,
                                                 const LaneOff &o) {
@@ -719,7 +750,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   const int nkv = P.sh.n_kv_heads * HD;
   const size_t nq = (size_t)n_heads * HD;
   const size_t row = P.sh.row_bytes;
-  const LaneOff lo = C::offsets(g * HD + c * CD);
+  const LaneOff lo = C::offsets(g * HD + c * CD, LPP);
   const int stride = kWavesPerSplit * PPW;    // positions between a wave's steps
   const size_t ustep = (size_t)stride * row;  // bytes between them
 
@@ -801,8 +832,11 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the region's reads are done
       for (uint32_t i = 0; 64u * i < np; i++) {
         if (64u * i + (uint32_t)lane < np) {
-          dma16(rk, la + 1024u * i, 16u * (64u * i + (uint32_t)lane));
-          dma16(rv, la + cbytes + 1024u * i, 16u * (64u * i + (uint32_t)lane));
+          // (F32: LDS piece p holds the row piece that lies transposed there)
+          const uint32_t p = 64u * i + (uint32_t)lane;
+          const uint32_t voff = 16u * (FMT == 0 ? f32_global_piece(p, (uint32_t)LPP) : p);
+          dma16(rk, la + 1024u * i, voff);
+          dma16(rv, la + cbytes + 1024u * i, voff);
         }
       }
     };
@@ -1125,8 +1159,9 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
           for (int i = 0; i < kStageLoads; i++) {
             const uint32_t pc = 64u * (uint32_t)i + (uint32_t)lane;
             if (pc < np) {
-              *reinterpret_cast<u32x4 *>(sk + 16u * pc) = rk[i];
-              *reinterpret_cast<u32x4 *>(sv + 16u * pc) = rv[i];
+              const uint32_t lp = FMT == 0 ? f32_lds_piece(pc, (uint32_t)LPP) : pc;
+              *reinterpret_cast<u32x4 *>(sk + 16u * lp) = rk[i];
+              *reinterpret_cast<u32x4 *>(sv + 16u * lp) = rv[i];
             }
           }
         };
@@ -1188,8 +1223,8 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     }
     if (owns_new) {
       typename C::Raw krr[1], vrr[1];
-      C::load_lds(krr[0], rowk, lo);
-      C::load_lds(vrr[0], rowv, lo);
+      C::load_row(krr[0], rowk, lo);
+      C::load_row(vrr[0], rowv, lo);
       const bool valid[1] = {wave == 0 && slot == 0};
       const int tpos[1] = {sd.pos};
       consume(krr, vrr, valid, tpos, std::integral_constant<int, 1>{}, std::true_type{});
