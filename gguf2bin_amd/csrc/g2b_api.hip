@@ -643,10 +643,14 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     // resident workgroups - measured on the 64-sequence SmolLM2 F32 batch
     // (c3): 1304 us per layer-serial step at 0.72 of a round against 1490 us
     // at 0.9, 1559 us at 1.13 and 1458 us at 1.5 rounds
-    const int64_t split_slots = !(fast && dp.stage_rows == 0) ? slots
-                                : one_unit                   ? std::max(1, c->n_cu / 2)
-                                : n_seq == 1                 ? std::max(1, c->n_cu)
-                                                             : slots * 7 / 10;
+    // Staged F32 rows of one sequence count one workgroup per CU as a round
+    // too (c1 all layers: 252 workgroups 83.3 us, 504 84.3-85.9 us).
+    const int64_t split_slots = !fast ? slots
+                                : dp.stage_rows > 0
+                                    ? (n_seq == 1 && !c->shape.kv_q8 ? std::max(1, c->n_cu) : slots)
+                                : one_unit   ? std::max(1, c->n_cu / 2)
+                                : n_seq == 1 ? std::max(1, c->n_cu)
+                                             : slots * 7 / 10;
     int32_t split_len = choose_split(c, std::max<int64_t>(split_slots, 1), n_seq, total_pos,
                                      max_pos, n_layers, fast, min_len);
     if (fast && one_unit && dp.stage_rows == 0 && c->split_override == 0) {
