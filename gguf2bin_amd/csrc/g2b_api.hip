@@ -458,17 +458,17 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // Staging pays for Q8_0 rows, whose per-lane block windows overlap, and
   // for F32 rows in calls over several layers (staged F32 rows lie
   // transposed in LDS; c3 all layers 601 against 720 us, c1 85.4 against
-  // 94.9), while one layer of F32 rows streams faster through per-lane loads
-  // (c3 layer-serial 1067 against 1179 us).  One layer of one sequence is
-  // bound by latency, not bytes: per-lane loads, whose first trip is in
-  // flight during the setup (c2, 8193 positions: 545 us per layer-serial
-  // step against 580 us for staged chunks).
+  // 94.9) and for one layer of a batch of F32 rows once its splits are sized
+  // for it (below; c3 layer-serial 895-899 against 1067 us for per-lane
+  // loads).  One layer of one sequence is bound by latency, not bytes:
+  // per-lane loads, whose first trip is in flight during the setup (c2, 8193
+  // positions: 545 us per layer-serial step against 580 us for staged
+  // chunks).
   const bool one_unit = n_seq == 1 && n_layers == 1;
-  dp.stage_mode = c->tune_stage < 0                        ? 0
-                  : c->tune_stage > 0                      ? c->tune_stage
-                  : c->shape.kv_q8 ? (one_unit ? 0 : kDefaultStageMode)
-                  : n_layers > 1                           ? kDefaultStageMode
-                                                           : 0;
+  dp.stage_mode = c->tune_stage < 0   ? 0
+                  : c->tune_stage > 0 ? c->tune_stage
+                  : one_unit          ? 0
+                                      : kDefaultStageMode;
   dp.stage_rows = fast ? decode_stage_rows(c->sh, dp.tune_chunk, dp.stage_mode) : 0;
   if (dp.stage_rows == 0) dp.stage_mode = 0;
   dp.n_layers_call = n_layers;
@@ -645,9 +645,19 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
     // at 0.9, 1559 us at 1.13 and 1458 us at 1.5 rounds
     // Staged F32 rows of one sequence count one workgroup per CU as a round
     // too (c1 all layers: 252 workgroups 83.3 us, 504 84.3-85.9 us).
+    // Staged F32 rows of one layer of a batch: about 0.78 of the resident
+    // workgroups, counting half a split per sequence for the ragged ends (c3,
+    // 64 sequences, 73527 positions, 512 slots: 405 workgroups of 201
+    // positions; layer-serial 895 us at 405-414 workgroups, 913-922 at
+    // 363-387, 1127-1173 at 428-492, 948-990 at 286-319).
+    const int64_t f32_batch_slots =
+        std::max<int64_t>(slots / 8, slots * 78 / 100 - (int64_t)n_seq / 2);
     const int64_t split_slots = !fast ? slots
                                 : dp.stage_rows > 0
-                                    ? (n_seq == 1 && !c->shape.kv_q8 ? std::max(1, c->n_cu) : slots)
+                                    ? (c->shape.kv_q8  ? slots
+                                       : n_seq == 1    ? std::max(1, c->n_cu)
+                                       : n_layers == 1 ? f32_batch_slots
+                                                       : slots)
                                 : one_unit   ? std::max(1, c->n_cu / 2)
                                 : n_seq == 1 ? std::max(1, c->n_cu)
                                              : slots * 7 / 10;

@@ -419,7 +419,7 @@ hipError_t launch_decode(const DecodeParams &p, int n_layers, hipStream_t s, boo
   }
   if (used_fast) *used_fast = 0;
   if (p.split_len > kGenericMaxSplit) return hipErrorInvalidValue;
-  dim3 grid(p.max_splits, p.n_seq, n_layers);
+  const dim3 grid = static_grid(p, n_layers);
   hipLaunchKernelGGL(k_decode_generic, grid, dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }

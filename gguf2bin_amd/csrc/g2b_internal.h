@@ -145,6 +145,18 @@ struct DecodeParams {
   int32_t direct_out;
   int32_t *span_ctr;  // k_short with several spans: [L][n_seq][n_kv_heads] tickets
 };
+// Grid of a static schedule: x = the splits of a (sequence, layer), the
+// fastest index of the linear workgroup order, which the device deals to its
+// eight XCDs in turn.  With an even x, sequence q's first split lands on XCD
+// (x*q) mod 8 - a few XCDs only - and in a ragged batch its short sequences'
+// splits crowd those (c3, 12 splits: 1.28x the average work on the busiest
+// XCD).  An odd x (one empty split per sequence more: t0 >= pos+1 for every
+// sequence, so it returns at once) starts the sequences on every XCD.
+inline dim3 static_grid(const DecodeParams &p, int n_layers) {
+  const int x = p.n_seq > 1 ? (p.max_splits | 1) : p.max_splits;
+  return dim3((unsigned)x, (unsigned)p.n_seq, (unsigned)n_layers);
+}
+
 constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte line each
 constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit
 constexpr int kWqMinParts = 16;  // partial slots per unit at least

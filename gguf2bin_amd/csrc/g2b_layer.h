@@ -1422,7 +1422,7 @@ static inline size_t layer_lds_bytes(const ShapeDev &sh, int32_t stage_rows) {
 
 template <int FMT, int HD, int CD, int G, int U, int STG, bool WQ>
 static hipError_t launch_fast_s(const DecodeParams &p, int n_layers, hipStream_t s) {
-  const dim3 grid = WQ ? dim3(p.wq_grid) : dim3(p.max_splits, p.n_seq, n_layers);
+  const dim3 grid = WQ ? dim3(p.wq_grid) : static_grid(p, n_layers);
   const size_t lds = layer_lds_bytes<HD, CD>(p.sh, layer_stage_rows(STG, p.stage_rows));
   if (p.att)
     hipLaunchKernelGGL((k_layer<FMT, HD, CD, G, U, true, STG, WQ>), grid, dim3(kThreads), lds, s, p);

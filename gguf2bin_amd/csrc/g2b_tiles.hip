@@ -11,7 +11,7 @@ bool tiles_available(const ShapeDev &sh) {
 
 template <int G, bool WQ>
 static hipError_t launch_tiles_g(const DecodeParams &p, int n_layers, hipStream_t s) {
-  const dim3 grid = WQ ? dim3(p.wq_grid) : dim3(p.max_splits, p.n_seq, n_layers);
+  const dim3 grid = WQ ? dim3(p.wq_grid) : static_grid(p, n_layers);
   hipLaunchKernelGGL((k_tiles<G, WQ>), grid, dim3(kThreads), tiles_lds_layout(p.sh).total, s, p);
   return hipGetLastError();
 }
