@@ -42,7 +42,8 @@ __device__ float block_reduce(float x, bool is_max, float *scratch) {
 __global__ __launch_bounds__(kThreads) void k_decode_generic(DecodeParams P) {
   __shared__ float sc[kGenericMaxSplit];
   __shared__ float red[kThreads / 64];
-  const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+  const int split = blockIdx.x, li = blockIdx.z;
+  const int seq = static_seq((int)blockIdx.y, li, P.n_seq);
   const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
   const int npos = sd.pos + 1;
   const int t0 = split * P.split_len;

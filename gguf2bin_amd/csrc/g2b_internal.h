@@ -156,6 +156,15 @@ inline dim3 static_grid(const DecodeParams &p, int n_layers) {
   const int x = p.n_seq > 1 ? (p.max_splits | 1) : p.max_splits;
   return dim3((unsigned)x, (unsigned)p.n_seq, (unsigned)n_layers);
 }
+// The sequence of static-schedule workgroup (y, z) = (blockIdx.y, layer):
+// rotated by the layer.  With n_seq a multiple of 8, workgroup (s, y, z)
+// lands on XCD (s + x*y) mod 8 in every layer, so without the rotation each
+// sequence would run on the same XCD in all layers of a call (c3 over 30
+// layers, one split each: the busiest XCD held 1.18x the average work).
+__device__ __forceinline__ int static_seq(int y, int z, int n_seq) {
+  const int s = y + z;
+  return s < n_seq ? s : s % n_seq;
+}
 
 constexpr int kWqStride = 32;    // int32 per unit counter pair: one 128-byte line each
 constexpr int kWqStealMin = 2;   // unclaimed pieces a unit needs to be worth a visit

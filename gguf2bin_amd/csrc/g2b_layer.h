@@ -1337,7 +1337,8 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
   };
 
   if constexpr (!WQ) {
-    const int split = blockIdx.x, seq = blockIdx.y, li = blockIdx.z;
+    const int split = blockIdx.x, li = blockIdx.z;
+    const int seq = static_seq((int)blockIdx.y, li, P.n_seq);
     const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
     const int npos = sd.pos + 1;
     const int t0 = split * P.split_len;
