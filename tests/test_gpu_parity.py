@@ -320,6 +320,28 @@ def test_static_splits_without_weights(gpu_device, name):
     run_batch_case(o, [1, 20, 33], [0, 19, 32], seed=33, fused=True, want_att=False, tune=tune)
 
 
+@pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3", "llama3_q8_g4"])
+@pytest.mark.parametrize("split,stage", [(64, 0), (100, 0), (100, 2), (128, 2)])
+def test_static_grid_odd_splits_and_layer_rotation(gpu_device, name, split, stage):
+    """Static schedules launch an odd number of splits per sequence (an even
+    count gets one empty split more) and rotate each layer's sequences over
+    the grid's y index.  Eight ragged sequences, three layers in one call (so
+    the rotation wraps) and layer by layer, splits of 64/128 positions (9 and
+    5 per sequence: odd already) and 100 (6: one empty split added), per-lane
+    and staged rows: against the oracle, KV bytes bit for bit."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(3, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    caps = [1, 40, 130, 300, 513, 64, 257, 100]
+    poss = [c - 1 for c in caps]
+    tune = (split, 0, stage, -1)
+    print(f"[grid] {name} split={split} stage={stage}", flush=True)
+    for fused in (True, False):
+        sched = {}
+        run_batch_case(o, caps, poss, seed=41 + split, fused=fused, want_att=False, tune=tune,
+                       sched=sched)
+        assert sched["split_len"] == split and sched["max_splits"] == -(-513 // split), sched
+
+
 @pytest.mark.parametrize("q8", [False, True])
 @pytest.mark.parametrize("norm", [False, True])
 def test_stepping_across_splits(gpu_device, q8, norm):
