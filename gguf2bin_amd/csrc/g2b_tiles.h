@@ -52,8 +52,12 @@ constexpr int kTileRows = kTilesRows;  // positions per tile (the MFMA's 16 colu
 constexpr int kTilesKvPerWave = 2;
 constexpr int kTilesHd = 128;
 // A tile tensor (16 K or V rows) in LDS: rows of 68 16-byte slots of data
-// and one of padding.
-constexpr int kTilesRowSlots = 69;
+// and G2B_TILES_PAD of padding.
+constexpr int kTilesRowData = 68;
+#ifndef G2B_TILES_PAD
+#define G2B_TILES_PAD 1
+#endif
+constexpr int kTilesRowSlots = kTilesRowData + G2B_TILES_PAD;
 constexpr uint32_t kTilesLdsRow = 16u * kTilesRowSlots;
 constexpr int kTilesSlots = kTileRows * kTilesRowSlots;   // per tensor
 constexpr int kTilesLoadsT = (kTilesSlots + 63) / 64;     // 1 KiB loads per tensor
@@ -67,7 +71,7 @@ constexpr uint32_t kTilesTileBytes = 2u * kTilesTensorBytes;
 __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
   if (!sh.kv_q8 || sh.head_dim != kTilesHd) return false;
   if (sh.n_kv_heads != kWavesPerSplit * kTilesKvPerWave) return false;
-  if (sh.row_bytes != 16u * (kTilesRowSlots - 1)) return false;
+  if (sh.row_bytes != 16u * kTilesRowData) return false;
   if (sh.n_heads % sh.n_kv_heads) return false;
   const int g = sh.n_heads / sh.n_kv_heads;
   return g >= 3 && g <= 4;
@@ -89,8 +93,13 @@ struct TilesLds {
   uint32_t kr, dig, vr, rows, row_pad, scr;  // (relative to scr0)
   uint32_t px, buf1, total;                   // (absolute)
 };
+// The exchange holds one group of kTileRows x 4 floats per (KV head, block),
+// kTilesPxGroup floats apart: the V loop's lanes read the eight groups at the
+// same position together, and at 64 floats (256 bytes) apart those reads all
+// fell on the same four banks.
+constexpr int kTilesPxGroup = kTileRows * 4 + 4;
 __host__ __device__ inline uint32_t tiles_px_floats() {
-  return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTileRows * 4 + kTilesKvPerWave * 4);
+  return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTilesPxGroup + kTilesKvPerWave * 4);
 }
 __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
@@ -150,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
   uint8_t *rowk = sb + ll.rows, *rowv = rowk + ll.row_pad;
   float *scr = reinterpret_cast<float *>(sb + ll.scr);
   float *px = reinterpret_cast<float *>(lds + ll.px) + (size_t)wave * tiles_px_floats();
-  float *pfac = px + KPW * NB * TP * 4;  // [kv][head] rescale factors
+  float *pfac = px + KPW * NB * kTilesPxGroup;  // [kv][head] rescale factors
   auto buf = [&](int k) { return lds + (k ? ll.buf1 : 0u); };
 
   // This wave's tile loads u: load j = wave + 4u of the tile, tensor j / 18
@@ -166,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     const int sl = 64 * (j % kTilesLoadsT) + lane;
     const int r = sl / kTilesRowSlots, c = sl - r * kTilesRowSlots;
     goff[u] = (uint32_t)r * row + 16u * (uint32_t)c;
-    if (sl < kTilesSlots && c < kTilesRowSlots - 1) gon |= 1u << u;
+    if (sl < kTilesSlots && c < kTilesRowData) gon |= 1u << u;
   }
 
   // lane roles: MFMA row / column (A row, B and C column = position) and
@@ -339,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
           const uint32_t blk = (uint32_t)(kvg * NB + b);
           const uint32_t sw = *reinterpret_cast<const uint32_t *>(vrow + ((34u * blk) & ~3u));
           const float vs = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
-          px[((kk * NB + b) * TP + col) * 4 + quarter] = p * vs;
+          px[(kk * NB + b) * kTilesPxGroup + col * 4 + quarter] = p * vs;
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -353,7 +362,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
 #pragma unroll
           for (int j = 0; j < 4; j++) acc[h][j] *= fa[h];
       }
-      const float *pv = px + (vkv * NB + vblk) * TP * 4;
+      const float *pv = px + (vkv * NB + vblk) * kTilesPxGroup;
       auto vstep = [&](int t) {
         const float4 p4 = *reinterpret_cast<const float4 *>(pv + t * 4);
         const uint32_t *w = reinterpret_cast<const uint32_t *>(V + (size_t)t * stride + valn);
