@@ -320,6 +320,26 @@ def test_static_splits_without_weights(gpu_device, name):
     run_batch_case(o, [1, 20, 33], [0, 19, 32], seed=33, fused=True, want_att=False, tune=tune)
 
 
+@pytest.mark.parametrize("name", ["qwen3_q8_g2", "qwen3_f32_g2", "smollm2_f32_g3", "hd64_q8_g3"])
+@pytest.mark.parametrize("split", [8, 16, 28])
+def test_many_partials_merge_bit_exact(gpu_device, name, split):
+    """33-256 partials per head (k_combine's one-round merge): one sequence of
+    900 positions in 113 / 57 / 33 splits against the oracle, and the same
+    output bits with and without the weights output (the weights are a
+    separate pass over the raw scores)."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    tune = (split, 0, 0, -1)
+    print(f"[merge] {name} split={split}", flush=True)
+    sched = {}
+    plain = run_batch_case(o, [900], [899], seed=61, fused=False, want_att=False, tune=tune,
+                           kernel=1, sched=sched)
+    assert sched["max_splits"] == -(-900 // split) > 32, sched
+    with_w = run_batch_case(o, [900], [899], seed=61, fused=False, want_att=True, tune=tune,
+                            kernel=1)
+    assert np.array_equal(plain.view(np.uint32), with_w.view(np.uint32))
+
+
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "smollm2_f32_g3", "llama3_q8_g4"])
 @pytest.mark.parametrize("split,stage", [(64, 0), (100, 0), (100, 2), (128, 2)])
 def test_static_grid_odd_splits_and_layer_rotation(gpu_device, name, split, stage):
