@@ -52,12 +52,9 @@ constexpr int kTileRows = kTilesRows;  // positions per tile (the MFMA's 16 colu
 constexpr int kTilesKvPerWave = 2;
 constexpr int kTilesHd = 128;
 // A tile tensor (16 K or V rows) in LDS: rows of 68 16-byte slots of data
-// and G2B_TILES_PAD of padding.
+// and one of padding (a pitch of 71 slots measured the same).
 constexpr int kTilesRowData = 68;
-#ifndef G2B_TILES_PAD
-#define G2B_TILES_PAD 1
-#endif
-constexpr int kTilesRowSlots = kTilesRowData + G2B_TILES_PAD;
+constexpr int kTilesRowSlots = kTilesRowData + 1;
 constexpr uint32_t kTilesLdsRow = 16u * kTilesRowSlots;
 constexpr int kTilesSlots = kTileRows * kTilesRowSlots;   // per tensor
 constexpr int kTilesLoadsT = (kTilesSlots + 63) / 64;     // 1 KiB loads per tensor
@@ -87,7 +84,7 @@ __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
 // planes, which are written only after the sums (the v copy is written before
 // them, so it stays clear).  The exchange overlaps only q and k, dead by the
 // time the owner consumes its new row; buffer 1 is loaded after a barrier
-// that follows that.  ~77 KiB for Llama-3-8B's heads: two workgroups per CU.
+// that follows that.  ~78 KiB for Llama-3-8B's heads: two workgroups per CU.
 struct TilesLds {
   uint32_t scr0;                              // the setup scratch (absolute)
   uint32_t kr, dig, vr, rows, row_pad, scr;  // (relative to scr0)
