@@ -106,6 +106,23 @@ def launch_bytes(s: attn.Shape, poss, layers_per_launch: int) -> int:
     return step_bytes(s, poss) // s.n_layers * layers_per_launch
 
 
+def source_digest() -> str:
+    """sha256 (first 16 hex digits) of the library's device and host sources
+    (gguf2bin_amd/csrc, gguf2bin_amd/host, include): the build a committed
+    profile was measured on records it, and a run compares it with its own
+    (the GPU box gets the tree without its git history)."""
+    import hashlib
+    h = hashlib.sha256()
+    for d in ("gguf2bin_amd/csrc", "gguf2bin_amd/host", "include"):
+        base = os.path.join(ROOT, d)
+        for name in sorted(os.listdir(base)):
+            if name.endswith((".h", ".hip", ".c")):
+                h.update(f"{d}/{name}\0".encode())
+                with open(os.path.join(base, name), "rb") as f:
+                    h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def load_traffic(workload: str, kernel: str):
     """HBM bytes per launch of the workload's decode kernel, measured with
     rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE) and scaled by a copy kernel of
@@ -225,14 +242,25 @@ class Workload:
             f"{gbps:.1f} GB/s, {100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak; decode kernel "
             f"{dn} launches, avg {dec_ms * 1e3:.2f} us, {dec_gbps:.1f} GB/s")
         traffic = load_traffic(self.name, sched["kernel"])
-        roof = {"bound": "hbm", "kernel": traffic.get("kernel") if traffic else sched["kernel"],
+        # the committed traffic counts only where they were measured on this
+        # kernel instance and these sources
+        digest = source_digest()
+        current = bool(traffic) and traffic.get("kernel") == sched["variant"] and \
+            traffic.get("source_digest") == digest
+        roof = {"bound": "hbm", "kernel": sched["variant"],
                 "achieved": round(dec_gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(dec_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": per_launch,
                 "avg_launch_us": round(dec_ms * 1e3, 3),
-                "traffic": traffic.get("hbm_bytes_per_launch") if traffic else None}
+                "traffic": traffic.get("hbm_bytes_per_launch") if current else None,
+                "source_digest": digest}
         if traffic:
             roof["traffic_source"] = traffic.get("source")
-            roof["traffic_over_algorithmic"] = traffic.get("traffic_over_algorithmic")
+            roof["traffic_profile"] = {"kernel": traffic.get("kernel"),
+                                       "commit": traffic.get("commit"),
+                                       "source_digest": traffic.get("source_digest"),
+                                       "matches_this_run": current}
+            if current:
+                roof["traffic_over_algorithmic"] = traffic.get("traffic_over_algorithmic")
         out = {"workload": self.desc, "n_seq": self.n_seq,
                "ctx_min": min(self.poss), "ctx_max": max(self.poss),
                "us_per_step": round(ms * 1e3, 2), "GBps": round(gbps, 2),
@@ -527,11 +555,10 @@ def model_leg(args):
             for i in range(4, 4 + K):
                 m.forward(ltoks[i], P0 + i)
             ldt = (time.perf_counter() - t0) / K
-            sched = (C.c_int32 * 6)()
+            sched = (C.c_int32 * attn.SCHED_FIELDS)()
             attn.lib().g2b_ctx_last_schedule(mctx, sched)
-            lsched = {"kernel": attn.Context.KERNEL_NAMES.get(sched[0], "none"),
-                      "split_len": sched[1], "max_splits": sched[3], "workgroups": sched[4],
-                      "output_in_kernel": bool(sched[5])}
+            lsched = attn.schedule_dict(attn.Shape(cfg["n_layers"], 16, 8, 128, 1e6,
+                                                   attn.ARCH_QWEN3, True), sched)
             kv_cap = cap
         res = {"workload": "Qwen3-0.6B shape, random Q8_0 weights (tied embeddings, QK-RMSNorm), "
                            "Q8_0 KV, batch 1",

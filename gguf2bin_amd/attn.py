@@ -318,6 +318,31 @@ def rope_table(pos0: int, n_pos: int, head_dim: int, theta: float) -> np.ndarray
     return out[:n_pos, :head_dim]
 
 
+SCHED_FIELDS = 9  # G2B_SCHED_FIELDS
+KERNEL_NAMES = {1: "k_layer", 2: "k_tiles", 3: "k_short", 4: "k_decode_generic"}
+
+
+def schedule_dict(shape: Shape, a) -> dict:
+    """g2b_ctx_last_schedule's fields as a dict, with "variant": the kernel
+    instance they name for this shape (include/g2b_synth.h)."""
+    kernel = KERNEL_NAMES.get(a[0], "none")
+    wq = "true" if a[2] > 0 else "false"
+    if kernel == "k_layer":
+        variant = (f"k_layer<{1 if shape.kv_q8 else 0}, {shape.head_dim}, {a[7]}, "
+                   f"{shape.n_heads // shape.n_kv_heads}, 2, {'true' if a[8] else 'false'}, "
+                   f"{a[6]}, {wq}>")
+    elif kernel == "k_tiles":
+        variant = f"k_tiles<{shape.n_heads // shape.n_kv_heads}, {wq}>"
+    elif kernel == "k_short":
+        variant = f"k_short<{1 if shape.kv_q8 else 0}, {shape.head_dim}>"
+    else:
+        variant = kernel
+    return {"kernel": kernel, "split_len": a[1], "piece_len": a[2], "max_splits": a[3],
+            "workgroups": a[4], "output_in_kernel": bool(a[5]),
+            "staging": {0: "per-lane loads", 1: "LDS DMA", 2: "register staging"}.get(a[6], "?"),
+            "chunk": a[7], "weights": bool(a[8]), "variant": variant}
+
+
 def stream_seed(base: int, seq: int, layer: int, tensor: int) -> int:
     return int(lib().g2b_stream_seed(base & 0xFFFFFFFFFFFFFFFF, seq, layer, tensor))
 
@@ -485,15 +510,13 @@ class Context:
         """0 automatic, 1 k_layer only, 2 k_tiles where it applies, 3 spanned k_short."""
         self._check(lib().g2b_ctx_tune_kernel(self.h, kernel), "g2b_ctx_tune_kernel")
 
-    KERNEL_NAMES = {1: "k_layer", 2: "k_tiles", 3: "k_short", 4: "k_decode_generic"}
+    KERNEL_NAMES = KERNEL_NAMES
 
     def last_schedule(self) -> dict:
         """The last decode call's schedule (g2b_ctx_last_schedule)."""
-        a = (C.c_int32 * 6)()
+        a = (C.c_int32 * SCHED_FIELDS)()
         self._check(lib().g2b_ctx_last_schedule(self.h, a), "g2b_ctx_last_schedule")
-        return {"kernel": self.KERNEL_NAMES.get(a[0], "none"), "split_len": a[1],
-                "piece_len": a[2], "max_splits": a[3], "workgroups": a[4],
-                "output_in_kernel": bool(a[5])}
+        return schedule_dict(self.shape, a)
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")

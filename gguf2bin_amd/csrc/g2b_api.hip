@@ -315,13 +315,17 @@ int span_counters(g2b_ctx *c, size_t n) {
 }
 
 void set_sched(g2b_ctx *c, int32_t kernel, int32_t split_len, int32_t piece_len,
-               int32_t max_splits, int64_t grid, bool direct) {
+               int32_t max_splits, int64_t grid, bool direct, int32_t staging = 0,
+               int32_t chunk = 0, bool weights = false) {
   c->sched[0] = kernel;
   c->sched[1] = split_len;
   c->sched[2] = piece_len;
   c->sched[3] = max_splits;
   c->sched[4] = (int32_t)std::min<int64_t>(grid, INT32_MAX);
   c->sched[5] = direct ? 1 : 0;
+  c->sched[6] = staging;
+  c->sched[7] = chunk;
+  c->sched[8] = weights ? 1 : 0;
 }
 
 // With g2b_ctx_profile on: records the first of two timing events around
@@ -730,9 +734,13 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   } else {
     G2B_HIP(c, launch_decode(dp, n_layers, c->stream, fast, &used_fast));
   }
+  // (what launch_layer instantiates: staging only with whole 16-byte row
+  // pieces; k_tiles always pulls its tiles into LDS by DMA)
+  const int32_t staging = tiles ? 1 : used_fast && dp.stage_rows > 0 ? dp.stage_mode : 0;
   set_sched(c, tiles ? G2B_KERNEL_TILES : used_fast ? G2B_KERNEL_LAYER : G2B_KERNEL_GENERIC,
             dp.split_len, use_wq ? dp.piece_len : 0, max_splits,
-            use_wq ? slots : (int64_t)max_splits * n_seq * n_layers, direct && used_fast);
+            use_wq ? slots : (int64_t)max_splits * n_seq * n_layers, direct && used_fast,
+            staging, used_fast && !tiles ? decode_chunk(c->sh, dp.tune_chunk) : 0, att != nullptr);
   if (ev1) G2B_HIP(c, hipEventRecord(ev1, c->stream));
   if (!direct || !used_fast) G2B_HIP(c, launch_combine(dp, n_layers, c->stream));
   if (use_wq) {

@@ -351,6 +351,11 @@ int32_t decode_ppw(const ShapeDev &sh, int32_t tune_chunk) {
   return lpp >= 1 && lpp <= 64 ? 64 / lpp : 1;
 }
 
+int32_t decode_chunk(const ShapeDev &sh, int32_t tune_chunk) {
+  if (!decode_fast_available(sh)) return 0;
+  return tune_chunk == 16 ? 16 : fast_chunk(sh);
+}
+
 int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode) {
   if (!decode_fast_available(sh)) return 0;
   return stage_rows_of(sh.row_bytes, decode_ppw(sh, tune_chunk), mode);

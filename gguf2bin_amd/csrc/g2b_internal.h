@@ -247,6 +247,9 @@ int decode_blocks_per_cu(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_m
 int32_t decode_stage_rows(const ShapeDev &sh, int32_t tune_chunk, int32_t mode);
 // Positions per wave-step of the specialised kernel (1 for other shapes).
 int32_t decode_ppw(const ShapeDev &sh, int32_t tune_chunk);
+// Row elements per lane of the k_layer variant launch_layer picks (its CD:
+// 32 = a Q8_0 block for groups up to 2, else 16), 0 for other shapes.
+int32_t decode_chunk(const ShapeDev &sh, int32_t tune_chunk);
 // Staging mode k_layer uses unless tuned otherwise.
 constexpr int32_t kDefaultStageMode = 2;
 // k_layer for one (KV format 0 = F32 / 1 = Q8_0, head_dim, GQA group),

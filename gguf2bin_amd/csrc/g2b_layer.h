@@ -96,38 +96,37 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // the range check is offset < the resource's byte count).
 constexpr int32_t kBufferRsrcWord3 = 0x00020000;
 
-// Streamed chunks go straight into LDS and work-queue claims return
-// through inline assembly, so that the compiler's wait-count bookkeeping
-// does not see them: it waits for every LDS DMA before any LDS read (which
-// would serialise each chunk's loads with the consumption of the one before),
-// and loads or claims issued on some loop paths and not others made it wait
-// for everything (vmcnt(0)) inside the consume phase.  The kernels wait for
-// them themselves, with s_waitcnt vmcnt(0) before each chunk is read.
+// Streamed chunks go straight into LDS through inline assembly, so that the
+// compiler's wait-count bookkeeping does not see them: it waits for every
+// LDS DMA before any LDS read (which would serialise each chunk's loads with
+// the consumption of the one before).  The kernels wait for them themselves,
+// with s_waitcnt vmcnt(0) (wait_vm0) before each chunk is read.  Loads the
+// compiler cannot see only make its own waits stricter than they need be
+// (vmcnt counts in issue order), never too weak.
 //
 // 16 bytes per lane from buffer resource rsrc at byte voff into LDS at
-// lds_addr + 16 * lane, non-temporal (M0 holds the LDS address).
+// lds_addr + 16 * lane, non-temporal (M0 holds the LDS address).  M0 is on
+// the clobber list: the statement becomes a definition of M0, so the compiler
+// re-initialises M0 before any later instruction of its own that reads it
+// (clang warns about clobbering a reserved register; that is the intent).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                :
                : "s"(lds_addr), "v"(voff), "s"(rsrc)
-               : "memory");
+               : "memory", "m0");
 }
-// Lane 0 adds 1 to *ctr (agent scope: global_atomic_add ... sc0, as the
-// compiler issues a relaxed agent-scope fetch_add) and finds the old value in
-// its lane of the result once the atomic completes: the caller reads it
-// (readlane 0) only after an s_waitcnt that covers it.  The other lanes are
-// masked off inside the statement.
-__device__ __forceinline__ int32_t claim_lane0(int32_t *ctr) {
-  int32_t r;
-  uint64_t save;
-  asm volatile(
-      "s_mov_b64 %1, exec\n\t"
-      "s_mov_b64 exec, 1\n\t"
-      "global_atomic_add %0, %2, %3, off sc0\n\t"
-      "s_mov_b64 exec, %1"
-      : "=&v"(r), "=&s"(save)
-      : "v"(ctr), "v"(1)
-      : "memory");
+#pragma clang diagnostic pop
+// A work-queue claim: lane 0 adds 1 to *ctr (a relaxed agent-scope
+// fetch_add, global_atomic_add ... sc0) and holds the old value in its lane
+// of the result; the other lanes hold 0.  The atomic is visible to the
+// compiler, which therefore waits for its result before any read or copy of
+// that register.  The kernels read it (readlane 0) only after a wait_vm0(),
+// so no such wait of the compiler's falls inside a chunk's consumption.
+__device__ __forceinline__ int32_t claim_lane0(int32_t *ctr, int lane) {
+  int32_t r = 0;
+  if (lane == 0) r = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return r;
 }
 // The raw buffer resource of `bytes` bytes at p (p the same in every lane).
@@ -144,14 +143,9 @@ __device__ __forceinline__ i32x4 raw_rsrc(const uint8_t *p, uint32_t bytes) {
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
 }
-// Every vector memory operation of this wave has completed.
+// Every vector memory operation of this wave has completed (the builtin, so
+// the compiler knows it and adds no wait of its own for claims read after it).
 __device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(kWaitVmcnt0); }
-// The same wait, with a and b (results of claim_lane0) passed through it:
-// the compiler cannot tell that such a register is still being written, and
-// would otherwise be free to read it before the wait.
-__device__ __forceinline__ void wait_vm0_claims(int32_t &a, int32_t &b) {
-  asm volatile("s_waitcnt vmcnt(0)" : "+v"(a), "+v"(b) : : "memory");
-}
 
 // Online softmax: how far (log2 units) a score may exceed the reference
 // before the accumulators are rescaled.
@@ -319,17 +313,32 @@ struct Codec<1, 16> {
 };
 
 // q for the integer K dot products: each q value of a (head, chunk) becomes
-// m = rint(q * 2^(22-e)) with 2^e > max|q| (so |m| <= 2^22, 23 bits of the
-// chunk maximum), split into three signed base-256 digits packed four per
-// dword.  sum_j m_j k_j is then three chains of v_dot4_i32_i8 (exact in
-// int32) and one fp32 rounding; the quantisation of q costs at most
-// 2^-23 * max|q| per element, less than an fp32 FMA chain over the same
-// int8 values loses.
+// m = rint(q * 2^(kQBits-e)) with 2^e > max|q| (so |m| <= 2^30: 31 bits of
+// the chunk maximum), split into kQPlanes signed base-256 digits packed four
+// per dword.  sum_j m_j k_j is then kQPlanes chains of v_dot4_i32_i8 (exact
+// in int32) and one fp32 combination; the quantisation of q costs at most
+// 2^-31 * max|q| per element, well below what an fp32 FMA chain over the
+// same int8 values loses, also where one element of a chunk is 10^3 times
+// the others (three planes, 23 bits, were not: such a chunk left its other
+// elements ~2^-13 relative precision).
+constexpr int kQPlanes = 4;
+constexpr int kQBits = 8 * kQPlanes - 2;  // 30
 template <int CD>
 struct QDigits {
-  uint32_t d[3][CD / 4];
-  float unit;  // 2^(e-22): value of one m step
+  uint32_t d[kQPlanes][CD / 4];
+  float unit;  // 2^(e-30): value of one m step
 };
+
+// The digits of m (|m| <= 2^30): planes 0..2 in [-128, 127], plane 3 the
+// rest (|d3| <= 64).
+__device__ __forceinline__ void split_digits(int m, int (&d)[kQPlanes]) {
+#pragma unroll
+  for (int p = 0; p < kQPlanes - 1; p++) {
+    d[p] = ((m + 128) & 255) - 128;
+    m = (m - d[p]) >> 8;
+  }
+  d[kQPlanes - 1] = m;
+}
 
 template <int CD>
 __device__ __forceinline__ QDigits<CD> make_digits(const float (&q)[CD]) {
@@ -339,40 +348,71 @@ __device__ __forceinline__ QDigits<CD> make_digits(const float (&q)[CD]) {
   for (int j = 0; j < CD; j++) mx = fmaxf(mx, fabsf(q[j]));
   int e = 0;
   (void)frexpf(mx, &e);
-  const float up = ldexpf(1.f, 22 - e);
-  r.unit = ldexpf(1.f, e - 22);
+  const float up = ldexpf(1.f, kQBits - e);
+  r.unit = ldexpf(1.f, e - kQBits);
 #pragma unroll
-  for (int k = 0; k < 3; k++)
+  for (int k = 0; k < kQPlanes; k++)
 #pragma unroll
     for (int j = 0; j < CD / 4; j++) r.d[k][j] = 0u;
 #pragma unroll
   for (int j = 0; j < CD; j++) {
-    const int m = (int)rintf(q[j] * up);
-    const int d0 = ((m + 128) & 255) - 128;
-    const int m1 = (m - d0) >> 8;
-    const int d1 = ((m1 + 128) & 255) - 128;
-    const int d2 = (m1 - d1) >> 8;
+    int d[kQPlanes];
+    split_digits((int)rintf(q[j] * up), d);
     const int sh = 8 * (j & 3);
-    r.d[0][j >> 2] |= ((uint32_t)d0 & 0xffu) << sh;
-    r.d[1][j >> 2] |= ((uint32_t)d1 & 0xffu) << sh;
-    r.d[2][j >> 2] |= ((uint32_t)d2 & 0xffu) << sh;
+#pragma unroll
+    for (int k = 0; k < kQPlanes; k++) r.d[k][j >> 2] |= ((uint32_t)d[k] & 0xffu) << sh;
   }
   return r;
 }
 
-// sum_j m_j * k_j for the chunk, as a float in units of m.
+// A chunk's value from its plane sums c[p] = sum_j d_pj k_j (at most 32
+// elements: |c[0..2]| <= 32*128*127, |c[3]| <= 32*64*127), in units of m:
+// c3*2^24 + c2*2^16 + c1*2^8 + c0 = (c3*256 + c2) * 65536 + (c1*256 + c0),
+// both parts exact in int32.
+//
+// k_layer takes it times the chunk's scale su (fp16 block scale x 2^(e-30),
+// exact) in one fp32 rounding: fma(hi, su * 65536, lo * su), where (float)hi
+// is exact below 2^24 (it rounds only for chunks near the int8 limits in
+// every element) and lo * su is 2^-16 of the value's scale.  A head's score
+// then adds its chunks in fp32 - a few roundings of the score's size, as
+// many as the reference's fp32 dot (l5_model.c:520-536) has.
+__device__ __forceinline__ float chunk_value(int c0, int c1, int c2, int c3, float su) {
+  const int hi = c3 * 256 + c2, lo = c1 * 256 + c0;
+  return fmaf((float)hi, su * 65536.f, (float)lo * su);
+}
+// k_tiles takes the value exactly in float64 (below 2^43) and sums a head's
+// blocks in float64 before one fp32 rounding: free there, where the VALU
+// does little else per block.
+__device__ __forceinline__ double chunk_value_exact(int c0, int c1, int c2, int c3) {
+  const int hi = c3 * 256 + c2, lo = c1 * 256 + c0;
+  return fma((double)hi, 65536.0, (double)lo);
+}
+
+// The first product of a dot chain, a.b with a zero accumulator: the
+// VOP3P form takes the 0 as an inline constant, where the compiler's
+// v_dot4c (accumulate into the destination) first needs a v_mov of 0 - one
+// VALU instruction per chain, 4% of k_layer's loop.
+__device__ __forceinline__ int sdot4_first(uint32_t a, uint32_t b) {
+  int r;
+  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// sum_j q_j * k_j for the chunk: the integer dot product of the digit planes
+// with the chunk's quants w, times su (chunk_value).
 template <int NW>
-__device__ __forceinline__ float qk_int(const uint32_t (&w)[NW], const uint32_t (&d)[3][NW]) {
-  int s0 = 0, s1 = 0, s2 = 0;
+__device__ __forceinline__ float qk_int(const uint32_t (&w)[NW],
+                                        const uint32_t (&d)[kQPlanes][NW], float su) {
+  int s[kQPlanes];
 #pragma unroll
-  for (int j = 0; j < NW; j++) {
-    s0 = __builtin_amdgcn_sdot4((int)w[j], (int)d[0][j], s0, false);
-    s1 = __builtin_amdgcn_sdot4((int)w[j], (int)d[1][j], s1, false);
-    s2 = __builtin_amdgcn_sdot4((int)w[j], (int)d[2][j], s2, false);
-  }
-  // |s2| <= 32*65*127, so s2*256 + s1 fits in int32
-  const int hi = s2 * 256 + s1;
-  return fmaf((float)hi, 256.f, (float)s0);
+  for (int p = 0; p < kQPlanes; p++) s[p] = sdot4_first(w[0], d[p][0]);
+#pragma unroll
+  for (int j = 1; j < NW; j++)
+#pragma unroll
+    for (int p = 0; p < kQPlanes; p++)
+      s[p] = __builtin_amdgcn_sdot4((int)w[j], (int)d[p][j], s[p], false);
+  static_assert(kQPlanes == 4, "chunk_value takes four planes");
+  return chunk_value(s[0], s[1], s[2], s[3], su);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) {
@@ -461,10 +501,25 @@ __device__ inline void append_new_row(const ShapeDev &sh, const SeqDev &sd, int 
 // elements 4i..4i+3 of head H at float4 [i][H] - so each head's sum reads
 // 16-byte pieces without bank conflicts; dig (DIG) reuses tr once the sums
 // are done, or is digp where the caller gives it (outside qrot, kr and vr):
-// dig_stride<CD>() dwords per chunk, chunk h * (hd / CD) + c.
+// dig_dwords<CD>(n_heads * hd / CD) dwords, chunk h * (hd / CD) + c.  In tr
+// they fit for every shape the specialised kernels take: n_heads * (hd/CD)
+// * (4 * CD/4 + 1) <= hd * (n_heads + n_kv_heads + 1) for CD 16 or 32 and
+// n_heads <= 4 * n_kv_heads.
+// The digit planes of a chunk: dig_stride<CD>() dwords (kQPlanes planes of
+// CD/4 dwords, 16-byte rows); the chunks' units 2^(e-30) follow all the
+// chunks' planes, one float each (dig_unit).
 template <int CD>
-constexpr int dig_stride() {
-  return (3 * (CD / 4) + 1 + 3) & ~3;  // three planes, the unit, 16-byte rows
+__host__ __device__ constexpr int dig_stride() {
+  return kQPlanes * (CD / 4);
+}
+// Where chunk ch's unit lies, and the dwords of n_chunks chunks' digits.
+template <int CD>
+__host__ __device__ constexpr int dig_unit_at(int n_chunks, int ch) {
+  return n_chunks * dig_stride<CD>() + ch;
+}
+template <int CD>
+__host__ __device__ constexpr int dig_dwords(int n_chunks) {
+  return n_chunks * (dig_stride<CD>() + 1);
 }
 
 template <int HD, int CD, bool DIG>
@@ -635,30 +690,26 @@ __device__ inline void visit_setup(const ShapeDev &sh, const SeqDev &sd, int lay
       mx = fmaxf(mx, __shfl_xor(mx, 2));
       int e = 0;
       (void)frexpf(mx, &e);
-      const float up = ldexpf(1.f, 22 - e);
-      uint32_t d[3][QE / 4];
+      const float up = ldexpf(1.f, kQBits - e);
+      uint32_t d[kQPlanes][QE / 4];
 #pragma unroll
-      for (int pl = 0; pl < 3; pl++)
+      for (int pl = 0; pl < kQPlanes; pl++)
 #pragma unroll
         for (int j = 0; j < QE / 4; j++) d[pl][j] = 0u;
 #pragma unroll
       for (int j = 0; j < QE; j++) {
-        const int m = (int)rintf(q[j] * up);
-        const int d0 = ((m + 128) & 255) - 128;
-        const int m1 = (m - d0) >> 8;
-        const int d1 = ((m1 + 128) & 255) - 128;
-        const int d2 = (m1 - d1) >> 8;
+        int dj[kQPlanes];
+        split_digits((int)rintf(q[j] * up), dj);
         const int sh8 = 8 * (j & 3);
-        d[0][j >> 2] |= ((uint32_t)d0 & 0xffu) << sh8;
-        d[1][j >> 2] |= ((uint32_t)d1 & 0xffu) << sh8;
-        d[2][j >> 2] |= ((uint32_t)d2 & 0xffu) << sh8;
+#pragma unroll
+        for (int pl = 0; pl < kQPlanes; pl++) d[pl][j >> 2] |= ((uint32_t)dj[pl] & 0xffu) << sh8;
       }
       uint32_t *o = dig + ch * dig_stride<CD>();
 #pragma unroll
-      for (int pl = 0; pl < 3; pl++)
+      for (int pl = 0; pl < kQPlanes; pl++)
 #pragma unroll
         for (int j = 0; j < QE / 4; j++) o[pl * (CD / 4) + k * (QE / 4) + j] = d[pl][j];
-      if (k == 0) o[3 * (CD / 4)] = __float_as_uint(ldexpf(1.f, e - 22));
+      if (k == 0) dig[dig_unit_at<CD>(nch, ch)] = __float_as_uint(ldexpf(1.f, e - kQBits));
     }
   }
   if (owns_new) {
@@ -898,9 +949,10 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       const uint32_t *dig = reinterpret_cast<const uint32_t *>(trq);
 #pragma unroll
       for (int i = 0; i < G; i++) {
-        const uint32_t *o = dig + ((g * G + i) * (HD / CD) + c) * dig_stride<CD>();
+        const int ch = (g * G + i) * (HD / CD) + c;
+        const uint32_t *o = dig + ch * dig_stride<CD>();
 #pragma unroll
-        for (int pl = 0; pl < 3; pl++)
+        for (int pl = 0; pl < kQPlanes; pl++)
 #pragma unroll
           for (int j = 0; j < CD / 4; j += 4) {
             const uint4 v4 = *reinterpret_cast<const uint4 *>(o + pl * (CD / 4) + j);
@@ -909,7 +961,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
             qd[i].d[pl][j + 2] = v4.z;
             qd[i].d[pl][j + 3] = v4.w;
           }
-        qd[i].unit = __uint_as_float(o[3 * (CD / 4)]);
+        qd[i].unit = __uint_as_float(dig[dig_unit_at<CD>(n_heads * (HD / CD), ch)]);
       }
     } else {
 #pragma unroll
@@ -956,7 +1008,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
           C::quants(kr_[u], w, ks, lo);
 #pragma unroll
           for (int i = 0; i < G; i++) {
-            const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d) * (ks * qd[i].unit));
+            const float s = group_sum<LPH>(qk_int<CD / 4>(w, qd[i].d, ks * qd[i].unit));
             sc[u][i] = (!CHECK || valid[u]) ? s : -INFINITY;
           }
         } else {
@@ -1115,12 +1167,12 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
             consume_region(k, cs0, min(R, tend - cs0));
           }
         } else {
-          // this wave's pieces: a claim (lane 0, in assembly) is issued when
+          // this wave's pieces: a claim (lane 0) is issued when
           // a piece starts and read when it runs out - at a later chunk, so
           // after a wait for all of the wave's loads
-          int32_t c0 = claim_lane0(ctr);
-          int32_t pend = claim_lane0(ctr);
-          wait_vm0_claims(c0, pend);
+          int32_t c0 = claim_lane0(ctr, lane);
+          int32_t pend = claim_lane0(ctr, lane);
+          wait_vm0();
           int pc = __builtin_amdgcn_readlane(c0, 0);
           int cs0 = 0, ce = 0;
           bool live = pc >= 0 && pc < npieces;
@@ -1131,7 +1183,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
             dma_chunk(0, cs0, min(R, ce - cs0));
           }
           for (int k = 0; live; k ^= 1) {
-            wait_vm0_claims(pend, c0);
+            wait_vm0();
             int ns = cs0 + R, nce = ce;
             bool nlive = true;
             if (ns >= ce) {  // next piece
@@ -1141,7 +1193,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
                 piece_range(pm, nc, tend, ns, nce);
                 ns = __builtin_amdgcn_readfirstlane(ns);
                 nce = __builtin_amdgcn_readfirstlane(nce);
-                pend = claim_lane0(ctr);
+                pend = claim_lane0(ctr, lane);
               }
             }
             if (nlive) dma_chunk(k ^ 1, ns, min(R, nce - ns));

@@ -418,9 +418,13 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   // The partials travel through device-coherent accesses: agent-scope
   // atomic stores (write-through to the device's coherence point) that each
   // thread waits for before the barrier, and agent-scope atomic loads in the
-  // merging span.  The ordering comes from the waits and the ticket; no
-  // L2-wide writeback or invalidation is needed (a release fence per wave
-  // cost more than the whole stream here).
+  // merging span.  The ticket orders them: after the barrier (workgroup
+  // scope: every thread's stores happen before it), thread 0 takes the
+  // ticket with an acq_rel agent-scope fetch_add, which releases this
+  // span's partials and, in the span that draws the last ticket, acquires
+  // every other span's before the barrier that precedes the merge.  One
+  // release per workgroup, not per wave (a release fence in every wave cost
+  // more than the whole stream here).
   for (int i = t; i < G * HD; i += kSThreads) {
     const int g = i / HD, e = i - g * HD;
     float *pp = part_of(g, span);
@@ -437,7 +441,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   if (t == 0) {
     int32_t *ctr = P.span_ctr + sidx * (size_t)nkvh + (size_t)kvh;
     const int32_t ticket =
-        __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = ticket == nspans - 1;
     if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last ? 1 : 0;

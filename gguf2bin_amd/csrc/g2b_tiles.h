@@ -5,20 +5,21 @@
 // /root/reference/src/l5_model.c:518-557 for Q8_0 KV caches with head_dim
 // 128, 8 KV heads and 3 or 4 q heads per KV head (Llama-3-8B's shape).  With
 // that many q heads per KV head, k_layer's per-lane integer dot products
-// (three v_dot4 chains per head and 4 bytes) make the loop bound by VALU
+// (four v_dot4 chains per head and 4 bytes) make the loop bound by VALU
 // issue; here one v_mfma_i32_16x16x32_i8 computes, for one 32-element block
-// of one KV head and 16 positions, all G x 3 digit-plane dot products:
+// of one KV head and 16 positions, all G x 4 digit-plane dot products:
 //   A (16 x 32 int8): row 4h + p = digit plane p of q head h of the group
-//                     (plane 3 and heads >= G are zero rows),
+//                     (heads >= G are zero rows),
 //   B (32 x 16 int8): the block's 32 quants of 16 positions (the cache bytes
 //                     as they are),
 //   C (16 x 16 int32): exact sums; lane (h = lane/16, t = lane%16) holds the
-//                     three planes of head h at position t.
-// q is held as three signed int8 digits of a 23-bit fixed point relative to
+//                     four planes of head h at position t.
+// q is held as four signed int8 digits of a 31-bit fixed point relative to
 // each (head, block)'s largest |q| (the digit planes k_layer uses), so the
-// block's score is (d2*65536 + d1*256 + d0)-weighted sums, exact in int32,
-// then one fp32 rounding and the block's fp16 scale; blocks are summed in
-// fp32.  Softmax stays in that layout (each lane one (head, position); the
+// block's score is (d3*2^24 + d2*2^16 + d1*2^8 + d0)-weighted sums, exact in
+// int32 per plane and combined exactly in float64 (chunk_value_exact), times
+// the block's fp16 scale; blocks are summed in float64 and the score is
+// rounded to fp32 once.  Softmax stays in that layout (each lane one (head, position); the
 // running maximum of a head is shared by its 16 lanes through DPP), and V is
 // accumulated on the VALU: lane (KV head of the wave's pair, four dims) takes
 // p * v_scale for its block from a per-wave LDS exchange and does 4 x G FMAs
@@ -101,7 +102,7 @@ __host__ __device__ inline uint32_t tiles_px_floats() {
 __host__ __device__ inline TilesLds tiles_lds_layout(const ShapeDev &sh) {
   const uint32_t nq = (uint32_t)(sh.n_heads * sh.head_dim);
   const uint32_t nkv4 = ((uint32_t)(sh.n_kv_heads * sh.head_dim) * 4u + 15u) & ~15u;
-  const uint32_t digb = (uint32_t)(sh.n_heads * (sh.head_dim / 32) * dig_stride<32>()) * 4u;
+  const uint32_t digb = (uint32_t)dig_dwords<32>(sh.n_heads * (sh.head_dim / 32)) * 4u;
   const uint32_t trb = (uint32_t)(sh.head_dim * (sh.n_heads + sh.n_kv_heads + 1)) * 4u;
   TilesLds l;
   l.kr = nq * 4u;
@@ -216,8 +217,8 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     // in flight during the setup.
     int32_t first = 0, pend = 0;
     if (WQ && wave == 0) {
-      first = claim_lane0(ctr);
-      pend = claim_lane0(ctr);
+      first = claim_lane0(ctr, lane);
+      pend = claim_lane0(ctr, lane);
     }
 
     // [QK-RMSNorm,] RoPE, the digit planes of q (32-element chunks = the
@@ -226,27 +227,29 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
                               P.v_in + sidx * nkv, P.rope, P.norm, P.qscale, qrot, kr, vr, rowk,
                               rowv, scr, trq, digs);
     // A operands: digit plane (col & 3) of head (col >> 2), bytes
-    // 8*quarter .. of block b; and the C lanes' units 2^(e-22) of
+    // 8*quarter .. of block b; and the C lanes' units 2^(e-30) of
     // (head quarter, block b)
     uint64_t qa[KPW][NB];
     float un[KPW][NB];
     {
       const uint32_t *dig = digs;
       constexpr int DS = dig_stride<32>();
+      static_assert(kQPlanes == 4, "A rows 4h + p: four digit planes per head");
       const int ah = col >> 2, ap = col & 3;
+      const int nch = P.sh.n_heads * NB;
 #pragma unroll
       for (int kk = 0; kk < KPW; kk++) {
         const int kvg = wave * KPW + kk;
 #pragma unroll
         for (int b = 0; b < NB; b++) {
           uint64_t a = 0;
-          if (ah < G && ap < 3) {
+          if (ah < G) {
             const uint32_t *o = dig + ((kvg * G + ah) * NB + b) * DS + ap * 8 + 2 * quarter;
             a = (uint64_t)o[0] | ((uint64_t)o[1] << 32);
           }
           qa[kk][b] = a;
           un[kk][b] = quarter < G
-                          ? __uint_as_float(dig[((kvg * G + quarter) * NB + b) * DS + 24])
+                          ? __uint_as_float(dig[dig_unit_at<32>(nch, (kvg * G + quarter) * NB + b)])
                           : 0.f;
         }
       }
@@ -296,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
           const uint32_t sw = *reinterpret_cast<const uint32_t *>(krow + ((34u * blk) & ~3u));
           ks[b] = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
         }
-        float sc = 0.f;
+        double sc = 0.0;  // (exact block values, summed in float64: chunk_value_exact)
 #pragma unroll
         for (int b0 = 0; b0 < NB; b0 += 2) {
           // two at a time (four accumulators would cost the second wave per SIMD)
@@ -307,12 +310,11 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
                                                          i32x4{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
           for (int j = 0; j < 2; j++) {
-            // |c2| <= 32*128*127, so c2*256 + c1 fits in int32
-            const float part = fmaf((float)(c[j][2] * 256 + c[j][1]), 256.f, (float)c[j][0]);
-            sc = fmaf(part, ks[b0 + j] * un[kk][b0 + j], sc);
+            const double part = chunk_value_exact(c[j][0], c[j][1], c[j][2], c[j][3]);
+            sc = fma(part, (double)ks[b0 + j] * (double)un[kk][b0 + j], sc);
           }
         }
-        s[kk] = valid ? sc : -INFINITY;
+        s[kk] = valid ? (float)sc : -INFINITY;
       }
       // online softmax per (KV head, q head): the 16 lanes of a head share
       // its reference m (raised lazily, as k_layer does)
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     auto publish = [&](int t) {  // (wave 0) tile t's descriptor, for all
       if (live && nx >= pe) {
         take_piece(__builtin_amdgcn_readlane(pend, 0));
-        if (live) pend = claim_lane0(ctr);
+        if (live) pend = claim_lane0(ctr, lane);
       }
       int ts = 0, n = 0;
       if (live) {
@@ -427,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     };
     if constexpr (WQ) {
       if (wave == 0) {
-        wait_vm0_claims(first, pend);  // (nothing else of this wave is in flight)
+        wait_vm0();  // (nothing else of this wave is in flight)
         take_piece(__builtin_amdgcn_readlane(first, 0));
         publish(0);
         publish(1);
@@ -445,7 +447,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
     for (int i = 0; n0 > 0; i++) {
       // this wave's loads of tile i are done; after the barrier everyone's
       // are, and everyone is done with tile i-1, whose buffer takes tile i+1
-      wait_vm0_claims(pend, first);
+      wait_vm0();
       __syncthreads();
       int n1 = 0;
       desc(i + 1, ts, n1);

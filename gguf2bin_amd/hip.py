@@ -131,6 +131,13 @@ def copy_d2d(dst: int, src: int, nbytes: int):
     check(lib().hipMemcpy(dst, src, nbytes, _D2D), "D2D")
 
 
+def device_sync():
+    """hipDeviceSynchronize: every stream of the device has drained (a
+    device-to-device hipMemcpy may return before it completes, and the null
+    stream does not order work on non-blocking streams)."""
+    check(lib().hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
 class Event:
     def __init__(self):
         e = C.c_void_p()
@@ -154,3 +161,63 @@ class Event:
                 lib().hipEventDestroy(self.e)
         except Exception:
             pass
+
+
+GRAPH_NODE_KERNEL = 0  # hipGraphNodeTypeKernel
+
+
+class Graph:
+    """A stream capture (hipStreamBeginCapture in thread-local mode ..
+    hipStreamEndCapture) instantiated for replay: fn() issues the work on
+    `stream` while it is captured."""
+
+    def __init__(self, stream, fn):
+        L = lib()
+        for name, args in (("hipStreamBeginCapture", [C.c_void_p, C.c_int]),
+                           ("hipStreamEndCapture", [C.c_void_p, C.POINTER(C.c_void_p)]),
+                           ("hipGraphInstantiate", [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p,
+                                                    C.c_char_p, C.c_size_t]),
+                           ("hipGraphLaunch", [C.c_void_p, C.c_void_p]),
+                           ("hipGraphGetNodes", [C.c_void_p, C.POINTER(C.c_void_p),
+                                                 C.POINTER(C.c_size_t)]),
+                           ("hipGraphNodeGetType", [C.c_void_p, C.POINTER(C.c_int)]),
+                           ("hipGraphExecDestroy", [C.c_void_p]),
+                           ("hipGraphDestroy", [C.c_void_p])):
+            getattr(L, name).argtypes = args
+        self.graph = self.exec = None
+        check(L.hipStreamBeginCapture(stream, 1), "hipStreamBeginCapture")
+        g = C.c_void_p()
+        try:
+            fn()
+        finally:
+            rc = L.hipStreamEndCapture(stream, C.byref(g))
+            self.graph = g.value
+        check(rc, "hipStreamEndCapture")
+        ex = C.c_void_p()
+        check(L.hipGraphInstantiate(C.byref(ex), self.graph, None, None, 0), "hipGraphInstantiate")
+        self.exec = ex.value
+
+    def node_types(self):
+        L = lib()
+        n = C.c_size_t(0)
+        check(L.hipGraphGetNodes(self.graph, None, C.byref(n)), "hipGraphGetNodes")
+        nodes = (C.c_void_p * max(n.value, 1))()
+        check(L.hipGraphGetNodes(self.graph, nodes, C.byref(n)), "hipGraphGetNodes")
+        out = []
+        for i in range(n.value):
+            t = C.c_int(-1)
+            check(L.hipGraphNodeGetType(nodes[i], C.byref(t)), "hipGraphNodeGetType")
+            out.append(t.value)
+        return out
+
+    def launch(self, stream):
+        check(lib().hipGraphLaunch(self.exec, stream), "hipGraphLaunch")
+
+    def destroy(self):
+        L = lib()
+        if self.exec:
+            L.hipGraphExecDestroy(self.exec)
+            self.exec = None
+        if self.graph:
+            L.hipGraphDestroy(self.graph)
+            self.graph = None

@@ -77,9 +77,16 @@ int g2b_ctx_tune_kernel(g2b_ctx *ctx, int32_t kernel);
  *   [3] partial slots per (sequence, layer) (splits, spans or queue slots),
  *   [4] workgroups launched,
  *   [5] 1 when the decode kernel wrote the output itself (no combine launch,
- *       or spans merged in the kernel).
- * All zero before the first call. */
-#define G2B_SCHED_FIELDS 6
+ *       or spans merged in the kernel),
+ *   [6] how KV rows reach the lanes: 0 per-lane loads straight from HBM,
+ *       1 chunks (k_tiles: tiles) pulled into LDS by LDS DMA, 2 chunks
+ *       loaded into registers one chunk ahead and written to LDS,
+ *   [7] k_layer: row elements per lane (32 = a Q8_0 block, 16); else 0,
+ *   [8] 1 when the call wrote the softmax weights.
+ * With the shape, [0], [2], [6], [7] and [8] name the kernel instance
+ * launched: k_layer<kv_q8, head_dim, [7], group, 2, [8], [6], [2] > 0>, or
+ * k_tiles<group, [2] > 0>.  All zero before the first call. */
+#define G2B_SCHED_FIELDS 9
 #define G2B_KERNEL_LAYER 1
 #define G2B_KERNEL_TILES 2
 #define G2B_KERNEL_SHORT 3

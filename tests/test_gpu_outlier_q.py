@@ -1,0 +1,83 @@
+"""Decode attention with outlier q channels: in every head and every
+32-element chunk of it, one channel of q is 10, 10^2 or 10^3 times the
+rest (before RoPE, which mixes it with its pair), with and without
+QK-RMSNorm weights spread over a factor ~10.  Through k_layer (Q8_0 KV with
+whole-block and half-block lanes, head_dim 64 and 128, groups 1-4; F32
+rows) with the softmax weights output, and through k_tiles (groups 3 and 4)
+without it; KV bytes bit-exact with the oracle, outputs within max-abs 1e-4
+of float64 and of the oracle (helpers.check_out).
+
+The weights bar.  The reference computes a score as an fp32 dot times an
+fp32 scale (/root/reference/src/l5_model.c:520-539), so each score carries
+about 2^-24 of its own magnitude, and a weight's relative error is about
+the error of the score difference that sets it.  With a 10^2 channel the
+scores reach tens (log2 units), with 10^3 hundreds: the reference's own
+weights are then 1.5e-5 - 1.3e-4 (relative) away from a float64 evaluation
+of the same bytes, above the 1e-5 bar, and even a score rounded to fp32
+only once is 3e-5 - 7e-5 away at 10^3 (a CPU emulation of the arithmetic).
+So at 10x without QK-RMSNorm the bar is the plain one (relative 1e-5 of
+float64); above it, and with the spread norm weights (which scale channels
+by up to ~10 more), the device must stay in the reference's accuracy class: within 1e-5 plus
+twice the reference's own error (helpers.check_weights, as_accurate_as_ref).
+The Q8_0 kernels hold q as four int8 digit planes of a 31-bit fixed point
+per chunk (exact integer dot products; k_layer rounds a chunk's value to
+fp32 once, k_tiles sums a head's chunks in float64 and rounds once); the
+F32 rows run an fp32 FMA dot like the reference.  Three planes (23 bits)
+were 2-7 times less accurate than the reference at 10^2 and 10^3.
+"""
+import numpy as np
+import pytest
+
+from oracle import orc
+from test_gpu_parity import SHAPES, run_batch_case
+
+pytestmark = pytest.mark.gpu
+
+# name: (n_heads, n_kv_heads, head_dim, arch, q8), kernel (g2b_ctx_tune_kernel), weights output
+CASES = {
+    "qwen3_q8_g2": (SHAPES["qwen3_q8_g2"], 1, True),     # k_layer, whole-block lanes
+    "llama3_q8_g4": (SHAPES["llama3_q8_g4"], 1, True),   # k_layer, half-block lanes
+    "hd64_q8_g3": (SHAPES["hd64_q8_g3"], 1, True),       # k_layer, head_dim 64
+    "mha_q8_g1": (SHAPES["mha_q8_g1"], 1, True),         # k_layer, group 1
+    "qwen3_f32_g2": (SHAPES["qwen3_f32_g2"], 1, True),   # k_layer, F32 rows (fp32 dots)
+    "tiles_g4": ((32, 8, 128, orc.ARCH_LLAMA, True), 2, False),  # k_tiles
+    "tiles_g3": ((24, 8, 128, orc.ARCH_QWEN3, True), 2, False),  # k_tiles
+}
+
+
+def outlier_gain(nq: int, hd: int, factor: float) -> np.ndarray:
+    """nq multipliers: 1, except one channel per (head, 32-element chunk)."""
+    g = np.ones(nq, np.float32)
+    for h in range(nq // hd):
+        for c in range(hd // 32):
+            g[h * hd + c * 32 + (h * 7 + c * 13) % 32] = np.float32(factor)
+    return g
+
+
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("factor", [10.0, 100.0, 1000.0])
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_outlier_q_channels(gpu_device, name, factor, norm):
+    (nh, nkv, hd, arch, q8), kernel, want_att = CASES[name]
+    o = orc.Shape(2, nh, nkv, hd, 5e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    norms = None
+    if norm:
+        seed = 900 + hd + nh
+        qn = np.exp(0.8 * orc.normal(seed, 2 * hd)).astype(np.float32).reshape(2, hd)
+        kn = np.exp(0.8 * orc.normal(seed + 1, 2 * hd)).astype(np.float32).reshape(2, hd)
+        norms = (qn, kn, 1e-6)
+    caps = [1, 37, 300, 700, 129]
+    poss = [0, 36, 211, 650, 64]
+    errs = []
+    print(f"[outlier] {name} x{factor:g} norm={norm}", flush=True)
+    run_batch_case(o, caps, poss, seed=int(factor) + 17 * nh, fused=False, want_att=want_att,
+                   norms=norms, kernel=kernel, q_gain=outlier_gain(o.nq, hd, factor),
+                   w_as_accurate_as_ref=factor > 10.0 or norm, errs=errs)
+    e_out = max(e[0] for e in errs)
+    if want_att:
+        r_w = max(e[1] for e in errs)
+        own = max(e[2] for e in errs)
+        print(f"[outlier] {name} x{factor:g} norm={norm}: max |out - f64| {e_out:.3g}, "
+              f"weights rel {r_w:.3g} (reference's own {own:.3g})", flush=True)
+    else:
+        print(f"[outlier] {name} x{factor:g} norm={norm}: max |out - f64| {e_out:.3g}", flush=True)

@@ -194,7 +194,8 @@ MODES = {
 
 
 def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, norms=None,
-                   setup=None, tune=None, misalign=0, kernel=0, sched=None):
+                   setup=None, tune=None, misalign=0, kernel=0, sched=None, q_gain=None,
+                   w_as_accurate_as_ref=False, errs=None):
     """n_seq ragged sequences, all layers: device (one fused call or layer by
     layer) against the oracle, sequence by sequence.  tune: None or the
     g2b_ctx_tune arguments for the context.  norms: None, or
@@ -204,7 +205,12 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
     is given to do that itself.  misalign: byte offset of q, k and v in their
     device buffers (not a multiple of 16: the generic kernels run).  kernel:
     g2b_ctx_tune_kernel (0 automatic, 1 k_layer only).  sched: None or a
-    dict that receives the last call's schedule (g2b_ctx_last_schedule)."""
+    dict that receives the last call's schedule (g2b_ctx_last_schedule).
+    q_gain: None or nq floats that multiply every q (outlier channels).
+    w_as_accurate_as_ref: the weights' float64 bar (helpers.check_weights).
+    errs: None or a list that receives (max |out - float64|, max relative
+    |w - float64| or None, the oracle's own relative weight error or None)
+    per (sequence, layer)."""
     n_seq, nL = len(caps), o.n_layers
     rng_seed = seed * 1000
     qn, kn, eps = norms if norms else (None, None, 1e-6)
@@ -238,6 +244,8 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
             q = orc.normal(seed + 1, nL * n_seq * o.nq).reshape(nL, n_seq, o.nq)
             k = orc.normal(seed + 2, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
             v = orc.normal(seed + 3, nL * n_seq * o.nkv).reshape(nL, n_seq, o.nkv)
+            if q_gain is not None:
+                q = (q * np.asarray(q_gain, np.float32)).astype(np.float32)
             if misalign:
                 qd, kd, vd = (hip.DeviceBuffer(a.nbytes + 64) for a in (q, k, v))
                 for buf, a in ((qd, q), (kd, k), (vd, v)):
@@ -274,9 +282,15 @@ def run_batch_case(o: orc.Shape, caps, poss, seed, fused: bool, want_att=True, n
             ql, kl = nq_(q[L, i], L), nk_(k[L, i], L)
             ref, ratt = orc.attn_layer(o, c, L, p, kc, vc, ql, kl, v[L, i])
             ex, wex = exact_attention(o, c, L, p, kc, vc, ql)
-            check_out(out[L, i], ref, ex)
+            e_out = check_out(out[L, i], ref, ex)[1]
+            r_w = own_w = None
             if w is not None:
-                check_weights(w[L, i, :, :p + 1], ratt, wex)
+                r_w = check_weights(w[L, i, :, :p + 1], ratt, wex,
+                                    as_accurate_as_ref=w_as_accurate_as_ref)
+                bw = wex > 1e-30
+                own_w = float(np.max(np.abs(ratt[bw] - wex[bw]) / wex[bw]))
+            if errs is not None:
+                errs.append((e_out, r_w, own_w))
         assert np.array_equal(dev_kv[i][0], kc), f"K bytes of sequence {i}"
         assert np.array_equal(dev_kv[i][1], vc), f"V bytes of sequence {i}"
     return out
@@ -292,6 +306,22 @@ def test_batched_ragged_vs_oracle(gpu_device, name, mode):
     fused, tune = MODES[mode]
     print(f"[batch] {name} mode={mode}", flush=True)
     run_batch_case(o, caps, poss, seed=zlib.crc32(name.encode()) % 1000, fused=fused, tune=tune)
+
+
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("arch", [orc.ARCH_LLAMA, orc.ARCH_QWEN3])
+def test_head_dim_over_1024_leaves_q_and_k_unrotated(gpu_device, arch, q8):
+    """head_dim 2048: the reference's RoPE prints a message and leaves q and
+    k as they are (/root/reference/src/l3_math.c:67,86; the oracle's branch
+    is pinned against the compiled reference in test_oracle_golden.py).  The
+    device takes the generic kernels with RoPE off: appended K bytes
+    bit-exact with the oracle's (the unrotated k), outputs and weights
+    within the bars, which fail if q were rotated."""
+    o = orc.Shape(2, 4, 2, 2048, 1e4, arch, q8)
+    print(f"[hd2048] arch={arch} q8={q8}", flush=True)
+    sched = {}
+    run_batch_case(o, [1, 40, 129], [0, 39, 100], seed=2048 + arch, fused=False, sched=sched)
+    assert sched["kernel"] == "k_decode_generic", sched
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "qwen3_f32_g2", "smollm2_f32_g3",

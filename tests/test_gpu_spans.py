@@ -1,6 +1,6 @@
-"""k_short over several spans of 128 positions (the single-sequence path of
-contexts above 128 positions, and any batch under g2b_ctx_tune_kernel(3)):
-each span of a (sequence, layer, KV head) writes its partials, the last to
+"""k_short over several spans of 128 positions, which calls take only under
+g2b_ctx_tune_kernel(3) (the automatic choice runs k_layer's splits past 128
+positions; below 128 positions k_short is a single span): each span of a (sequence, layer, KV head) writes its partials, the last to
 take a ticket merges them and writes the output; no combine launch.
 Against the oracle on the same seeded inputs: K and V bytes bit-exact,
 outputs within max-abs 1e-4 of float64 and of the oracle up to its own

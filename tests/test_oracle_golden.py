@@ -80,3 +80,20 @@ def test_forward_case_bit_exact(name):
     else:
         assert np.array_equal(bits(att), bits(d["att"]))
         assert np.array_equal(kr, d["kc"]) and np.array_equal(vr, d["vc"])
+
+
+@pytest.mark.parametrize("arch", [orc.ARCH_LLAMA, orc.ARCH_QWEN3])
+def test_rope_head_dim_over_1024_is_left_unrotated(arch):
+    """rope_th_llama / rope_th_neox (/root/reference/src/l3_math.c:67,86)
+    print a message and return when head_dim/2 > 512: the compiled
+    reference's rope leaves x unchanged for head_dim 1026 and 2048 and
+    rotates it at 1024; the oracle does the same, bit for bit."""
+    from helpers import require_ref
+    L = require_ref()
+    for hd, rotated in ((1024, True), (1026, False), (2048, False)):
+        x = orc.normal(61 + hd, 2 * hd)
+        ref = x.copy()
+        L.ref_rope(arch, ref, ref.size, 37, hd, 1e4)
+        got = orc.rope(arch, x, 37, hd, 1e4)
+        assert np.array_equal(bits(got), bits(ref)), hd
+        assert np.array_equal(bits(got), bits(x)) != rotated, hd

@@ -5,7 +5,9 @@ g2b_attn_forward on the same inputs and caches (KV bytes bit for bit,
 outputs within 1e-4 - bit for bit where both take the same splits), and
 against the oracle; two calls in a row on one context, the second at a
 smaller position, so nothing the first left in the scratch leaks into the
-second.  Also the refusals: a RoPE table that does not reach pos (nothing
+second.  The contract itself: the first call on a fresh context leaves the
+device's free memory unchanged, and a call captured into a HIP graph (kernel
+nodes only) replays bit for bit like the direct call.  Also the refusals: a RoPE table that does not reach pos (nothing
 may be allocated to extend it), and a shape whose partials need more than
 the 2 MiB scratch."""
 import numpy as np
@@ -103,8 +105,9 @@ def test_noalloc_refusals(gpu_device):
             owner.kv_free(kc, vc)
     # a shape without a specialised kernel (group 8: the generic kernels, at
     # most 1024 positions per split): one split is 16 x 132 floats of
-    # partials, so the 2 MiB scratch (after the rotated q) holds 247 splits,
-    # 252,928 positions; 259,999 need longer splits than the kernel takes
+    # partials, so the 2 MiB scratch (524,288 floats, after the 1024 counter
+    # words and the 2048 floats of rotated q) holds 246 splits, 251,904
+    # positions; 259,999 need longer splits than the kernel takes
     big = attn.Shape(1, 16, 2, 128, 1e6, attn.ARCH_QWEN3, True)
     with attn.Context(big) as ctx:
         kc, vc = ctx.kv_alloc(260000)
@@ -117,4 +120,80 @@ def test_noalloc_refusals(gpu_device):
             ctx.attn_forward_noalloc(0, 20000, 260000, kc, vc, q.ptr, k.ptr, k.ptr)
             ctx.sync()
         finally:
+            ctx.kv_free(kc, vc)
+
+
+def test_noalloc_allocates_nothing_and_replays_from_a_graph(gpu_device):
+    """hipMemGetInfo around the first g2b_attn_forward_noalloc of a context
+    that has only allocated its KV (k_layer's static splits: 50 splits of
+    partials in the fixed scratch), then the same call captured on the
+    context's stream and replayed three times, with eager calls and
+    synchronisations between the replays, each replay bit for bit equal to
+    the direct call (the append at pos rewrites the same bytes)."""
+    o = orc.Shape(1, 16, 8, 128, 1e6, orc.ARCH_QWEN3, True)
+    s = ashape(o)
+    cap, pos = 6000, 5999
+    rng = np.random.default_rng(4711)
+    kp = rng.standard_normal((pos, o.nkv)).astype(np.float32)
+    vp = rng.standard_normal((pos, o.nkv)).astype(np.float32)
+    q = rng.standard_normal(o.nq).astype(np.float32)
+    k = rng.standard_normal(o.nkv).astype(np.float32)
+    v = rng.standard_normal(o.nkv).astype(np.float32)
+    with attn.Context(s) as warm:  # kernels loaded, runtime pools set up
+        kc, vc = warm.kv_alloc(cap)
+        qd, kd = hip.to_device(q), hip.to_device(k)
+        warm.attn_forward_noalloc(0, pos, cap, kc, vc, qd.ptr, kd.ptr, kd.ptr)
+        warm.sync()
+        warm.kv_free(kc, vc)
+    with attn.Context(s) as ctx:
+        kc, vc = ctx.kv_alloc(cap)
+        graph = None
+        try:
+            kpd, vpd = hip.to_device(kp), hip.to_device(vp)
+            ctx.kv_append_rows(kc, vc, cap, 0, 0, pos, kpd.ptr, vpd.ptr)
+            pristine, qd = hip.to_device(q), hip.to_device(q)
+            kd, vd = hip.to_device(k), hip.to_device(v)
+            ctx.sync()
+            free0, _ = hip.mem_info()
+            print("[noalloc] first call on a fresh context", flush=True)
+            ctx.attn_forward_noalloc(0, pos, cap, kc, vc, qd.ptr, kd.ptr, vd.ptr)
+            ctx.sync()
+            free1, _ = hip.mem_info()
+            assert free1 == free0, f"device free memory moved by {free0 - free1} bytes"
+            assert ctx.last_schedule()["max_splits"] > 1  # the scratch holds partials
+            direct = qd.download(np.float32, o.nq)
+            host = orc.alloc_kv(o, cap)
+            orc.kv_prefill(o, cap, 0, 0, host[0], host[1], kp, vp)
+            ref, _ = orc.attn_layer(o, cap, 0, pos, host[0], host[1], q, k, v)
+            ex, _ = exact_attention(o, cap, 0, pos, host[0], host[1], q)
+            check_out(direct, ref, ex)
+
+            hip.copy_d2d(qd.ptr, pristine.ptr, q.nbytes)
+            hip.device_sync()
+            print("[noalloc] capture into a graph", flush=True)
+            graph = hip.Graph(ctx.stream, lambda: ctx.attn_forward_noalloc(
+                0, pos, cap, kc, vc, qd.ptr, kd.ptr, vd.ptr))
+            types = graph.node_types()
+            assert types and all(t == hip.GRAPH_NODE_KERNEL for t in types), types
+            for r in range(3):
+                hip.copy_d2d(qd.ptr, pristine.ptr, q.nbytes)
+                hip.device_sync()
+                print(f"[noalloc] replay {r}", flush=True)
+                graph.launch(ctx.stream)
+                ctx.sync()
+                got = qd.download(np.float32, o.nq)
+                assert np.array_equal(got.view(np.uint32), direct.view(np.uint32)), r
+                # eager work between replays
+                hip.copy_d2d(qd.ptr, pristine.ptr, q.nbytes)
+                hip.device_sync()
+                ctx.attn_forward_noalloc(0, pos, cap, kc, vc, qd.ptr, kd.ptr, vd.ptr)
+                ctx.sync()
+                assert np.array_equal(qd.download(np.float32, o.nq).view(np.uint32),
+                                      direct.view(np.uint32))
+            nbytes = attn.kv_bytes(s, cap)
+            assert np.array_equal(hip.copy_d2h(kc, np.uint8, nbytes), host[0])
+            assert np.array_equal(hip.copy_d2h(vc, np.uint8, nbytes), host[1])
+        finally:
+            if graph is not None:
+                graph.destroy()
             ctx.kv_free(kc, vc)
