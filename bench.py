@@ -432,8 +432,9 @@ def main():
 def gemv_leg(args):
     """Device weight GEMVs (g2b_matmul, matmul_q of l2_codec.c:342-360) on
     Qwen3-0.6B's output projection (vocab 151936 x dim 1024), the largest
-    single matmul_q call of a decode step: weight GB/s of each fused type,
-    with the reference's own AVX2+OpenMP matmul (compiled reference, when it
+    single matmul_q call of a decode step: weight GB/s of each fused type and
+    of F16 / Q4_1 (the reference's dequantising fallback), with the
+    reference's own AVX2+OpenMP matmul_q (compiled reference, when it
     was built; else the oracle's scalar restatement on one thread) timed on
     the host cores as the CPU baseline, and a row sample checked against the
     float64 product."""
@@ -448,7 +449,8 @@ def gemv_leg(args):
     res = {"workload": f"Qwen3-0.6B output projection: d={d} rows x n={n}, x ~ N(0,1)",
            "unit": "GB/s of weight bytes"}
     ref = orc.ref_lib("avx2")
-    for t, name in ((attn.T_Q8_0, "q8_0"), (attn.T_Q4_0, "q4_0"), (attn.T_F32, "f32")):
+    for t, name in ((attn.T_Q8_0, "q8_0"), (attn.T_Q4_0, "q4_0"), (attn.T_F32, "f32"),
+                    (attn.T_F16, "f16"), (attn.T_Q4_1, "q4_1")):
         w = orc.random_weights(rng, t, n, d)
         wd = ctx.weights_upload(w)
         for _ in range(3):

@@ -197,8 +197,7 @@ def kv_offset(shape: Shape, ctx_cap: int, layer: int, pos: int) -> int:
     return int(lib().g2b_kv_offset(C.byref(shape.c()), ctx_cap, layer, pos))
 
 
-T_F32, T_Q4_0, T_Q8_0 = 0, 2, 8  # GGML type ids of the device GEMVs
-T_F16 = 1
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0 = 0, 1, 2, 3, 8  # GGML type ids of the device GEMVs
 CFG_FIELDS = ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab", "seq_len",
               "head_dim", "eps", "rope_theta")
 

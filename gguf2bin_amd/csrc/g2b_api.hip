@@ -1147,8 +1147,10 @@ size_t g2b_matmul_row_bytes(int32_t type, int32_t n) {
   if (n < 0) return 0;
   switch (type) {
     case G2B_T_F32: return (size_t)n * 4u;
+    case G2B_T_F16: return (size_t)n * 2u;
     case G2B_T_Q8_0: return (size_t)(n / 32) * 34u;
     case G2B_T_Q4_0: return (size_t)(n / 32) * 18u;
+    case G2B_T_Q4_1: return (size_t)(n / 32) * 20u;
     default: return 0;
   }
 }
@@ -1156,15 +1158,18 @@ size_t g2b_matmul_row_bytes(int32_t type, int32_t n) {
 int g2b_matmul(g2b_ctx *c, float *out, const float *x, const void *w, int32_t type, int32_t n,
                int32_t d) {
   if (!c) return G2B_EINVAL;
-  if (type != G2B_T_F32 && type != G2B_T_Q8_0 && type != G2B_T_Q4_0)
+  if (type != G2B_T_F32 && type != G2B_T_F16 && type != G2B_T_Q8_0 && type != G2B_T_Q4_0 &&
+      type != G2B_T_Q4_1)
     return fail(c, G2B_EUNSUP, "weight type %d has no device GEMV", type);
   if (int rc = set_device(c)) return rc;
   if (!out || !x || !w || n <= 0 || d <= 0) {  // matmul_q's guard (l2_codec.c:343-346)
     if (out && d > 0) G2B_HIP(c, launch_fill_zero(out, d, c->stream));
     return G2B_OK;
   }
+  if (type == G2B_T_Q4_1 && n % 32)
+    return fail(c, G2B_EINVAL, "Q4_1 rows must be whole blocks (n %% 32 == 0), n = %d", n);
   if (((uintptr_t)w & 1u) && type != G2B_T_F32)
-    return fail(c, G2B_EINVAL, "quantised weights must be 2-byte aligned");
+    return fail(c, G2B_EINVAL, "F16 and quantised weights must be 2-byte aligned");
   if (((uintptr_t)w & 3u) && type == G2B_T_F32)
     return fail(c, G2B_EINVAL, "F32 weights must be 4-byte aligned");
   GemvParams p{};

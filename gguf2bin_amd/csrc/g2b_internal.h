@@ -263,7 +263,7 @@ int layer_occupancy(const ShapeDev &sh, int32_t tune_chunk, int32_t stage_mode,
 
 // Device GEMVs (g2b_matmul.hip) for matmul_q's fused types (GGML type ids,
 // /root/reference/include/g2b.h:13-14).
-constexpr int32_t kTypeF32 = 0, kTypeQ4_0 = 2, kTypeQ8_0 = 8;
+constexpr int32_t kTypeF32 = 0, kTypeF16 = 1, kTypeQ4_0 = 2, kTypeQ4_1 = 3, kTypeQ8_0 = 8;
 struct GemvParams {
   float *out;          // [d]
   const float *x;      // [n]

@@ -1,7 +1,9 @@
-// g2b_matmul.hip - device GEMVs of gguf2bin2's fused weight types:
-// matmul_q8_0 / matmul_q4_0 (/root/reference/src/l2_codec.c:203-340) and
-// the F32 matmul (src/l3_math.c:17-20), dispatched as matmul_q does
-// (l2_codec.c:342-349): out[i] = sum_j W[i][j] * x[j], i < d.
+// g2b_matmul.hip - device GEMVs of gguf2bin2's weight types: the fused
+// matmul_q8_0 / matmul_q4_0 (/root/reference/src/l2_codec.c:203-340) and the
+// F32 matmul (src/l3_math.c:17-20), dispatched as matmul_q does
+// (l2_codec.c:342-349), and the types matmul_q runs through its dequantising
+// fallback (:350-366; gguf_dequant :186-199) whose dequantisation is
+// defined: F16 and Q4_1.  out[i] = sum_j W[i][j] * x[j], i < d.
 //
 // Weight rows are streamed once per call (HBM-bound: 1.0625 B per weight for
 // Q8_0, 0.5625 B for Q4_0, 4 B for F32).  Q8_0 / Q4_0: a row of nb = n/32
@@ -25,6 +27,7 @@ namespace g2b {
 namespace {
 
 typedef float gemv_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gemv_u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvUnroll = 4;  // steps whose loads are in flight together
@@ -62,10 +65,17 @@ __device__ __forceinline__ float scale_of(uint32_t d0, uint32_t sh) {
   return half_bits_to_f32_hw((d0 >> (8u * sh)) & 0xFFFFu);
 }
 
-// Raw block bytes: Q8_0 34 bytes -> 9 dwords, Q4_0 18 bytes -> 5 dwords.
+// Block formats of k_gemv_q: FMT 1 = Q8_0 (34 bytes), 2 = Q4_0 (18), 3 =
+// Q4_1 (20: fp16 d, fp16 m, 16 bytes of nibbles).
+template <int FMT>
+constexpr int block_bytes() {
+  return FMT == 1 ? 34 : FMT == 2 ? 18 : 20;
+}
+// Raw block bytes: the dwords covering a 2-byte aligned block (Q8_0 9, Q4_0
+// 5, Q4_1 6).
 template <int FMT>
 struct BlockRaw {
-  static constexpr int N = FMT == 1 ? 9 : 5;
+  static constexpr int N = FMT == 1 ? 9 : FMT == 2 ? 5 : 6;
   uint32_t d[N];
   uint32_t sh;
 };
@@ -117,7 +127,7 @@ __device__ __forceinline__ float block_dot(const BlockRaw<FMT> &r, const float *
       a3 = fmaf((float)(int8_t)(w >> 24), x[4 * j + 3], a3);
     }
     return ((a0 + a1) + (a2 + a3)) * scale_of(r.d[0], r.sh);
-  } else {
+  } else if constexpr (FMT == 2) {
     // Q4_0 (l2_codec.c:321-337): byte j holds element j (low nibble) and
     // element j + 16 (high nibble), each (nibble - 8) * d.  v_cvt_off_f32_i4
     // turns a signed nibble s into s / 16; nibble ^ 8 read as signed is
@@ -136,6 +146,34 @@ __device__ __forceinline__ float block_dot(const BlockRaw<FMT> &r, const float *
       a3 = fmaf(nib_f<3>(h), x[16 + 4 * j + 3], a3);
     }
     return ((a0 + a1) + (a2 + a3)) * (16.f * scale_of(r.d[0], r.sh));
+  } else {
+    // Q4_1 (gguf_dequant's deq_q4_1, l2_codec.c:65-75): byte j holds
+    // elements j (low nibble) and j + 16 (high), each d * q + m.  With the
+    // same signed-nibble converts as Q4_0 (S = sum (q - 8)/16 * x), the
+    // block is 16 d S + (8 d + m) sum x.  (The reference rounds each weight
+    // d*q + m to fp32 before its products; the difference is within one
+    // fp32 rounding of each product, inside the GEMV bound.)
+    float x0 = 0.f, x1 = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t w =
+          r.sh ? __builtin_amdgcn_perm(r.d[j + 2], r.d[j + 1], 0x05040302u) : r.d[j + 1];
+      const uint32_t t = w ^ 0x88888888u;
+      const uint32_t h = t >> 4;
+      a0 = fmaf(nib_f<0>(t), x[4 * j + 0], a0);
+      a1 = fmaf(nib_f<1>(t), x[4 * j + 1], a1);
+      a0 = fmaf(nib_f<2>(t), x[4 * j + 2], a0);
+      a1 = fmaf(nib_f<3>(t), x[4 * j + 3], a1);
+      a2 = fmaf(nib_f<0>(h), x[16 + 4 * j + 0], a2);
+      a3 = fmaf(nib_f<1>(h), x[16 + 4 * j + 1], a3);
+      a2 = fmaf(nib_f<2>(h), x[16 + 4 * j + 2], a2);
+      a3 = fmaf(nib_f<3>(h), x[16 + 4 * j + 3], a3);
+      x0 += (x[4 * j + 0] + x[4 * j + 1]) + (x[4 * j + 2] + x[4 * j + 3]);
+      x1 += (x[16 + 4 * j + 0] + x[16 + 4 * j + 1]) + (x[16 + 4 * j + 2] + x[16 + 4 * j + 3]);
+    }
+    const float d = scale_of(r.d[0], r.sh);
+    const float m = half_bits_to_f32_hw(r.sh ? (r.d[1] & 0xFFFFu) : (r.d[0] >> 16));
+    return fmaf((a0 + a1) + (a2 + a3), 16.f * d, (x0 + x1) * fmaf(8.f, d, m));
   }
 }
 
@@ -249,7 +287,7 @@ template <int FMT, int LPR, int KB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
   extern __shared__ float xs[];
   constexpr int RPS = 64 / LPR;  // rows per wave-step
-  constexpr int BB = FMT == 1 ? 34 : 18;
+  constexpr int BB = block_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
   const int rr = lane / LPR, c = lane % LPR;
@@ -511,7 +549,7 @@ template <int FMT, int LPR, int KB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q_split(GemvParams P) {
   extern __shared__ float xs[];  // the fused SiLU x up: n floats
   constexpr int RPS = 64 / LPR;
-  constexpr int BB = FMT == 1 ? 34 : 18;
+  constexpr int BB = block_bytes<FMT>();
   constexpr int NW = kGemvThreads / 64;
   __shared__ float part[kGemvUnroll][NW][RPS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -585,6 +623,39 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_f32(GemvParams P) {
       for (int j = 4 * n4 + lane; j < n; j += 64) a0 = fmaf(wr[j], P.x[j], a0);
     } else {
       for (int j = lane; j < n; j += 64) a0 = fmaf(wr[j], P.x[j], a0);
+    }
+    const float acc = lanes_sum<64>(a0 + a1);
+    if (lane == 0) P.out[row] = acc;
+  }
+}
+
+// F16 (matmul_q's fallback: gguf_dequant's exact half_to_float, then the
+// products, l2_codec.c:350-366): a wave per row, lanes over 16-byte pieces
+// of eight halves (rows 16-byte aligned), else over single halves.
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_f16(GemvParams P) {
+  const int lane = threadIdx.x & 63;
+  const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
+  const int n = P.n, n8 = n / 8;
+  for (int row = gw; row < P.d; row += P.n_waves) {
+    const uint16_t *wr = reinterpret_cast<const uint16_t *>(P.w + (size_t)row * P.row_bytes);
+    float a0 = 0.f, a1 = 0.f;
+    if (P.vec4) {
+      for (int j = lane; j < n8; j += 64) {
+        const gemv_u32x4 w8 = nt_load<gemv_u32x4>(wr + 8 * j);
+        const float4 xa = *reinterpret_cast<const float4 *>(P.x + 8 * j);
+        const float4 xb = *reinterpret_cast<const float4 *>(P.x + 8 * j + 4);
+        a0 = fmaf(half_bits_to_f32_hw(w8.x & 0xFFFFu), xa.x, a0);
+        a1 = fmaf(half_bits_to_f32_hw(w8.x >> 16), xa.y, a1);
+        a0 = fmaf(half_bits_to_f32_hw(w8.y & 0xFFFFu), xa.z, a0);
+        a1 = fmaf(half_bits_to_f32_hw(w8.y >> 16), xa.w, a1);
+        a0 = fmaf(half_bits_to_f32_hw(w8.z & 0xFFFFu), xb.x, a0);
+        a1 = fmaf(half_bits_to_f32_hw(w8.z >> 16), xb.y, a1);
+        a0 = fmaf(half_bits_to_f32_hw(w8.w & 0xFFFFu), xb.z, a0);
+        a1 = fmaf(half_bits_to_f32_hw(w8.w >> 16), xb.w, a1);
+      }
+      for (int j = 8 * n8 + lane; j < n; j += 64) a0 = fmaf(half_bits_to_f32_hw(wr[j]), P.x[j], a0);
+    } else {
+      for (int j = lane; j < n; j += 64) a0 = fmaf(half_bits_to_f32_hw(wr[j]), P.x[j], a0);
     }
     const float acc = lanes_sum<64>(a0 + a1);
     if (lane == 0) P.out[row] = acc;
@@ -728,9 +799,17 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
     hipLaunchKernelGGL(k_gemv_f32, dim3(wgs), dim3(kGemvThreads), 0, s, p);
     return hipGetLastError();
   }
-  const int fmt = type == kTypeQ8_0 ? 1 : 2;
+  if (type == kTypeF16) {
+    p.row_bytes = (uint32_t)p.n * 2u;
+    p.vec4 = ((uintptr_t)p.w % 16 == 0 && (uintptr_t)p.x % 16 == 0 && p.n % 8 == 0) ? 1 : 0;
+    const int wgs = std::max(1, std::min((p.d + waves_per_wg - 1) / waves_per_wg, n_cu * 8));
+    p.n_waves = wgs * waves_per_wg;
+    hipLaunchKernelGGL(k_gemv_f16, dim3(wgs), dim3(kGemvThreads), 0, s, p);
+    return hipGetLastError();
+  }
+  const int fmt = type == kTypeQ8_0 ? 1 : type == kTypeQ4_0 ? 2 : 3;
   p.nb = p.n / 32;
-  p.row_bytes = (uint32_t)p.nb * (fmt == 1 ? 34u : 18u);
+  p.row_bytes = (uint32_t)p.nb * (fmt == 1 ? 34u : fmt == 2 ? 18u : 20u);
   if (p.nb > 128 && p.nb <= 4 * 128 && p.x_vec4) {
     // rows split over the workgroup's four waves (x in registers)
     const int nbw = (p.nb + 3) / 4;  // > 32, so 64 lanes per row
@@ -740,8 +819,9 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
                                       std::min(p.steps, n_cu)),
                              n_cu * 4);
     p.n_waves = wgs * waves_per_wg;
-    return fmt == 1 ? launch_split<1>(p, 64, kb, dim3(wgs), s)
-                    : launch_split<2>(p, 64, kb, dim3(wgs), s);
+    return fmt == 1   ? launch_split<1>(p, 64, kb, dim3(wgs), s)
+           : fmt == 2 ? launch_split<2>(p, 64, kb, dim3(wgs), s)
+                      : launch_split<3>(p, 64, kb, dim3(wgs), s);
   }
   // The int8 matrix cores (k_gemv_mma) where they pay: plain (unfused) Q4_0
   // products of 1024-element rows, at least kGemvMmaMinRows of them (the lm
@@ -777,13 +857,17 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   // resident round of workgroups (a partial second round would leave most
   // of the chip idle at the end)
   const size_t lds = kbv < 0 ? (size_t)p.nb * 128u : pro_lds(p);
-  const int occ = fmt == 1 ? occ_q_fmt<1>(lpr, kbv, lds) : occ_q_fmt<2>(lpr, kbv, lds);
+  const int occ = fmt == 1   ? occ_q_fmt<1>(lpr, kbv, lds)
+                  : fmt == 2 ? occ_q_fmt<2>(lpr, kbv, lds)
+                             : occ_q_fmt<3>(lpr, kbv, lds);
   const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
                                       std::min(p.steps, n_cu * 4)),
                              n_cu * std::max(1, occ) * waves_per_wg);
   const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
   p.n_waves = wgs * waves_per_wg;
-  return fmt == 1 ? launch_q<1>(p, lpr, kbv, dim3(wgs), s) : launch_q<2>(p, lpr, kbv, dim3(wgs), s);
+  return fmt == 1   ? launch_q<1>(p, lpr, kbv, dim3(wgs), s)
+         : fmt == 2 ? launch_q<2>(p, lpr, kbv, dim3(wgs), s)
+                    : launch_q<3>(p, lpr, kbv, dim3(wgs), s);
 }
 
 }  // namespace g2b

@@ -42,6 +42,13 @@ __global__ void k_embed_row(float *out, const uint8_t *emb, const int32_t *tok, 
       const uint8_t *b = row + (size_t)(i / 32) * 34;
       const float s = half_bits_to_f32((uint32_t)b[0] | (uint32_t)b[1] << 8);
       v = s * (float)(int8_t)b[2 + i % 32];
+    } else if (type == kTypeQ4_1) {  // deq_q4_1 (l2_codec.c:65-75): s*q + m
+      const uint8_t *b = row + (size_t)(i / 32) * 20;
+      const float s = half_bits_to_f32((uint32_t)b[0] | (uint32_t)b[1] << 8);
+      const float mn = half_bits_to_f32((uint32_t)b[2] | (uint32_t)b[3] << 8);
+      const int j = i % 32;
+      const int q = j < 16 ? (b[4 + j] & 0x0f) : (b[4 + j - 16] >> 4);
+      v = s * (float)q + mn;
     } else {  // Q4_0
       const uint8_t *b = row + (size_t)(i / 32) * 18;
       const float s = half_bits_to_f32((uint32_t)b[0] | (uint32_t)b[1] << 8);
@@ -83,8 +90,12 @@ __global__ void k_add(float *x, const float *y, int32_t n) {
 
 int ew_blocks(int32_t n) { return (n + kEwThreads - 1) / kEwThreads < 1024 ? (n + kEwThreads - 1) / kEwThreads : 1024; }
 
-bool matrix_type_ok(int32_t t) { return t == kTypeF32 || t == kTypeQ8_0 || t == kTypeQ4_0; }
-bool embed_type_ok(int32_t t) { return matrix_type_ok(t) || t == 1; }
+// matmul_q's types with a device GEMV (g2b_matmul); embeddings: the same
+// (gguf_dequant of a row).  The K-quants are refused (include/g2b_matmul.h).
+bool matrix_type_ok(int32_t t) {
+  return t == kTypeF32 || t == kTypeF16 || t == kTypeQ8_0 || t == kTypeQ4_0 || t == kTypeQ4_1;
+}
+bool embed_type_ok(int32_t t) { return matrix_type_ok(t); }
 
 // row_stride (l5_model.c:444-446) for the supported types.
 uint64_t row_stride_of(int32_t t, int32_t n) {
@@ -93,6 +104,7 @@ uint64_t row_stride_of(int32_t t, int32_t n) {
     case 1: return (uint64_t)n * 2u;
     case kTypeQ8_0: return (uint64_t)(n / 32) * 34u;
     case kTypeQ4_0: return (uint64_t)(n / 32) * 18u;
+    case kTypeQ4_1: return (uint64_t)(n / 32) * 20u;
     default: return 0;
   }
 }
@@ -490,7 +502,6 @@ int enqueue_step(g2b_model *m, int32_t max_pos) {
   if (!on) return G2B_EINVAL;
   const g2b_slot *out = m->get(G2B_R_OUTPUT, -1);
   if (!out) out = emb;  // tied embeddings (l5_model.c:602)
-  if (out->type == 1) return G2B_EUNSUP;  // F16 logits matrix: no device GEMV
   if (m->fuse && gemv_fusable_pro(out->type, dim)) {
     GemvParams p{};
     p.out = m->logits;

@@ -261,19 +261,44 @@ def attn_batch(shape: Shape, layer0: int, n_layers: int, pos: np.ndarray,
 # without AVX2, kvtest flags: no FMA contraction), vectorised over rows but
 # in the reference's per-row operation order, so they are bit-exact with it.
 
-T_F32, T_Q4_0, T_Q8_0 = 0, 2, 8
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0 = 0, 1, 2, 3, 8
+# (the K-quant ids, include/g2b.h:14)
+T_Q2_K, T_Q3_K, T_Q4_K, T_Q5_K, T_Q6_K, T_Q8_K = 10, 11, 12, 13, 14, 15
+_BLOCK_BYTES = {T_Q8_0: 34, T_Q4_0: 18, T_Q4_1: 20}
 
 
 def matmul_row_bytes(t: int, n: int) -> int:
-    """row_stride (l2_codec.c:340) of the fused types."""
-    return {T_F32: n * 4, T_Q8_0: (n // 32) * 34, T_Q4_0: (n // 32) * 18}[t]
+    """row_stride (l2_codec.c:340): the fused types and the fallback's F16 / Q4_1."""
+    if t == T_F32:
+        return n * 4
+    if t == T_F16:
+        return n * 2
+    return (n // 32) * _BLOCK_BYTES[t]
 
 
 def _blocks(w: np.ndarray, t: int, n: int, d: int):
-    nb, bb = n // 32, (34 if t == T_Q8_0 else 18)
+    nb, bb = n // 32, _BLOCK_BYTES[t]
     blk = np.ascontiguousarray(w[:d * nb * bb]).reshape(d, nb, bb)
     scale = half_to_float(blk[:, :, :2].copy().view(np.uint16)).reshape(d, nb)
     return nb, blk, scale
+
+
+def dequant_rows(w: np.ndarray, t: int, n: int, d: int) -> np.ndarray:
+    """gguf_dequant (l2_codec.c:186-199) of d rows, float32: F16 is exact
+    half_to_float (:189); Q4_1 (deq_q4_1, :65-75) is s*q + m with q the low
+    nibble of byte j for element j and the high nibble for j + 16, the
+    product exact (fp16 x 4 bits) and the sum rounded to float32."""
+    f = np.float32
+    if t == T_F16:
+        h = np.ascontiguousarray(w[:d * n * 2]).view(np.uint16).reshape(d, n)
+        return half_to_float(h.reshape(-1)).reshape(d, n)
+    assert t == T_Q4_1 and n % 32 == 0
+    nb, blk, scale = _blocks(w, t, n, d)
+    mn = half_to_float(blk[:, :, 2:4].copy().view(np.uint16)).reshape(d, nb)
+    qs = blk[:, :, 4:]
+    q = np.concatenate([(qs & 0x0F), (qs >> 4)], axis=2).astype(f)  # [d, nb, 32]
+    out = (scale[:, :, None].astype(f) * q).astype(f) + mn[:, :, None].astype(f)
+    return out.astype(f).reshape(d, nb * 32)
 
 
 def matmul_scalar(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int) -> np.ndarray:
@@ -283,6 +308,13 @@ def matmul_scalar(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int) -> np.nd
     x = np.ascontiguousarray(x, np.float32)
     f = np.float32
     acc = np.zeros(d, np.float32)
+    if t in (T_F16, T_Q4_1):
+        # matmul_q's fallback (l2_codec.c:350-366): the row through
+        # gguf_dequant, then s += tmp[j]*x[j] serially
+        wf = dequant_rows(w, t, n, d)
+        for j in range(n):
+            acc = acc + wf[:, j] * x[j]
+        return acc
     if t == T_F32:
         wf = np.ascontiguousarray(w[:d * n * 4]).view(np.float32).reshape(d, n)
         for j in range(n):
@@ -312,6 +344,8 @@ def matmul_exact(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int):
     x64 = np.asarray(x, np.float64)
     if t == T_F32:
         wf = np.ascontiguousarray(w[:d * n * 4]).view(np.float32).reshape(d, n).astype(np.float64)
+    elif t in (T_F16, T_Q4_1):
+        wf = dequant_rows(w, t, n, d).astype(np.float64)  # the reference's float32 weights
     else:
         nb, blk, scale = _blocks(w, t, n, d)
         if t == T_Q8_0:
@@ -327,18 +361,39 @@ def matmul_exact(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int):
 
 def ref_matmul(x: np.ndarray, w: np.ndarray, t: int, n: int, d: int,
                variant: str = "avx2") -> np.ndarray:
-    """The compiled reference's matmul_q8_0 / matmul_q4_0 / matmul."""
+    """The compiled reference's matmul_q8_0 / matmul_q4_0 / matmul, and
+    matmul_q (its dequantising fallback) for the other types."""
     L = ref_lib(variant)
     if L is None:
         raise RuntimeError("compiled reference not built (make -C oracle ref)")
     out = np.zeros(d, np.float32)
     xx = np.ascontiguousarray(x, np.float32).copy()
     ww = np.ascontiguousarray(w, np.uint8)
-    fn = {T_Q8_0: L.matmul_q8_0, T_Q4_0: L.matmul_q4_0, T_F32: L.matmul}[t]
-    fn.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32]
-    fn.restype = None
-    fn(out.ctypes.data, xx.ctypes.data, ww.ctypes.data, n, d)
+    if t in (T_Q8_0, T_Q4_0, T_F32):
+        fn = {T_Q8_0: L.matmul_q8_0, T_Q4_0: L.matmul_q4_0, T_F32: L.matmul}[t]
+        fn.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32]
+        fn.restype = None
+        fn(out.ctypes.data, xx.ctypes.data, ww.ctypes.data, n, d)
+        return out
+    L.matmul_q.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_int32,
+                           C.c_int32, C.c_void_p]
+    L.matmul_q.restype = None
+    L.matmul_q(out.ctypes.data, xx.ctypes.data, ww.ctypes.data, t, n, d, None)
     return out
+
+
+def ref_gguf_dequant(t: int, src: np.ndarray, out: np.ndarray, ne: int, variant: str = "avx2"):
+    """The compiled reference's gguf_dequant(t, src, out, ne) (l2_codec.c:
+    186-199), writing into the caller's out (whatever it held stays where
+    the reference does not write)."""
+    L = ref_lib(variant)
+    if L is None:
+        raise RuntimeError("compiled reference not built (make -C oracle ref)")
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    ss = np.ascontiguousarray(src, np.uint8)
+    L.gguf_dequant.argtypes = [C.c_uint32, C.c_void_p, C.c_void_p, C.c_uint64]
+    L.gguf_dequant.restype = None
+    L.gguf_dequant(t, ss.ctypes.data, out.ctypes.data, ne)
 
 
 def ref_g2bx_info(path: str):
@@ -430,10 +485,15 @@ def random_weights(rng: np.random.Generator, t: int, n: int, d: int) -> np.ndarr
     [-128, 127] (Q8_0) or nibbles (Q4_0); N(0,1) floats for F32."""
     if t == T_F32:
         return rng.standard_normal(d * n).astype(np.float32).view(np.uint8).copy()
-    nb, bb = n // 32, (34 if t == T_Q8_0 else 18)
+    if t == T_F16:
+        return (rng.standard_normal(d * n) * 0.1).astype(np.float16).view(np.uint8).copy()
+    nb, bb = n // 32, _BLOCK_BYTES[t]
     blk = rng.integers(0, 256, (d, nb, bb), dtype=np.uint8)
     sc = np.exp2(rng.uniform(-10, -4, (d, nb))).astype(np.float16)
     blk[:, :, :2] = sc.view(np.uint8).reshape(d, nb, 2)
+    if t == T_Q4_1:  # the block minimum: about -8 scales (q in 0..15 centred)
+        mn = (-8.0 * sc.astype(np.float32) * rng.uniform(0.5, 1.5, (d, nb))).astype(np.float16)
+        blk[:, :, 2:4] = mn.view(np.uint8).reshape(d, nb, 2)
     return blk.reshape(-1).copy()
 
 

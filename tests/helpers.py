@@ -259,7 +259,8 @@ def write_g2bx(path, cfg: dict, arch: int, flags: int, slots, version: int = 1):
 
 def random_matrix_bytes(rng, t: int, rows: int, n: int, gain: float = 1.0) -> bytes:
     """rows x n weights of type t with values ~ gain * U(-1, 1) / sqrt(n) (Q8_0,
-    Q4_0: random quants with one fp16 scale per block; F32: normal / sqrt(n))."""
+    Q4_0, Q4_1: random quants with fp16 block scales; F32, F16: normal /
+    sqrt(n))."""
     if t == 0:
         return (rng.standard_normal((rows, n)) * gain / np.sqrt(n)).astype(np.float32).tobytes()
     if t == 1:
@@ -269,6 +270,15 @@ def random_matrix_bytes(rng, t: int, rows: int, n: int, gain: float = 1.0) -> by
         blk = np.zeros((rows, nb, 34), np.uint8)
         blk[:, :, 2:] = rng.integers(-127, 128, (rows, nb, 32)).astype(np.int8).view(np.uint8)
         sc = np.full((rows, nb), gain / (127 * np.sqrt(n)) * 1.7, np.float32)
+    elif t == 3:  # Q4_1: d, m (about -8 d: nibbles centred), 16 bytes of nibbles
+        blk = np.zeros((rows, nb, 20), np.uint8)
+        blk[:, :, 4:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)
+        sc = (np.full((rows, nb), gain / (8 * np.sqrt(n)) * 1.7, np.float32)
+              * rng.uniform(0.5, 1.5, (rows, nb)).astype(np.float32))
+        mn = (-8.0 * sc * rng.uniform(0.8, 1.2, (rows, nb))).astype(np.float16)
+        blk[:, :, :2] = sc.astype(np.float16).view(np.uint8).reshape(rows, nb, 2)
+        blk[:, :, 2:4] = mn.view(np.uint8).reshape(rows, nb, 2)
+        return blk.tobytes()
     else:
         blk = np.zeros((rows, nb, 18), np.uint8)
         blk[:, :, 2:] = rng.integers(0, 256, (rows, nb, 16), dtype=np.uint8)

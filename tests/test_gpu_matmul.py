@@ -16,7 +16,7 @@ from gguf2bin_amd import attn, hip
 pytestmark = pytest.mark.gpu
 
 U = 2.0 ** -24
-TYPES = [orc.T_Q8_0, orc.T_Q4_0, orc.T_F32]
+TYPES = [orc.T_Q8_0, orc.T_Q4_0, orc.T_F32, orc.T_F16, orc.T_Q4_1]
 # n covers every lane layout: 1, 2, 3 (+ tail), 18, 32, 48, 64, 96, 128 blocks
 # (x of one or two blocks per lane in registers) and 256 / 448 blocks (x
 # through the cache); d covers partial wave-steps and several grid passes
@@ -38,6 +38,8 @@ def check(out, x, w, t, n, d, what):
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n,d", SHAPES)
 def test_matmul_vs_exact(gpu_device, t, n, d):
+    if t == orc.T_Q4_1 and n % 32:
+        pytest.skip("Q4_1 rows are whole blocks (G2B_EINVAL otherwise)")
     rng = np.random.default_rng(1000 * n + d + t)
     w = orc.random_weights(rng, t, n, d)
     x = rng.standard_normal(n).astype(np.float32)
@@ -57,7 +59,7 @@ def test_matmul_vs_exact(gpu_device, t, n, d):
     assert np.array_equal(out.view(np.uint32), host.view(np.uint32))
 
 
-@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0])
+@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0, orc.T_Q4_1, orc.T_F16])
 def test_matmul_unaligned_operands(gpu_device, t):
     """x at a 4-byte (not 16-byte) boundary takes the cached-x path; weights
     starting 2 bytes into an allocation put every other block at the other
@@ -96,9 +98,13 @@ def test_matmul_guards_and_errors(gpu_device):
                 ctx.sync()
                 assert not od.download(np.float32, d).any(), args
             ctx.matmul(od.ptr, xd.ptr, wd, orc.T_Q8_0, n, 0)  # d = 0: nothing to do
-            with pytest.raises(attn.G2BError) as e:
-                ctx.matmul(od.ptr, xd.ptr, wd, 1, n, d)  # F16
-            assert e.value.code == attn.G2B_EUNSUP
+            for kq in (orc.T_Q2_K, orc.T_Q4_K, orc.T_Q6_K, orc.T_Q8_K):  # K-quants
+                with pytest.raises(attn.G2BError) as e:
+                    ctx.matmul(od.ptr, xd.ptr, wd, kq, 256, d)
+                assert e.value.code == attn.G2B_EUNSUP
+            with pytest.raises(attn.G2BError) as e:  # Q4_1 rows of whole blocks only
+                ctx.matmul(od.ptr, xd.ptr, wd, orc.T_Q4_1, 48, d)
+            assert e.value.code == attn.G2B_EINVAL
             with pytest.raises(attn.G2BError) as e:
                 ctx.matmul(od.ptr, xd.ptr, wd + 1, orc.T_Q8_0, n, d)
             assert e.value.code == attn.G2B_EINVAL
@@ -107,7 +113,7 @@ def test_matmul_guards_and_errors(gpu_device):
             ctx.weights_free(wd)
 
 
-@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0])
+@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0, orc.T_F16, orc.T_Q4_1])
 def test_matmul_lm_head_full_size(gpu_device, t):
     """The measured shape: Qwen3-0.6B's output projection (vocab 151936 x
     dim 1024), every row against the float64 product."""

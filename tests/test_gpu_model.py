@@ -47,6 +47,14 @@ CASES = {
                          vocab=300, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
                     attn.ARCH_QWEN3, F_QK_NORM, {"*": 8, R_ATTN_K: 2, R_ATTN_O: 0, R_FFN_DOWN: 2},
                     8, 2),
+    # the types matmul_q runs through its dequantising fallback: F16
+    # matrices, embeddings and output; Q4_1 matrices and tied Q4_1 embeddings
+    "llama_f16": (dict(dim=256, hidden_dim=512, n_layers=2, n_heads=8, n_kv_heads=2,
+                       vocab=400, seq_len=64, head_dim=32, eps=1e-5, rope_theta=5e5),
+                  attn.ARCH_LLAMA, 0, 1, 1, 1),
+    "qwen3_q4_1_tied": (dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2,
+                             vocab=300, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
+                        attn.ARCH_QWEN3, F_QK_NORM | F_TIE_EMBD, 3, 3, None),
     # rows of 132 blocks: rmsnorm + Q/K/V, rmsnorm + gate/up and rmsnorm +
     # logits on the split-row GEMV
     "wide_dim_q4": (dict(dim=4224, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=4,
