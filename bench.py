@@ -338,6 +338,9 @@ def main():
                     help="semicolon list of split,chunk,stage,piece: time layer-serial and fused")
     ap.add_argument("--model-only", action="store_true",
                     help="only the whole-decode-step leg (model_forward), printed as its JSON")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the weight-GEMV leg (with --calibrate-copy first when given), "
+                         "printed as its JSON")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -350,6 +353,19 @@ def main():
     hip.set_device(0)
     if args.model_only:
         print(json.dumps({"model_forward": model_leg(args)}), flush=True)
+        return
+    if args.gemv_only:
+        if args.calibrate_copy:
+            cctx = attn.Context(attn.Shape(1, 2, 1, 64, 1e4, attn.ARCH_QWEN3, False))
+            nb = args.calibrate_copy << 20
+            src, dst = hip.DeviceBuffer(nb), hip.DeviceBuffer(nb)
+            cctx.synth_copy(dst.ptr, src.ptr, nb)
+            cctx.sync()
+            src.free()
+            dst.free()
+            cctx.close()
+            log(f"calibration copy of {args.calibrate_copy} MiB done")
+        print(json.dumps({"gemv": gemv_leg(args)}), flush=True)
         return
 
     w = Workload(args.config, args, args.n_seq)

@@ -557,23 +557,32 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   // the workgroups take the units in turn; otherwise static splits, sized
   // so the launch's workgroups form whole rounds.
   const int64_t n_units = (int64_t)n_seq * n_layers;
-  const int64_t wq_slots = tiles                        ? tiles_slots(c, true)
-                           : fast && dp.stage_mode != 0 ? slots_for(c, dp, true)
-                                                         : 0;
+  // k_layer's work queue pulls its chunks straight into LDS (mode 1): 1-2%
+  // faster than register staging on the batched configs, while a single
+  // sequence's static splits, bound by latency, keep register staging.  The
+  // work queue's slots are counted for the variant it would run (the
+  // register-staging variant holds more registers: fewer resident
+  // workgroups, which had sent c2's all-layers call through the work queue,
+  // 115 against 97-101 us).
+  DecodeParams wq_dp = dp;
+  if (!tiles && c->tune_stage == 0 && dp.stage_mode == kDefaultStageMode) {
+    const int32_t r1 = decode_stage_rows(c->sh, dp.tune_chunk, 1);
+    if (r1 > 0) {
+      wq_dp.stage_mode = 1;
+      wq_dp.stage_rows = r1;
+    }
+  }
+  const int64_t wq_slots = tiles                           ? tiles_slots(c, true)
+                           : fast && wq_dp.stage_mode != 0 ? slots_for(c, wq_dp, true)
+                                                            : 0;
   // (F32 rows: static splits unless a piece is asked for - c3 all layers
   // 601 us static against 659 us through the work queue)
   const bool use_wq = !fixed && fast && dp.stage_mode != 0 && c->tune_piece >= 0 &&
                       (c->tune_piece > 0 ||
                        (c->shape.kv_q8 && wq_slots * kWavesPerSplit <= n_units * kWqMaxWavesPerUnit));
-  // k_layer's work queue pulls its chunks straight into LDS (mode 1): 1-2%
-  // faster than register staging on the batched configs, while a single
-  // sequence's static splits, bound by latency, keep register staging.
-  if (use_wq && !tiles && c->tune_stage == 0 && dp.stage_mode == kDefaultStageMode) {
-    const int32_t r1 = decode_stage_rows(c->sh, dp.tune_chunk, 1);
-    if (r1 > 0) {
-      dp.stage_mode = 1;
-      dp.stage_rows = r1;
-    }
+  if (use_wq && !tiles) {
+    dp.stage_mode = wq_dp.stage_mode;
+    dp.stage_rows = wq_dp.stage_rows;
   }
   const int64_t slots = use_wq ? (tiles ? wq_slots : slots_for(c, dp, true))
                         : tiles ? tiles_slots(c, false)
