@@ -345,7 +345,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is described in DESIGN.md, not built)", file=sys.stderr)
+              "(sharding across GPUs is designed, not built)", file=sys.stderr)
         sys.exit(2)
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)

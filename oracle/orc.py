@@ -425,8 +425,8 @@ def ref_model_forward(path: str, tokens, vocab: int, kv_q8: bool = False,
     """The compiled reference's model_forward over tokens at positions
     0..n-1 of a G2BX file: logits [n][vocab]; with timed, (logits, seconds
     of the token loop alone, without the load).  variant "gpu": the
-    reference with the drop-in patch of INTEGRATION.md section 1
-    (libg2bref_gpu.so), whose attention runs on the device (G2B_GPU is set
+    reference with the maintainer's drop-in patch (oracle/refpatch.py;
+    libg2bref_gpu.so), whose attention runs on the device (G2B_GPU is set
     for the call)."""
     L = ref_lib(variant)
     if L is None:

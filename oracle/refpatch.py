@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Apply the drop-in patch of INTEGRATION.md section 1 to a COPY of the
+"""Apply the maintainer's drop-in patch for the reference to a COPY of the
 reference sources (test infrastructure: build recipe of oracle/_ref).
 
     python3 oracle/refpatch.py /root/reference /tmp/g2b_refpatch
@@ -15,8 +15,8 @@ anchors in include/g2b.h and src/l5_model.c:
   - model_forward's attention block (:505-578) as one g2b_attn_forward_host
     call when the context exists;
   - the context's release in model_free (:418-434).
-Every snippet below is the text INTEGRATION.md section 1 shows (checked by
-tests/test_refpatch.py).  Each anchor must match exactly once; the script
+Every snippet below is also shown, verbatim, in the repository's integration
+guide for maintainers (checked by tests/test_refpatch.py).  Each anchor must match exactly once; the script
 fails otherwise, so a reference that moved under the patch is reported, not
 silently mis-patched.
 """

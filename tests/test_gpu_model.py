@@ -199,8 +199,8 @@ def test_forward_errors(gpu_device, tmp_path):
 @pytest.mark.parametrize("name", ["qwen3_q8_tied", "qwen3_hd128_q8", "llama_q4_f16emb"])
 @pytest.mark.parametrize("kv_q8", [False, True])
 def test_patched_reference_runs_device_attention(gpu_device, tmp_path, name, kv_q8):
-    """The reference's own model_forward with INTEGRATION.md section 1 applied
-    (oracle/refpatch.py; KV from g2b_kv_alloc in alloc_rt, the attention block
+    """The reference's own model_forward with the maintainer's drop-in patch
+    applied (oracle/refpatch.py; KV from g2b_kv_alloc in alloc_rt, the attention block
     as g2b_attn_forward_host, QK-RMSNorm weights handed over at load) against
     the unpatched reference on the same file: everything but the attention
     is the reference's own code.  140 tokens reach the split kernel.  F32 KV:

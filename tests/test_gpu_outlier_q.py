@@ -29,7 +29,7 @@ import numpy as np
 import pytest
 
 from oracle import orc
-from test_gpu_parity import SHAPES, run_batch_case
+from test_gpu_parity import MODES, SHAPES, run_batch_case
 
 pytestmark = pytest.mark.gpu
 
@@ -81,3 +81,28 @@ def test_outlier_q_channels(gpu_device, name, factor, norm):
               f"weights rel {r_w:.3g} (reference's own {own:.3g})", flush=True)
     else:
         print(f"[outlier] {name} x{factor:g} norm={norm}: max |out - f64| {e_out:.3g}", flush=True)
+
+
+@pytest.mark.parametrize("mode", ["layers", "static", "dma_wq", "wq_fused"])
+@pytest.mark.parametrize("name", ["qwen3_q8_g2", "llama3_q8_g4", "hd64_q8_g3"])
+def test_mixed_outlier_sequences(gpu_device, name, mode):
+    """Sequences 1 and 3 of the batch with a 10^2 channel per (head, chunk),
+    the others N(0,1), through k_layer's static and work-queue schedules
+    (the work queue hands pieces of both kinds to one workgroup in turn, so
+    a visit's digit planes must come from its own sequence's q).  Outputs
+    within max-abs 1e-4 of float64 and the oracle; weights within 1e-5 plus
+    twice the reference's own error of float64 (the outlier sequences'
+    reference error is above 1e-5)."""
+    nh, nkv, hd, arch, q8 = SHAPES[name]
+    o = orc.Shape(2, nh, nkv, hd, 5e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
+    caps = [1, 37, 300, 700, 129]
+    poss = [0, 36, 211, 650, 64]
+    gain = np.ones((len(caps), o.nq), np.float32)
+    gain[1] = gain[3] = outlier_gain(o.nq, hd, 100.0)
+    fused, tune = MODES[mode]
+    errs = []
+    print(f"[outlier-mixed] {name} mode={mode}", flush=True)
+    run_batch_case(o, caps, poss, seed=4242 + hd, fused=fused, tune=tune, kernel=1,
+                   q_gain=gain, w_as_accurate_as_ref=True, errs=errs)
+    print(f"[outlier-mixed] {name} mode={mode}: max |out - f64| {max(e[0] for e in errs):.3g}, "
+          f"weights rel {max(e[1] for e in errs):.3g}", flush=True)

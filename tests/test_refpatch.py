@@ -1,9 +1,10 @@
-"""The drop-in patch of INTEGRATION.md section 1 (oracle/refpatch.py), on
+"""The maintainer's drop-in patch for the reference (oracle/refpatch.py), on
 the CPU: it applies to a copy of the reference sources (/root/reference,
 present in the build container only), the patched sources compile with the
 reference's own flags and warnings (the patch adds none), and every snippet
-the patch inserts is the text INTEGRATION.md shows.  The patched reference
-itself runs on the GPU in tests/test_gpu_model.py."""
+the patch inserts is the text the integration guide at the repository root
+shows.  The patched reference itself runs on the GPU in
+tests/test_gpu_model.py."""
 import os
 import re
 import subprocess
