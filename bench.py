@@ -637,9 +637,9 @@ def cpu_leg(w: Workload, na: int, nb: int, min_s: float):
     on one thread, as the reference's single-threaded attention runs them)
     and mode B (OpenMP over the nb sequences, all host threads), each
     repeated for at least min_s seconds.  Its outputs are compared with the
-    GPU's layer-serial outputs, the appended rows byte for byte, and two
-    (sequence, layer) units are also evaluated in float64 from the same
-    bytes."""
+    GPU's layer-serial outputs, the appended rows byte for byte, and up to
+    three (sequence, layer) units are also evaluated in float64 from the
+    same bytes."""
     from oracle import orc  # CPU baseline and checker only
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from helpers import exact_attention  # float64 checker
@@ -699,15 +699,25 @@ def cpu_leg(w: Workload, na: int, nb: int, min_s: float):
         np.array_equal(host[j][0].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][0]) and
         np.array_equal(host[j][1].reshape(L, caps[i], rb)[:, poss[i]], gpu_rows[j][1])
         for j, i in enumerate(idx))
-    # float64 evaluation of two units (the first and last sampled sequence,
-    # first and last layer) from the same cache bytes
+    # float64 evaluation from the same cache bytes of three units: the first
+    # and last sampled sequence (first and last layer) and the unit where the
+    # GPU and the oracle differ most.  The tests' rule (helpers.check_out):
+    # max |gpu - float64| <= 1e-4, and max |gpu - oracle| <= 1e-4 plus the
+    # oracle's own error from float64 (its serial fp32 sums drift at 16k-32k
+    # positions), unit by unit.
+    per_unit = np.max(np.abs(out_b - out_gpu[:, idx]), axis=2)  # [layer][sample]
+    worst_l, worst_j = (int(v) for v in np.unravel_index(np.argmax(per_unit), per_unit.shape))
     f64_gpu = f64_orc = 0.0
-    for j, layer in ((0, 0), (len(idx) - 1, L - 1)):
+    within = True
+    units = [(0, 0), (len(idx) - 1, L - 1), (worst_j, worst_l)]
+    for j, layer in dict.fromkeys(units):
         i = idx[j]
         ex, _ = exact_attention(o, caps[i], layer, poss[i], host[j][0], host[j][1],
                                 q_all[layer, i])
-        f64_gpu = max(f64_gpu, float(np.max(np.abs(out_gpu[layer, i] - ex))))
-        f64_orc = max(f64_orc, float(np.max(np.abs(out_b[layer, j] - ex))))
+        e_ex = float(np.max(np.abs(out_gpu[layer, i] - ex)))
+        own = float(np.max(np.abs(out_b[layer, j] - ex)))
+        f64_gpu, f64_orc = max(f64_gpu, e_ex), max(f64_orc, own)
+        within &= e_ex <= 1e-4 and float(per_unit[layer, j]) <= 1e-4 + own
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -732,10 +742,15 @@ def cpu_leg(w: Workload, na: int, nb: int, min_s: float):
                           "seconds": round(ta * reps_a, 2)}}
     parity = {"units_checked": nb * L, "max_abs_out_err_vs_oracle": err,
               "appended_rows_bit_exact": bool(rows_exact),
-              "float64_units": 2, "max_abs_out_err_gpu_vs_float64": f64_gpu,
-              "max_abs_out_err_oracle_vs_float64": f64_orc}
+              "float64_units": len(dict.fromkeys(units)),
+              "max_abs_out_err_gpu_vs_float64": f64_gpu,
+              "max_abs_out_err_oracle_vs_float64": f64_orc,
+              "rule": "per unit: |gpu - float64| <= 1e-4 and |gpu - oracle| <= 1e-4 + "
+                      "|oracle - float64| (float64 on the first, last and worst unit)",
+              "within_rule": bool(within)}
     log(f"{w.name} parity: {nb * L} units, max |gpu - oracle| {err:.3g}, rows bit-exact "
-        f"{rows_exact}, float64: gpu {f64_gpu:.3g}, oracle {f64_orc:.3g}")
+        f"{rows_exact}, float64: gpu {f64_gpu:.3g}, oracle {f64_orc:.3g}, within the rule "
+        f"{within}")
     return cpu, parity
 
 
