@@ -33,6 +33,7 @@ and two units in float64).  rank 0 prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import collections
 import ctypes as C
 import json
 import os
@@ -338,6 +339,10 @@ def main():
                     help="semicolon list of split,chunk,stage,piece: time layer-serial and fused")
     ap.add_argument("--model-only", action="store_true",
                     help="only the whole-decode-step leg (model_forward), printed as its JSON")
+    ap.add_argument("--phases", action="store_true",
+                    help="only the per-phase breakdown of the config's layer-serial launches, "
+                         "from the phase-stamp library (make -C gguf2bin_amd stamps), printed "
+                         "as its JSON")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only the weight-GEMV leg (with --calibrate-copy first when given), "
                          "printed as its JSON")
@@ -350,7 +355,14 @@ def main():
     if hip.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.phases:  # (before anything loads the library)
+        attn.LIBPATH = attn.STAMPS_LIBPATH
     hip.set_device(0)
+    if args.phases:
+        w = Workload(args.config, args, args.n_seq)
+        print(json.dumps({"phases": phases_leg(w, args.steps, args.warmup)}), flush=True)
+        w.close()
+        return
     if args.model_only:
         print(json.dumps({"model_forward": model_leg(args)}), flush=True)
         return
@@ -627,6 +639,69 @@ def model_leg(args):
         return res
     finally:
         os.unlink(path)
+
+
+def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
+    """Where a layer-serial launch's time goes, from the phase-stamp build:
+    thread 0 of every workgroup of a static k_layer launch reads the device's
+    constant wall clock at entry, after the setup (loads, QK-RMSNorm, RoPE,
+    digit planes, the owner's append), after the stream of its positions,
+    after the fold of its waves' position slots, after the merge and the
+    partial stores, and at exit; every combine workgroup at entry and exit.
+    Each layer call is followed by a read of the stamps (the launches
+    themselves run as in the bench).  Per launch: the spread of the
+    workgroups' starts, each phase's median over the workgroups, the first
+    start to the last exit, and the combine after it; medians over every
+    layer call of the timed steps."""
+    ctx, s, n = w.ctx, w.shape, w.n_seq
+    khz = hip.wall_clock_khz(0)
+    cap = 1 << 16
+    ctx.stamps_enable(cap)
+
+    def one_step(rec):
+        ctx.synth_copy(w.qw.ptr, w.q0.ptr, w.nQ * 4)
+        for layer in range(s.n_layers):
+            ctx.attn_layers(layer, 1, w.qw.ptr + layer * n * s.nq * 4,
+                            w.kb.ptr + layer * n * s.nkv * 4, w.vb.ptr + layer * n * s.nkv * 4)
+            st = ctx.stamps_read()
+            if rec is not None:
+                rec.append((st, ctx.last_schedule()))
+
+    for _ in range(max(1, warmup)):
+        one_step(None)
+    rec = []
+    for _ in range(steps):
+        one_step(rec)
+    us = 1e3 / khz  # microseconds per tick
+    per = collections.defaultdict(list)
+    sched = rec[0][1]
+    for st, sc in rec:
+        ks = st[0][st[0][:, 5] != 0].astype(np.int64)
+        cs = st[1][st[1][:, 5] != 0].astype(np.int64)
+        if len(ks) == 0:
+            raise RuntimeError(f"no k_layer stamps (phases need a static k_layer launch): {sc}")
+        t0, t_end = ks[:, 0].min(), ks[:, 5].max()
+        per["workgroups"].append(len(ks))
+        per["start_spread"].append((ks[:, 0].max() - t0) * us)
+        for name, (a, b) in (("setup", (0, 1)), ("stream", (1, 2)), ("fold", (2, 3)),
+                             ("merge_and_partial_stores", (3, 4)), ("exit", (4, 5)),
+                             ("workgroup_total", (0, 5))):
+            per[name].append(float(np.median(ks[:, b] - ks[:, a])) * us)
+        per["first_start_to_last_exit"].append((t_end - t0) * us)
+        if len(cs):
+            per["gap_to_combine"].append((cs[:, 0].min() - t_end) * us)
+            per["combine_first_start_to_last_exit"].append((cs[:, 5].max() - cs[:, 0].min()) * us)
+            per["first_start_to_combine_exit"].append((cs[:, 5].max() - t0) * us)
+    out = {"workload": w.name, "variant": sched.get("variant"), "schedule": sched,
+           "launches": len(rec), "wall_clock_khz": khz,
+           "unit": "us (medians over the launches; per launch, phase = median over workgroups)"}
+    for k, v in per.items():
+        out[k] = round(float(np.median(v)), 2)
+    ev_ms, _, ev_dec, ev_n = w.timed(w.step_layer_serial, steps, warmup)
+    out["same_build_events"] = {"layer_serial_us_per_step": round(ev_ms * 1e3, 1),
+                                "decode_avg_us": round(ev_dec / max(ev_n, 1) * 1e3, 2)}
+    log(f"{w.name} phases: " + ", ".join(f"{k} {out[k]}" for k in per))
+    return out
 
 
 def cpu_leg(w: Workload, na: int, nb: int, min_s: float):

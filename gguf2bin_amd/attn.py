@@ -19,6 +19,11 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBPATH = os.path.join(HERE, "libg2b_attn.so")
+# The phase-stamp build (make -C gguf2bin_amd stamps): the same library with
+# per-workgroup wall-clock stamps in static k_layer launches and their
+# combine; loaded instead of LIBPATH only by bench.py --phases.
+STAMPS_LIBPATH = os.path.join(HERE, "libg2b_attn_stamps.so")
+STAMP_WORDS = 8
 
 G2B_OK, G2B_EINVAL, G2B_EPOS, G2B_ENOKV, G2B_ENOMEM, G2B_EDEVICE, G2B_ESWAP, G2B_EUNSUP = (
     0, -1, -2, -3, -4, -5, -6, -7)
@@ -177,6 +182,11 @@ def lib() -> C.CDLL:
             f = getattr(L, name)
             f.argtypes = args
             f.restype = res
+        if hasattr(L, "g2b_stamps_enable"):  # (the phase-stamp build only)
+            L.g2b_stamps_enable.argtypes = [vp, i32]
+            L.g2b_stamps_enable.restype = C.c_int
+            L.g2b_stamps_read.argtypes = [vp, vp, i32]
+            L.g2b_stamps_read.restype = C.c_int
         _lib = L
     return _lib
 
@@ -519,6 +529,24 @@ class Context:
 
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")
+
+    def stamps_enable(self, cap: int):
+        """Room for the phase stamps of cap workgroups per launch (the
+        phase-stamp build only)."""
+        if not hasattr(lib(), "g2b_stamps_enable"):
+            raise RuntimeError(f"{LIBPATH} has no phase stamps: load {STAMPS_LIBPATH} "
+                               "(make -C gguf2bin_amd stamps) instead")
+        self._check(lib().g2b_stamps_enable(self.h, cap), "g2b_stamps_enable")
+        self._stamp_cap = cap
+
+    def stamps_read(self, clear: bool = True) -> np.ndarray:
+        """The stamps of the last launches: [2][cap][STAMP_WORDS] uint64 (the
+        decode kernel's workgroups, then its combine's), zeroed afterwards
+        when clear."""
+        out = np.zeros((2, self._stamp_cap, STAMP_WORDS), np.uint64)
+        self._check(lib().g2b_stamps_read(self.h, out.ctypes.data, 1 if clear else 0),
+                    "g2b_stamps_read")
+        return out
 
     def profile_read(self):
         """(summed decode-kernel milliseconds, launches) since the last read."""

@@ -92,6 +92,10 @@ struct g2b_ctx {
 
   float *fixed = nullptr;  // this device's copy of `scratch` (g2b_attn_forward_noalloc)
 
+  // phase stamps (DecodeParams.stamps; set only by the G2B_STAMPS build)
+  uint64_t *stamps = nullptr;
+  int32_t stamp_cap = 0;
+
   std::string err;
 };
 
@@ -456,6 +460,8 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.att = att;
   dp.att_stride = att_stride;
   dp.qscale = c->qscale;
+  dp.stamps = c->stamps;
+  dp.stamp_cap = c->stamp_cap;
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
                    c->shape.n_kv_heads * (c->shape.head_dim / 16) <= 64) ? 16 : 0;
@@ -877,6 +883,7 @@ int g2b_ctx_destroy(g2b_ctx *c) {
   if (c->h_seqs) (void)hipHostFree(c->h_seqs);
   if (c->qrot) (void)hipFree(c->qrot);
   if (c->part) (void)hipFree(c->part);
+  if (c->stamps) (void)hipFree(c->stamps);
   if (c->hstage) (void)hipFree(c->hstage);
   if (c->qkn_w) (void)hipFree(c->qkn_w);
   if (c->qkn_on) (void)hipFree(c->qkn_on);
@@ -1336,5 +1343,39 @@ int g2b_ctx_profile_read(g2b_ctx *c, double *decode_ms, int64_t *launches) {
   c->prof_used = 0;
   return G2B_OK;
 }
+
+#ifdef G2B_STAMPS
+// The phase-stamp build's own entry points (libg2b_attn_stamps.so; not part
+// of the ABI of include/, no counterpart in the reference): room for cap
+// workgroups' stamps of a k_layer launch and as many of its combine, all
+// words zero; g2b_stamps_read synchronises the stream and copies out
+// 2 * cap * kStampWords words.
+int g2b_stamps_enable(g2b_ctx *c, int32_t cap) {
+  if (!c || cap < 1) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  if (c->stamps) G2B_HIP(c, hipFree(c->stamps));
+  c->stamps = nullptr;
+  c->stamp_cap = 0;
+  const size_t bytes = (size_t)2 * cap * kStampWords * sizeof(uint64_t);
+  if (hipMalloc((void **)&c->stamps, bytes) != hipSuccess) {
+    c->stamps = nullptr;
+    (void)hipGetLastError();
+    return fail(c, G2B_ENOMEM, "phase stamps");
+  }
+  G2B_HIP(c, hipMemset(c->stamps, 0, bytes));
+  c->stamp_cap = cap;
+  return G2B_OK;
+}
+
+int g2b_stamps_read(g2b_ctx *c, uint64_t *host, int32_t clear) {
+  if (!c || !host || !c->stamps) return G2B_EINVAL;
+  if (int rc = set_device(c)) return rc;
+  const size_t bytes = (size_t)2 * c->stamp_cap * kStampWords * sizeof(uint64_t);
+  G2B_HIP(c, hipStreamSynchronize(c->stream));
+  G2B_HIP(c, hipMemcpy(host, c->stamps, bytes, hipMemcpyDeviceToHost));
+  if (clear) G2B_HIP(c, hipMemset(c->stamps, 0, bytes));
+  return G2B_OK;
+}
+#endif
 
 }  // extern "C"

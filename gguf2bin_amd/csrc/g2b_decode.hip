@@ -130,7 +130,25 @@ __device__ inline double block_sum_d(double x, double *red) {
   return r;
 }
 
+#ifdef G2B_STAMPS
+// Phase stamps of a combine workgroup (thread 0): entry and exit.
+__device__ inline void combine_stamp(const DecodeParams &P, uint64_t in) {
+  const uint64_t g = blockIdx.x + (uint64_t)gridDim.x * (blockIdx.y + (uint64_t)gridDim.y * blockIdx.z);
+  if (threadIdx.x == 0 && P.stamps && g < (uint64_t)P.stamp_cap) {
+    uint64_t *o = P.stamps + ((uint64_t)P.stamp_cap + g) * kStampWords;
+    o[0] = in;
+    o[5] = (uint64_t)wall_clock64();
+  }
+}
+#define G2B_COMBINE_IN const uint64_t stamp_in = (uint64_t)wall_clock64()
+#define G2B_COMBINE_OUT combine_stamp(P, stamp_in)
+#else
+#define G2B_COMBINE_IN ((void)0)
+#define G2B_COMBINE_OUT ((void)0)
+#endif
+
 __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, float *q_out) {
+  G2B_COMBINE_IN;
   __shared__ float w[kCombineMaxParts];
   __shared__ double part_sum[4 * kCombineThreads];
   __shared__ double red[kCombineThreads / 64];
@@ -214,6 +232,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
       for (int t = tid; t < npos; t += blockDim.x)
         at[t] = (float)(exp2((double)at[t] - (double)M) / L);
     }
+    G2B_COMBINE_OUT;
     return;
   }
 
@@ -266,6 +285,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
     for (int t = tid; t < npos; t += blockDim.x)
       a[t] = (float)(exp2((double)a[t] - (double)M) / L);
   }
+  G2B_COMBINE_OUT;
 }
 
 // k_combine with few partials (max_splits <= kCombineFewParts): one wave per
@@ -274,6 +294,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
 // arithmetic as k_combine with a 64-thread workgroup (its block reductions
 // are this wave's), so the two give the same output bit for bit.
 __global__ __launch_bounds__(kCombineThreads) void k_combine_waves(DecodeParams P, float *q_out) {
+  G2B_COMBINE_IN;
   __shared__ float wsh[kCombineThreads / 64][kCombineFewParts];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = blockIdx.x * (kCombineThreads / 64) + wave;
@@ -334,6 +355,7 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine_waves(DecodeParams 
     float *at = P.att + (unit * nh + h) * (size_t)P.att_stride;
     for (int t = lane; t < npos; t += 64) at[t] = (float)(exp2((double)at[t] - (double)M) / L);
   }
+  G2B_COMBINE_OUT;
 }
 
 // ---------------------------------------------------------------- dispatch

@@ -144,7 +144,18 @@ struct DecodeParams {
   // (float)((double)acc / (double)l).
   int32_t direct_out;
   int32_t *span_ctr;  // k_short with several spans: [L][n_seq][n_kv_heads] tickets
+  // Phase stamps (the library built with G2B_STAMPS only; nullptr in the
+  // product build, whose kernels have no stamp code): kStampWords words per
+  // workgroup of a static k_layer launch at [g], of its k_combine at
+  // [stamp_cap + g], g the linear workgroup id (launches of more than
+  // stamp_cap workgroups leave them unwritten).
+  uint64_t *stamps;
+  int32_t stamp_cap;
 };
+// Phase stamp words (wall_clock64, 100 MHz): k_layer 0 entry, 1 setup done,
+// 2 stream done, 3 fold done, 4 partials stored, 5 exit, 6 split index;
+// k_combine 0 entry, 5 exit.
+constexpr int kStampWords = 8;
 // Grid of a static schedule: x = the splits of a (sequence, layer), the
 // fastest index of the linear workgroup order, which the device deals to its
 // eight XCDs in turn.  With an even x, sequence q's first split lands on XCD

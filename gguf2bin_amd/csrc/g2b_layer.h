@@ -780,8 +780,18 @@ __device__ inline void visit_setup(const ShapeDev &sh, const SeqDev &sd, int lay
 // global_load_lds, then read from there.  2: the same chunks loaded into
 // registers with coalesced non-temporal loads one chunk ahead (in flight
 // while the current chunk is consumed) and written to LDS.
+#ifdef G2B_STAMPS
+#define G2B_STAMP(i) (stamp_[i] = wall_clock64())
+#else
+#define G2B_STAMP(i) ((void)0)
+#endif
+
 template <int FMT, int HD, int CD, int G, int U, bool ATT, int STG, bool WQ>
 __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
+#ifdef G2B_STAMPS
+  uint64_t stamp_[kStampWords] = {};
+  G2B_STAMP(0);
+#endif
   static_assert(!WQ || STG != 0, "the work queue streams through LDS");
   extern __shared__ __align__(16) uint8_t lds[];
   __shared__ int32_t s_bcast;
@@ -939,6 +949,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
                                     P.k_in + sidx * nkv, P.v_in + sidx * nkv, P.rope, P.norm,
                                     P.qscale, qrot, kr, vr, rowk, rowv, scr, trq);
     }
+    G2B_STAMP(1);
     constexpr bool kDig = FMT == 1 && !WQ;  // the digit planes come from the setup
 
     // q in registers: F32 rows take the values, Q8_0 rows the digit planes
@@ -1273,6 +1284,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         pipe_step(tb + stride * UP, kn, vn, ka, va);
       }
     }
+    G2B_STAMP(2);
     if (owns_new) {
       typename C::Raw krr[1], vrr[1];
       C::load_row(krr[0], rowk, lo);
@@ -1331,6 +1343,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     // partial per head.  LDS: [wave][slot][head][kPartHead + HD] floats, S
     // slots per wave (1 when the wave folded them).
     constexpr int pstr = kPartHead + HD;
+    G2B_STAMP(3);
     __syncthreads();
     float *ws = reinterpret_cast<float *>(lds);
     if (S > 1 ? lane_on : slot == 0) {
@@ -1385,6 +1398,7 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         pp[1] = lsum;
       }
     }
+    G2B_STAMP(4);
     __syncthreads();  // LDS is free for the next visit
   };
 
@@ -1399,6 +1413,14 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     const bool owns_new = t1 == npos;  // this split holds position pos
     // Positions [t0, tend) stream from HBM; pos itself, when owned, from LDS.
     visit(sd, seq, li, t0, owns_new ? t1 - 1 : t1, owns_new, split, nullptr);
+#ifdef G2B_STAMPS
+    const uint64_t g = blockIdx.x + (uint64_t)gridDim.x * (blockIdx.y + (uint64_t)gridDim.y * blockIdx.z);
+    if (threadIdx.x == 0 && P.stamps && g < (uint64_t)P.stamp_cap) {
+      G2B_STAMP(5);
+      stamp_[6] = (uint64_t)split;
+      for (int i = 0; i < kStampWords; i++) P.stamps[g * kStampWords + i] = stamp_[i];
+    }
+#endif
   } else {
     const int n_units = P.n_seq * P.n_layers_call;
     int32_t *const wq = P.wq + (size_t)P.wq_set * (size_t)P.wq_cap * kWqStride;

@@ -47,6 +47,7 @@ def lib() -> C.CDLL:
         L.hipEventDestroy.argtypes = [C.c_void_p]
         L.hipStreamSynchronize.argtypes = [C.c_void_p]
         L.hipMemGetInfo.argtypes = [C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]
+        L.hipDeviceGetAttribute.argtypes = [C.POINTER(C.c_int), C.c_int, C.c_int]
     return _lib
 
 
@@ -67,6 +68,17 @@ def device_count() -> int:
 
 def set_device(d: int):
     check(lib().hipSetDevice(d), "hipSetDevice")
+
+
+HIP_ATTR_WALL_CLOCK_RATE = 10017  # hipDeviceAttributeWallClockRate (kHz)
+
+
+def wall_clock_khz(d: int = 0) -> int:
+    """Frequency of the device's constant wall clock (wall_clock64), kHz."""
+    v = C.c_int(0)
+    check(lib().hipDeviceGetAttribute(C.byref(v), HIP_ATTR_WALL_CLOCK_RATE, d),
+          "hipDeviceGetAttribute")
+    return v.value
 
 
 def mem_info():
