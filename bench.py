@@ -688,6 +688,15 @@ def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
                              ("workgroup_total", (0, 5))):
             per[name].append(float(np.median(ks[:, b] - ks[:, a])) * us)
         per["first_start_to_last_exit"].append((t_end - t0) * us)
+        xcd = ks[:, 7]
+        firsts = [ks[xcd == x, 0].min() for x in np.unique(xcd)]
+        for x in np.unique(xcd):
+            per[f"xcd{int(x)}_first_start"].append((ks[xcd == x, 0].min() - t0) * us)
+            per[f"xcd{int(x)}_last_exit"].append((ks[xcd == x, 5].max() - t0) * us)
+        per["xcds"].append(len(firsts))
+        per["xcd_first_start_spread"].append((max(firsts) - min(firsts)) * us)
+        per["start_spread_within_xcd"].append(float(np.max(
+            [(ks[xcd == x, 0].max() - ks[xcd == x, 0].min()) * us for x in np.unique(xcd)])))
         if len(cs):
             per["gap_to_combine"].append((cs[:, 0].min() - t_end) * us)
             per["combine_first_start_to_last_exit"].append((cs[:, 5].max() - cs[:, 0].min()) * us)

@@ -153,7 +153,7 @@ struct DecodeParams {
   int32_t stamp_cap;
 };
 // Phase stamp words (wall_clock64, 100 MHz): k_layer 0 entry, 1 setup done,
-// 2 stream done, 3 fold done, 4 partials stored, 5 exit, 6 split index;
+// 2 stream done, 3 fold done, 4 partials stored, 5 exit, 6 split index, 7 XCD;
 // k_combine 0 entry, 5 exit.
 constexpr int kStampWords = 8;
 // Grid of a static schedule: x = the splits of a (sequence, layer), the

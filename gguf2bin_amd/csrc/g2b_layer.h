@@ -1418,6 +1418,8 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
     if (threadIdx.x == 0 && P.stamps && g < (uint64_t)P.stamp_cap) {
       G2B_STAMP(5);
       stamp_[6] = (uint64_t)split;
+      // HW_REG_XCC_ID (hwreg 20), bits 3:0: the XCD the workgroup ran on
+      stamp_[7] = (uint64_t)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
       for (int i = 0; i < kStampWords; i++) P.stamps[g * kStampWords + i] = stamp_[i];
     }
 #endif
