@@ -647,69 +647,68 @@ def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
     constant wall clock at entry, after the setup (loads, QK-RMSNorm, RoPE,
     digit planes, the owner's append), after the stream of its positions,
     after the fold of its waves' position slots, after the merge and the
-    partial stores, and at exit; every combine workgroup at entry and exit.
-    Each layer call is followed by a read of the stamps (the launches
-    themselves run as in the bench).  Per launch: the spread of the
-    workgroups' starts, each phase's median over the workgroups, the first
+    partial stores, and at exit, and notes its XCD; every combine workgroup
+    at entry and exit.  The steps run as the bench runs them (every layer's
+    launches back to back; each call writes its own stamp region, read once
+    per step).  Per launch: the spread of the workgroups' starts (in all and
+    within one XCD), each phase's median over the workgroups, the first
     start to the last exit, and the combine after it; medians over every
     layer call of the timed steps."""
-    ctx, s, n = w.ctx, w.shape, w.n_seq
+    ctx, s = w.ctx, w.shape
     khz = hip.wall_clock_khz(0)
-    cap = 1 << 16
-    ctx.stamps_enable(cap)
-
-    def one_step(rec):
-        ctx.synth_copy(w.qw.ptr, w.q0.ptr, w.nQ * 4)
-        for layer in range(s.n_layers):
-            ctx.attn_layers(layer, 1, w.qw.ptr + layer * n * s.nq * 4,
-                            w.kb.ptr + layer * n * s.nkv * 4, w.vb.ptr + layer * n * s.nkv * 4)
-            st = ctx.stamps_read()
-            if rec is not None:
-                rec.append((st, ctx.last_schedule()))
-
+    cap = max(1024, w.n_seq * 64)
+    ctx.stamps_enable(cap, s.n_layers)
     for _ in range(max(1, warmup)):
-        one_step(None)
+        w.step_layer_serial()
+        ctx.stamps_read()
     rec = []
     for _ in range(steps):
-        one_step(rec)
+        w.step_layer_serial()
+        rec.append((ctx.stamps_read(), ctx.last_schedule()))
     us = 1e3 / khz  # microseconds per tick
     per = collections.defaultdict(list)
     sched = rec[0][1]
-    for st, sc in rec:
-        ks = st[0][st[0][:, 5] != 0].astype(np.int64)
-        cs = st[1][st[1][:, 5] != 0].astype(np.int64)
-        if len(ks) == 0:
-            raise RuntimeError(f"no k_layer stamps (phases need a static k_layer launch): {sc}")
-        t0, t_end = ks[:, 0].min(), ks[:, 5].max()
-        per["workgroups"].append(len(ks))
-        per["start_spread"].append((ks[:, 0].max() - t0) * us)
-        for name, (a, b) in (("setup", (0, 1)), ("stream", (1, 2)), ("fold", (2, 3)),
-                             ("merge_and_partial_stores", (3, 4)), ("exit", (4, 5)),
-                             ("workgroup_total", (0, 5))):
-            per[name].append(float(np.median(ks[:, b] - ks[:, a])) * us)
-        per["first_start_to_last_exit"].append((t_end - t0) * us)
-        xcd = ks[:, 7]
-        firsts = [ks[xcd == x, 0].min() for x in np.unique(xcd)]
-        for x in np.unique(xcd):
-            per[f"xcd{int(x)}_first_start"].append((ks[xcd == x, 0].min() - t0) * us)
-            per[f"xcd{int(x)}_last_exit"].append((ks[xcd == x, 5].max() - t0) * us)
-        per["xcds"].append(len(firsts))
-        per["xcd_first_start_spread"].append((max(firsts) - min(firsts)) * us)
-        per["start_spread_within_xcd"].append(float(np.max(
-            [(ks[xcd == x, 0].max() - ks[xcd == x, 0].min()) * us for x in np.unique(xcd)])))
-        if len(cs):
-            per["gap_to_combine"].append((cs[:, 0].min() - t_end) * us)
-            per["combine_first_start_to_last_exit"].append((cs[:, 5].max() - cs[:, 0].min()) * us)
-            per["first_start_to_combine_exit"].append((cs[:, 5].max() - t0) * us)
+    for st_all, sc in rec:
+        prev_end = None
+        for st in st_all:
+            ks = st[0][st[0][:, 5] != 0].astype(np.int64)
+            cs = st[1][st[1][:, 5] != 0].astype(np.int64)
+            if len(ks) == 0:
+                raise RuntimeError(f"no k_layer stamps (phases need static k_layer launches): {sc}")
+            t0, t_end = ks[:, 0].min(), ks[:, 5].max()
+            per["workgroups"].append(len(ks))
+            per["start_spread"].append((ks[:, 0].max() - t0) * us)
+            for name, (a, b) in (("setup", (0, 1)), ("stream", (1, 2)), ("fold", (2, 3)),
+                                 ("merge_and_partial_stores", (3, 4)), ("exit", (4, 5)),
+                                 ("workgroup_total", (0, 5))):
+                per[name].append(float(np.median(ks[:, b] - ks[:, a])) * us)
+            per["first_start_to_last_exit"].append((t_end - t0) * us)
+            xcd = ks[:, 7]
+            firsts = {int(x): ks[xcd == x, 0].min() for x in np.unique(xcd)}
+            per["xcds"].append(len(firsts))
+            per["xcd_first_start_spread"].append((max(firsts.values()) - t0) * us)
+            per["start_spread_within_xcd"].append(float(np.max(
+                [(ks[xcd == x, 0].max() - ks[xcd == x, 0].min()) * us for x in firsts])))
+            for x, f in firsts.items():
+                per[f"xcd{x}_first_start"].append((f - t0) * us)
+            if prev_end is not None:
+                per["previous_combine_exit_to_first_start"].append((t0 - prev_end) * us)
+            prev_end = t_end
+            if len(cs):
+                per["gap_to_combine"].append((cs[:, 0].min() - t_end) * us)
+                per["combine_first_start_to_last_exit"].append(
+                    (cs[:, 5].max() - cs[:, 0].min()) * us)
+                per["first_start_to_combine_exit"].append((cs[:, 5].max() - t0) * us)
+                prev_end = cs[:, 5].max()
     out = {"workload": w.name, "variant": sched.get("variant"), "schedule": sched,
-           "launches": len(rec), "wall_clock_khz": khz,
+           "launches": sum(len(r[0]) for r in rec), "wall_clock_khz": khz,
            "unit": "us (medians over the launches; per launch, phase = median over workgroups)"}
-    for k, v in per.items():
+    for k, v in sorted(per.items()):
         out[k] = round(float(np.median(v)), 2)
     ev_ms, _, ev_dec, ev_n = w.timed(w.step_layer_serial, steps, warmup)
     out["same_build_events"] = {"layer_serial_us_per_step": round(ev_ms * 1e3, 1),
                                 "decode_avg_us": round(ev_dec / max(ev_n, 1) * 1e3, 2)}
-    log(f"{w.name} phases: " + ", ".join(f"{k} {out[k]}" for k in per))
+    log(f"{w.name} phases: " + ", ".join(f"{k} {out[k]}" for k in sorted(per)))
     return out
 
 

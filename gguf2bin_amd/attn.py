@@ -183,7 +183,7 @@ def lib() -> C.CDLL:
             f.argtypes = args
             f.restype = res
         if hasattr(L, "g2b_stamps_enable"):  # (the phase-stamp build only)
-            L.g2b_stamps_enable.argtypes = [vp, i32]
+            L.g2b_stamps_enable.argtypes = [vp, i32, i32]
             L.g2b_stamps_enable.restype = C.c_int
             L.g2b_stamps_read.argtypes = [vp, vp, i32]
             L.g2b_stamps_read.restype = C.c_int
@@ -530,20 +530,20 @@ class Context:
     def profile(self, enable: bool):
         self._check(lib().g2b_ctx_profile(self.h, 1 if enable else 0), "g2b_ctx_profile")
 
-    def stamps_enable(self, cap: int):
-        """Room for the phase stamps of cap workgroups per launch (the
-        phase-stamp build only)."""
+    def stamps_enable(self, cap: int, launches: int = 1):
+        """Room for the phase stamps of `launches` decode calls of up to cap
+        workgroups each (the phase-stamp build only)."""
         if not hasattr(lib(), "g2b_stamps_enable"):
             raise RuntimeError(f"{LIBPATH} has no phase stamps: load {STAMPS_LIBPATH} "
                                "(make -C gguf2bin_amd stamps) instead")
-        self._check(lib().g2b_stamps_enable(self.h, cap), "g2b_stamps_enable")
-        self._stamp_cap = cap
+        self._check(lib().g2b_stamps_enable(self.h, cap, launches), "g2b_stamps_enable")
+        self._stamp_cap, self._stamp_launches = cap, launches
 
     def stamps_read(self, clear: bool = True) -> np.ndarray:
-        """The stamps of the last launches: [2][cap][STAMP_WORDS] uint64 (the
-        decode kernel's workgroups, then its combine's), zeroed afterwards
-        when clear."""
-        out = np.zeros((2, self._stamp_cap, STAMP_WORDS), np.uint64)
+        """The stamps of the decode calls since the last read:
+        [launches][2][cap][STAMP_WORDS] uint64 (call i's decode kernel
+        workgroups, then its combine's), zeroed afterwards when clear."""
+        out = np.zeros((self._stamp_launches, 2, self._stamp_cap, STAMP_WORDS), np.uint64)
         self._check(lib().g2b_stamps_read(self.h, out.ctypes.data, 1 if clear else 0),
                     "g2b_stamps_read")
         return out

@@ -92,9 +92,11 @@ struct g2b_ctx {
 
   float *fixed = nullptr;  // this device's copy of `scratch` (g2b_attn_forward_noalloc)
 
-  // phase stamps (DecodeParams.stamps; set only by the G2B_STAMPS build)
+  // phase stamps (DecodeParams.stamps; set only by the G2B_STAMPS build):
+  // stamp_launches regions of 2 * stamp_cap * kStampWords words, decode call
+  // i using region i % stamp_launches since the last read
   uint64_t *stamps = nullptr;
-  int32_t stamp_cap = 0;
+  int32_t stamp_cap = 0, stamp_launches = 0, stamp_next = 0;
 
   std::string err;
 };
@@ -460,7 +462,9 @@ int run_layers(g2b_ctx *c, const SeqDev *d_seqs, const SeqDev &one, int32_t n_se
   dp.att = att;
   dp.att_stride = att_stride;
   dp.qscale = c->qscale;
-  dp.stamps = c->stamps;
+  dp.stamps = c->stamps ? c->stamps + (size_t)(c->stamp_next++ % c->stamp_launches) * 2 *
+                                           c->stamp_cap * kStampWords
+                        : nullptr;
   dp.stamp_cap = c->stamp_cap;
   // half-block lanes need twice the lanes per position; keep them only where they fit
   dp.tune_chunk = (c->tune_chunk == 16 && c->shape.kv_q8 &&
@@ -1346,17 +1350,18 @@ int g2b_ctx_profile_read(g2b_ctx *c, double *decode_ms, int64_t *launches) {
 
 #ifdef G2B_STAMPS
 // The phase-stamp build's own entry points (libg2b_attn_stamps.so; not part
-// of the ABI of include/, no counterpart in the reference): room for cap
-// workgroups' stamps of a k_layer launch and as many of its combine, all
-// words zero; g2b_stamps_read synchronises the stream and copies out
-// 2 * cap * kStampWords words.
-int g2b_stamps_enable(g2b_ctx *c, int32_t cap) {
-  if (!c || cap < 1) return G2B_EINVAL;
+// of the ABI of include/, no counterpart in the reference): room for the
+// stamps of `launches` decode calls, each cap workgroups of a k_layer launch
+// and as many of its combine, all words zero; g2b_stamps_read synchronises
+// the stream, copies out launches * 2 * cap * kStampWords words (call i
+// since the previous read in region i) and starts the next calls at region 0.
+int g2b_stamps_enable(g2b_ctx *c, int32_t cap, int32_t launches) {
+  if (!c || cap < 1 || launches < 1) return G2B_EINVAL;
   if (int rc = set_device(c)) return rc;
   if (c->stamps) G2B_HIP(c, hipFree(c->stamps));
   c->stamps = nullptr;
-  c->stamp_cap = 0;
-  const size_t bytes = (size_t)2 * cap * kStampWords * sizeof(uint64_t);
+  c->stamp_cap = c->stamp_launches = c->stamp_next = 0;
+  const size_t bytes = (size_t)launches * 2 * cap * kStampWords * sizeof(uint64_t);
   if (hipMalloc((void **)&c->stamps, bytes) != hipSuccess) {
     c->stamps = nullptr;
     (void)hipGetLastError();
@@ -1364,14 +1369,17 @@ int g2b_stamps_enable(g2b_ctx *c, int32_t cap) {
   }
   G2B_HIP(c, hipMemset(c->stamps, 0, bytes));
   c->stamp_cap = cap;
+  c->stamp_launches = launches;
   return G2B_OK;
 }
 
 int g2b_stamps_read(g2b_ctx *c, uint64_t *host, int32_t clear) {
   if (!c || !host || !c->stamps) return G2B_EINVAL;
   if (int rc = set_device(c)) return rc;
-  const size_t bytes = (size_t)2 * c->stamp_cap * kStampWords * sizeof(uint64_t);
+  const size_t bytes =
+      (size_t)c->stamp_launches * 2 * c->stamp_cap * kStampWords * sizeof(uint64_t);
   G2B_HIP(c, hipStreamSynchronize(c->stream));
+  c->stamp_next = 0;
   G2B_HIP(c, hipMemcpy(host, c->stamps, bytes, hipMemcpyDeviceToHost));
   if (clear) G2B_HIP(c, hipMemset(c->stamps, 0, bytes));
   return G2B_OK;

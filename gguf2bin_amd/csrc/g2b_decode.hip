@@ -138,6 +138,7 @@ __device__ inline void combine_stamp(const DecodeParams &P, uint64_t in) {
     uint64_t *o = P.stamps + ((uint64_t)P.stamp_cap + g) * kStampWords;
     o[0] = in;
     o[5] = (uint64_t)wall_clock64();
+    o[7] = (uint64_t)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);  // XCD
   }
 }
 #define G2B_COMBINE_IN const uint64_t stamp_in = (uint64_t)wall_clock64()
@@ -284,6 +285,79 @@ __global__ __launch_bounds__(kCombineThreads) void k_combine(DecodeParams P, flo
     float *a = P.att + (sidx * nh + h) * (size_t)P.att_stride;
     for (int t = tid; t < npos; t += blockDim.x)
       a[t] = (float)(exp2((double)a[t] - (double)M) / L);
+  }
+  G2B_COMBINE_OUT;
+}
+
+// k_combine for one unit's many partials (static splits, more than
+// kCombineFewParts of them, at most kCombineThreads): each head's dims in
+// kCombineParts parts, one workgroup per (head, part), so that a workgroup
+// requests R rows of a quarter of the dims instead of a whole head's rows
+// (c1 / c2, 129 partials of 16 heads: 16 workgroups of 17 row loads per
+// thread became 64 of 5).  The same float64 merge as k_combine - weights
+// exp2(m_p - M), sums over the partials in GRP groups, then over the groups
+// in order, divided by the sum of the weighted l - with the partials dealt
+// to more groups, so the order of the float64 additions differs.
+constexpr int kCombineParts = 4;
+template <int R>
+__global__ __launch_bounds__(kCombineThreads) void k_combine_part(DecodeParams P, float *q_out) {
+  G2B_COMBINE_IN;
+  __shared__ float w[kCombineThreads];
+  __shared__ double gs[4 * kCombineThreads];  // [group][dims of the part]
+  __shared__ double red[kCombineThreads / 64];
+  const int h = (int)blockIdx.x / kCombineParts, part = (int)blockIdx.x - h * kCombineParts;
+  const int seq = blockIdx.y, li = blockIdx.z, tid = threadIdx.x;
+  const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
+  const int npos = sd.pos + 1;
+  const int np = (npos + P.split_len - 1) / P.split_len;
+  const int HD = P.sh.head_dim, nh = P.sh.n_heads, PD = HD / kCombineParts;
+  const size_t pstr = (size_t)(kPartHead + HD);
+  const size_t sidx = (size_t)li * (size_t)P.n_seq + (size_t)seq;
+  const float *base = P.part + (sidx * nh + h) * (size_t)P.max_splits * pstr;
+  const int tpr = PD / 4, GRP = kCombineThreads / tpr;  // (the host checks np <= GRP * R)
+  const int grp = tid / tpr, q = tid - grp * tpr;
+  // every load unconditional, as in k_combine's one-round path
+  float2 ml = *reinterpret_cast<const float2 *>(base + (size_t)min(tid, np - 1) * pstr);
+  if (tid >= np) ml = make_float2(kNegBig, 0.f);
+  float4 v[R];
+  const float *a = base + kPartHead + part * PD + 4 * q;
+#pragma unroll
+  for (int u = 0; u < R; u++) {
+    const int p = min(grp + GRP * u, np - 1);
+    v[u] = *reinterpret_cast<const float4 *>(a + (size_t)p * pstr);
+  }
+  const float M = block_max_f(ml.x, reinterpret_cast<float *>(red));
+  double lsum = 0.0;
+  if (tid < np) {
+    const float wp = exp2f(ml.x - M);
+    w[tid] = wp;
+    lsum = (double)ml.y * (double)wp;
+  }
+  const double L = block_sum_d(lsum, red);  // (its barriers also publish w)
+  double o[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int u = 0; u < R; u++) {
+    const int p = grp + GRP * u;
+    if (p < np) {
+      const double wp = (double)w[p];
+      o[0] = fma((double)v[u].x, wp, o[0]);
+      o[1] = fma((double)v[u].y, wp, o[1]);
+      o[2] = fma((double)v[u].z, wp, o[2]);
+      o[3] = fma((double)v[u].w, wp, o[3]);
+    }
+  }
+  for (int j = 0; j < 4; j++) gs[grp * PD + 4 * q + j] = o[j];
+  __syncthreads();
+  float *out = q_out + sidx * (size_t)(nh * HD) + (size_t)h * HD + (size_t)part * PD;
+  for (int d = tid; d < PD; d += kCombineThreads) {
+    double sum = 0.0;
+    for (int g = 0; g < GRP; g++) sum += gs[g * PD + d];
+    out[d] = (float)(sum / L);
+  }
+  if (P.att && part == 0) {
+    float *at = P.att + (sidx * nh + h) * (size_t)P.att_stride;
+    for (int t = tid; t < npos; t += blockDim.x)
+      at[t] = (float)(exp2((double)at[t] - (double)M) / L);
   }
   G2B_COMBINE_OUT;
 }
@@ -464,6 +538,18 @@ hipError_t launch_combine(const DecodeParams &p, int n_layers, hipStream_t s) {
     const int hpw = kCombineThreads / 64;  // heads per workgroup
     dim3 g4((p.sh.n_heads + hpw - 1) / hpw, p.n_seq, n_layers);
     hipLaunchKernelGGL(k_combine_waves, g4, dim3(kCombineThreads), 0, s, p, p.q_out);
+    return hipGetLastError();
+  }
+  // Static splits of few units with many partials: a workgroup per (head,
+  // quarter of its dims).
+  const int hd = p.sh.head_dim, grp = kCombineThreads / (hd / kCombineParts / 4);
+  if (!p.wq && hd % (4 * kCombineParts) == 0 && p.max_splits <= kCombineThreads &&
+      p.max_splits <= 8 * grp) {
+    dim3 gp(p.sh.n_heads * kCombineParts, p.n_seq, n_layers);
+    if (p.max_splits <= 4 * grp)
+      hipLaunchKernelGGL(k_combine_part<4>, gp, dim3(kCombineThreads), 0, s, p, p.q_out);
+    else
+      hipLaunchKernelGGL(k_combine_part<8>, gp, dim3(kCombineThreads), 0, s, p, p.q_out);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_combine, grid, dim3(kCombineThreads), 0, s, p, p.q_out);
