@@ -153,8 +153,9 @@ struct DecodeParams {
   int32_t stamp_cap;
 };
 // Phase stamp words (wall_clock64, 100 MHz): k_layer 0 entry, 1 setup done,
-// 2 stream done, 3 fold done, 4 partials stored, 5 exit, 6 split index, 7 XCD;
-// k_combine 0 entry, 5 exit, 7 XCD.
+// 2 stream done, 3 fold done, 4 partials stored, 5 exit, 6 split index (work
+// queue: visits, phases 1-4 the last visit's), 7 XCD; k_combine 0 entry,
+// 5 exit, 7 XCD.
 constexpr int kStampWords = 8;
 // Grid of a static schedule: x = the splits of a (sequence, layer), the
 // fastest index of the linear workgroup order, which the device deals to its

@@ -1444,6 +1444,9 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
         const int seq = unit % P.n_seq, li = unit / P.n_seq;
         const SeqDev sd = P.seqs ? P.seqs[seq] : P.one;
         visit(sd, seq, li, 0, sd.pos, pslot == 0, pslot, ctr);
+#ifdef G2B_STAMPS
+        stamp_[6]++;  // visits (phases 1-4 are the last visit's)
+#endif
       }
       if (fresh_left) {
         if (threadIdx.x == 0)
@@ -1486,6 +1489,14 @@ __global__ __launch_bounds__(kThreads) void k_layer(DecodeParams P) {
       __syncthreads();
       if (unit < 0) break;
     }
+#ifdef G2B_STAMPS
+    const uint64_t g = blockIdx.x;
+    if (threadIdx.x == 0 && P.stamps && g < (uint64_t)P.stamp_cap) {
+      G2B_STAMP(5);
+      stamp_[7] = (uint64_t)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
+      for (int i = 0; i < kStampWords; i++) P.stamps[g * kStampWords + i] = stamp_[i];
+    }
+#endif
   }
 }
 
