@@ -643,12 +643,13 @@ def model_leg(args):
 
 def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
     """Where a layer-serial launch's time goes, from the phase-stamp build:
-    thread 0 of every workgroup of a static k_layer launch reads the device's
+    thread 0 of every workgroup of a k_layer launch reads the device's
     constant wall clock at entry, after the setup (loads, QK-RMSNorm, RoPE,
     digit planes, the owner's append), after the stream of its positions,
     after the fold of its waves' position slots, after the merge and the
-    partial stores, and at exit, and notes its XCD; every combine workgroup
-    at entry and exit.  The steps run as the bench runs them (every layer's
+    partial stores, and at exit, and notes its XCD (a work-queue workgroup:
+    its visits, and the phases of its last one); every combine workgroup at
+    entry and exit.  The steps run as the bench runs them (every layer's
     launches back to back; each call writes its own stamp region, read once
     per step).  Per launch: the spread of the workgroups' starts (in all and
     within one XCD), each phase's median over the workgroups, the first
@@ -656,7 +657,7 @@ def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
     layer call of the timed steps."""
     ctx, s = w.ctx, w.shape
     khz = hip.wall_clock_khz(0)
-    cap = max(1024, w.n_seq * 64)
+    cap = max(4096, w.n_seq * 64)
     ctx.stamps_enable(cap, s.n_layers)
     for _ in range(max(1, warmup)):
         w.step_layer_serial()
@@ -668,19 +669,34 @@ def phases_leg(w: Workload, steps: int, warmup: int) -> dict:
     us = 1e3 / khz  # microseconds per tick
     per = collections.defaultdict(list)
     sched = rec[0][1]
+    wq = sched.get("piece_len", 0) > 0
     for st_all, sc in rec:
         prev_end = None
         for st in st_all:
             ks = st[0][st[0][:, 5] != 0].astype(np.int64)
             cs = st[1][st[1][:, 5] != 0].astype(np.int64)
             if len(ks) == 0:
-                raise RuntimeError(f"no k_layer stamps (phases need static k_layer launches): {sc}")
+                raise RuntimeError(f"no k_layer stamps (phases need k_layer launches): {sc}")
             t0, t_end = ks[:, 0].min(), ks[:, 5].max()
             per["workgroups"].append(len(ks))
             per["start_spread"].append((ks[:, 0].max() - t0) * us)
+            if wq:
+                # work queue: the workgroups' exits, visits, and the phases of
+                # each workgroup's last visit (its first when it made one)
+                ex = (ks[:, 5] - t0) * us
+                for q in (10, 50, 90):
+                    per[f"exit_p{q}"].append(float(np.percentile(ex, q)))
+                per["exit_last"].append(float(ex.max()))
+                per["visits_mean"].append(float(ks[:, 6].mean()))
+                one = ks[ks[:, 6] == 1]
+                if len(one):
+                    per["single_visit_setup_from_entry"].append(
+                        float(np.median(one[:, 1] - one[:, 0])) * us)
             for name, (a, b) in (("setup", (0, 1)), ("stream", (1, 2)), ("fold", (2, 3)),
                                  ("merge_and_partial_stores", (3, 4)), ("exit", (4, 5)),
                                  ("workgroup_total", (0, 5))):
+                if wq and name in ("setup", "workgroup_total"):
+                    continue  # (from entry: the last visit's setup follows earlier visits)
                 per[name].append(float(np.median(ks[:, b] - ks[:, a])) * us)
             per["first_start_to_last_exit"].append((t_end - t0) * us)
             xcd = ks[:, 7]
