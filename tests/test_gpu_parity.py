@@ -351,12 +351,13 @@ def test_static_splits_without_weights(gpu_device, name):
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_g2", "qwen3_f32_g2", "smollm2_f32_g3", "hd64_q8_g3"])
-@pytest.mark.parametrize("split", [8, 16, 28])
+@pytest.mark.parametrize("split", [3, 8, 16, 28])
 def test_many_partials_merge_bit_exact(gpu_device, name, split):
-    """33-256 partials per head (k_combine's one-round merge): one sequence of
-    900 positions in 113 / 57 / 33 splits against the oracle, and the same
-    output bits with and without the weights output (the weights are a
-    separate pass over the raw scores)."""
+    """Many partials per head: one sequence of 900 positions in 300 splits
+    (more than 256: k_combine's merge in rounds) and 113 / 57 / 33 (33-256:
+    k_combine_part, a workgroup per head and quarter of its dims) against the
+    oracle, and the same output bits with and without the weights output (the
+    weights are a separate pass over the raw scores)."""
     nh, nkv, hd, arch, q8 = SHAPES[name]
     o = orc.Shape(2, nh, nkv, hd, 1e5 if arch == orc.ARCH_LLAMA else 1e6, arch, q8)
     tune = (split, 0, 0, -1)
