@@ -163,8 +163,21 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+#ifdef G2B_STAMPS
+// Phase stamps of a k_short workgroup (thread 0; one-span calls): 0 entry,
+// 1 inputs and the norm factors in, 2 RoPE done, 3 append done, 4 scores
+// done, 6 softmax done, 5 exit (after V and the output), 7 XCD.
+#define G2B_SSTAMP(i) (sst_[i] = wall_clock64())
+#else
+#define G2B_SSTAMP(i) ((void)0)
+#endif
+
 template <int FMT, int HD>
 __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
+#ifdef G2B_STAMPS
+  uint64_t sst_[kStampWords] = {};
+  G2B_SSTAMP(0);
+#endif
   using Geo = ShortGeom<FMT, HD>;
   constexpr int NB = Geo::NB, HB = Geo::HB, XS = Geo::XS, EPL = Geo::EPL;
   constexpr int half = HD / 2;
@@ -218,6 +231,26 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     const float *src = xh < G ? qo + xh * HD : (xh == G ? ki : vi);
     x4 = *reinterpret_cast<const float4 *>(src + 4 * xj);
   }
+  // Step 3's inputs for this thread's first pair (pair t: head t / half):
+  // the norm weights of its two elements and the cos/sin of pos, loaded
+  // with the inputs, before the KV loads, so that step 3 waits for neither.
+  const float *wq = norm_weights(P.norm, layer, 0, HD);
+  const float *wk = norm_weights(P.norm, layer, 1, HD);
+  const float *cs = (sh.rope_on && P.rope) ? P.rope + (size_t)pos * HD : nullptr;
+  float wa0 = 1.f, wb0 = 1.f, c0 = 1.f, s0 = 0.f;
+  if (t < (G + 1) * half) {
+    const int h = t / half, j = t - h * half;
+    int ia, ib;
+    rope_pair_index(sh.arch_llama, j, half, ia, ib);
+    if (const float *w = h < G ? wq : wk) {
+      wa0 = w[ia];
+      wb0 = w[ib];
+    }
+    if (cs) {
+      c0 = cs[2 * j];
+      s0 = cs[2 * j + 1];
+    }
+  }
   // Every KV load of the span is issued now, so that it is in flight during
   // the setup: the K pieces of its positions below pos (each thread one
   // piece per round) and, per wave, the V elements of its positions
@@ -238,10 +271,9 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     fetch_v<FMT, EPL>(vb + (size_t)(tp < pos ? tp : 0) * row, e0, vq[i], vsb[i]);
   }
   if (has_x) *reinterpret_cast<float4 *>(xs + xh * XS + 4 * xj) = x4;
-  const float *wq = norm_weights(P.norm, layer, 0, HD);
-  const float *wk = norm_weights(P.norm, layer, 1, HD);
   __syncthreads();
 
+  G2B_SSTAMP(1);
   // 2. QK-RMSNorm factors
   if (t <= G) {
     const float *w = t < G ? wq : wk;
@@ -265,25 +297,27 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   }
   __syncthreads();
 
-  // 3. (w * x) * inv, then RoPE(pos), per pair
-  const float *cs = (sh.rope_on && P.rope) ? P.rope + (size_t)pos * HD : nullptr;
+  // 3. (w * x) * inv, then RoPE(pos), per pair (the first pair's inputs
+  // are in registers)
   for (int i = t; i < (G + 1) * half; i += kSThreads) {
     const int h = i / half, j = i - h * half;
+    const bool first = i == t;
     int ia, ib;
     rope_pair_index(sh.arch_llama, j, half, ia, ib);
     float *x = xs + h * XS;
     float a = x[ia], c = x[ib];
     if (const float *w = h < G ? wq : wk) {
       const float f = inv[h];
-      a = (w[ia] * a) * f;
-      c = (w[ib] * c) * f;
+      a = ((first ? wa0 : w[ia]) * a) * f;
+      c = ((first ? wb0 : w[ib]) * c) * f;
     }
-    if (cs) rope_pair(a, c, cs[2 * j], cs[2 * j + 1]);
+    if (cs) rope_pair(a, c, first ? c0 : cs[2 * j], first ? s0 : cs[2 * j + 1]);
     x[ia] = a;
     x[ib] = c;
   }
   __syncthreads();
 
+  G2B_SSTAMP(2);
   // 4. the new row's slice (the span of pos only): LDS copy, then the caches
   const float *kr = xs + G * XS, *vr = xs + (G + 1) * XS;
   if (!owner) {
@@ -315,6 +349,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
     }
   }
 
+  G2B_SSTAMP(3);
   // 5. scores: position tp's NB pieces on NB consecutive lanes
   const float qscale = P.qscale;
 #pragma unroll
@@ -348,6 +383,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   }
   __syncthreads();
 
+  G2B_SSTAMP(4);
   // 6. softmax statistics: wave g for head g
   if (wave < G) {
     float *s = sc + wave * kShortMaxPos;
@@ -368,12 +404,24 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   }
   __syncthreads();
 
+  G2B_SSTAMP(6);
   // 7. V-accumulate, wave w over positions w, w + 4, ... (pos itself from LDS)
   float acc[kSMaxG][EPL];
 #pragma unroll
   for (int g = 0; g < kSMaxG; g++)
 #pragma unroll
     for (int i = 0; i < EPL; i++) acc[g][i] = 0.f;
+  // The weights of the wave's positions: lane i holds position wave + 4i's
+  // (one LDS read per head), handed to every lane by readlane in the loop -
+  // an LDS read per position and head, each waited for, was 2-5 us of the
+  // kernel's 9-12 at 40-100 positions.
+  static_assert(VI <= 64, "one lane per position of the wave");
+  float pw[kSMaxG];
+#pragma unroll
+  for (int g = 0; g < kSMaxG; g++)
+    pw[g] = (g < G && lane < VI && wave + 4 * lane < n_here)
+                ? sc[g * kShortMaxPos + wave + 4 * lane]
+                : 0.f;
 #pragma unroll
   for (int i = 0; i < VI; i++) {
     const int lp = wave + 4 * i, tp = t0 + lp;
@@ -385,7 +433,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
 #pragma unroll
       for (int g = 0; g < kSMaxG; g++) {
         if (g < G) {
-          const float p = sc[g * kShortMaxPos + lp];
+          const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pw[g]), i));
 #pragma unroll
           for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, v[e], acc[g][e]);
         }
@@ -404,6 +452,14 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
                       (accs[(2 * kSMaxG + g) * HD + e] + accs[(3 * kSMaxG + g) * HD + e]);
       qo[g * HD + e] = s / lsum[g];
     }
+#ifdef G2B_STAMPS
+    const uint64_t gw = blockIdx.x + (uint64_t)gridDim.x * (blockIdx.y + (uint64_t)gridDim.y * blockIdx.z);
+    if (threadIdx.x == 0 && P.stamps && gw < (uint64_t)P.stamp_cap) {
+      G2B_SSTAMP(5);
+      sst_[7] = (uint64_t)(__builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 15);
+      for (int i = 0; i < kStampWords; i++) P.stamps[gw * kStampWords + i] = sst_[i];
+    }
+#endif
     return;
   }
 
