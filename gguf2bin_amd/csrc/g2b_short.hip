@@ -74,6 +74,40 @@ struct PieceRaw<0> {
   float4 f[8];
 };
 
+// A load from device (global) memory through a global-address-space
+// pointer: the compiler then counts it with the other vector loads (a flat
+// load returns out of order with them, so a wait for any load behind it
+// becomes a wait for all).
+template <typename T>
+__device__ __forceinline__ T gload(const void *p) {
+  return *(const __attribute__((address_space(1))) T *)p;
+}
+typedef float gload_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t gload_u32x2 __attribute__((ext_vector_type(2)));
+template <>
+__device__ __forceinline__ float4 gload<float4>(const void *p) {
+  const gload_f32x4 v = *(const __attribute__((address_space(1))) gload_f32x4 *)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+template <>
+__device__ __forceinline__ uint2 gload<uint2>(const void *p) {
+  const gload_u32x2 v = *(const __attribute__((address_space(1))) gload_u32x2 *)p;
+  return make_uint2(v.x, v.y);
+}
+
+// Piece b of a head slice in the cache (global memory), as fetch_piece.
+template <int FMT>
+__device__ __forceinline__ void fetch_piece_g(const uint8_t *slice, int b, PieceRaw<FMT> &r) {
+  if constexpr (FMT == 1) {
+    const uint8_t *w = slice + ((34 * b) & ~3);
+#pragma unroll
+    for (int i = 0; i < 9; i++) r.d[i] = gload<uint32_t>(w + 4 * i);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.f[i] = gload<float4>(slice + 128 * b + 16 * i);
+  }
+}
+
 template <int FMT>
 __device__ __forceinline__ void fetch_piece(const uint8_t *slice, int b, PieceRaw<FMT> &r) {
   if constexpr (FMT == 1) {
@@ -138,6 +172,29 @@ __device__ __forceinline__ void fetch_v(const uint8_t *slice, int e0, uint32_t &
   }
 }
 
+// The same from the cache (global memory).
+template <int FMT, int EPL>
+__device__ __forceinline__ void fetch_v_g(const uint8_t *slice, int e0, uint32_t &q, uint32_t &s) {
+  if constexpr (FMT == 1) {
+    const uint8_t *blk = slice + 34 * (e0 >> 5);
+    s = gload<uint16_t>(blk);
+    if constexpr (EPL == 2)
+      q = gload<uint16_t>(blk + 2 + (e0 & 31));
+    else
+      q = gload<uint8_t>(blk + 2 + (e0 & 31));
+  } else {
+    const uint8_t *f = slice + 4 * e0;
+    if constexpr (EPL == 2) {
+      const uint2 t = gload<uint2>(f);
+      q = t.x;
+      s = t.y;
+    } else {
+      q = gload<uint32_t>(f);
+      s = 0u;
+    }
+  }
+}
+
 // Dequantised as kv_val_row does (d * q).
 template <int FMT, int EPL>
 __device__ __forceinline__ void decode_v(uint32_t q, uint32_t s, float (&v)[EPL]) {
@@ -161,6 +218,17 @@ __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
   return x;
+}
+
+// A workgroup barrier that orders LDS only: the phases up to the output
+// share nothing else, so the KV loads issued with the inputs stay in flight
+// through the norm, RoPE and append phases (a full __syncthreads waits for
+// every outstanding global load first); the compiler waits for each KV
+// register where the scores and V use it.
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 #ifdef G2B_STAMPS
@@ -226,52 +294,58 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   constexpr int P4 = HD / 4;
   const bool has_x = t < (G + 2) * P4;
   const int xh = t / P4, xj = t - xh * P4;
-  float4 x4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (has_x) {
-    const float *src = xh < G ? qo + xh * HD : (xh == G ? ki : vi);
-    x4 = *reinterpret_cast<const float4 *>(src + 4 * xj);
-  }
+  // (every load of step 1 unconditional, threads without a piece reading
+  // one that exists: a load in a per-thread branch is waited for, with all
+  // loads before it, where the branches join)
+  const int xhc = xh < G + 2 ? xh : G + 1;
+  const float *src = xhc < G ? qo + xhc * HD : (xhc == G ? ki : vi);
+  const float4 x4 = gload<float4>(src + 4 * xj);
   // Step 3's inputs for this thread's first pair (pair t: head t / half):
   // the norm weights of its two elements and the cos/sin of pos, loaded
   // with the inputs, before the KV loads, so that step 3 waits for neither.
   const float *wq = norm_weights(P.norm, layer, 0, HD);
   const float *wk = norm_weights(P.norm, layer, 1, HD);
   const float *cs = (sh.rope_on && P.rope) ? P.rope + (size_t)pos * HD : nullptr;
-  float wa0 = 1.f, wb0 = 1.f, c0 = 1.f, s0 = 0.f;
-  if (t < (G + 1) * half) {
-    const int h = t / half, j = t - h * half;
+  // (unconditional too: a missing table reads q instead, and the values of
+  // a thread without a pair or a table are not used)
+  float wa0, wb0, c0, s0;
+  {
+    const int pt = t < (G + 1) * half ? t : 0;
+    const int h = pt / half, j = pt - h * half;
     int ia, ib;
     rope_pair_index(sh.arch_llama, j, half, ia, ib);
-    if (const float *w = h < G ? wq : wk) {
-      wa0 = w[ia];
-      wb0 = w[ib];
-    }
-    if (cs) {
-      c0 = cs[2 * j];
-      s0 = cs[2 * j + 1];
-    }
+    const float *w = h < G ? wq : wk;
+    const float *ws = w ? w : qo, *cz = cs ? cs : qo;
+    wa0 = gload<float>(ws + ia);
+    wb0 = gload<float>(ws + ib);
+    c0 = gload<float>(cz + 2 * j);
+    s0 = gload<float>(cz + 2 * j + 1);
   }
   // Every KV load of the span is issued now, so that it is in flight during
   // the setup: the K pieces of its positions below pos (each thread one
   // piece per round) and, per wave, the V elements of its positions
   // t0 + wave, t0 + wave + 4, ... below pos.  Other slots read row 0 instead
-  // (in bounds, never used), which keeps the loads unconditional.
+  // (in bounds, never used), which keeps the loads unconditional.  The
+  // inputs go to LDS between the K and the V loads: the wait for them counts
+  // the K loads issued after them, not the V loads' 2 * VI (more than the
+  // wait counter holds), and the barriers up to the scores order LDS only,
+  // so the KV bytes land during steps 2-4.
   const int b = t % NB;
   PieceRaw<FMT> kraw[RK];
 #pragma unroll
   for (int r = 0; r < RK; r++) {
     const int tp = t0 + r * PPR + t / NB;
-    fetch_piece<FMT>(kb + (size_t)(tp < pos ? tp : 0) * row, b, kraw[r]);
+    fetch_piece_g<FMT>(kb + (size_t)(tp < pos ? tp : 0) * row, b, kraw[r]);
   }
+  if (has_x) *reinterpret_cast<float4 *>(xs + xh * XS + 4 * xj) = x4;
   const int e0 = lane * EPL;
   uint32_t vq[VI], vsb[VI];
 #pragma unroll
   for (int i = 0; i < VI; i++) {
     const int tp = t0 + wave + 4 * i;
-    fetch_v<FMT, EPL>(vb + (size_t)(tp < pos ? tp : 0) * row, e0, vq[i], vsb[i]);
+    fetch_v_g<FMT, EPL>(vb + (size_t)(tp < pos ? tp : 0) * row, e0, vq[i], vsb[i]);
   }
-  if (has_x) *reinterpret_cast<float4 *>(xs + xh * XS + 4 * xj) = x4;
-  __syncthreads();
+  barrier_lds();
 
   G2B_SSTAMP(1);
   // 2. QK-RMSNorm factors
@@ -295,27 +369,36 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
       inv[t] = __fdiv_rn(1.f, sqrtf(__fdiv_rn(ss, (float)HD) + P.norm.eps));
     }
   }
-  __syncthreads();
+  barrier_lds();
 
-  // 3. (w * x) * inv, then RoPE(pos), per pair (the first pair's inputs
-  // are in registers)
-  for (int i = t; i < (G + 1) * half; i += kSThreads) {
+  // 3. (w * x) * inv, then RoPE(pos), per pair: the thread's first pair
+  // from the inputs in registers (no global load here, whose wait would
+  // include the V loads still in flight), further ones (more than
+  // kSThreads pairs: groups of 4) from the tables
+  auto rotate = [&](int i, float wa, float wb, float co, float si) {
     const int h = i / half, j = i - h * half;
-    const bool first = i == t;
     int ia, ib;
     rope_pair_index(sh.arch_llama, j, half, ia, ib);
     float *x = xs + h * XS;
     float a = x[ia], c = x[ib];
-    if (const float *w = h < G ? wq : wk) {
+    if (h < G ? wq : wk) {
       const float f = inv[h];
-      a = ((first ? wa0 : w[ia]) * a) * f;
-      c = ((first ? wb0 : w[ib]) * c) * f;
+      a = (wa * a) * f;
+      c = (wb * c) * f;
     }
-    if (cs) rope_pair(a, c, first ? c0 : cs[2 * j], first ? s0 : cs[2 * j + 1]);
+    if (cs) rope_pair(a, c, co, si);
     x[ia] = a;
     x[ib] = c;
+  };
+  if (t < (G + 1) * half) rotate(t, wa0, wb0, c0, s0);
+  for (int i = t + kSThreads; i < (G + 1) * half; i += kSThreads) {
+    const int h = i / half, j = i - h * half;
+    int ia, ib;
+    rope_pair_index(sh.arch_llama, j, half, ia, ib);
+    const float *w = h < G ? wq : wk;
+    rotate(i, w ? w[ia] : 1.f, w ? w[ib] : 1.f, cs ? cs[2 * j] : 1.f, cs ? cs[2 * j + 1] : 0.f);
   }
-  __syncthreads();
+  barrier_lds();
 
   G2B_SSTAMP(2);
   // 4. the new row's slice (the span of pos only): LDS copy, then the caches
@@ -337,7 +420,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
       *reinterpret_cast<float4 *>((is_k ? rowk : rowv) + 16 * j) = v;
     }
   }
-  __syncthreads();
+  barrier_lds();
   if (owner) {
     constexpr int W = HB / 4;  // dwords of a slice (HB is a multiple of 4)
     const size_t off = (size_t)pos * row;
@@ -381,7 +464,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
       }
     }
   }
-  __syncthreads();
+  barrier_lds();
 
   G2B_SSTAMP(4);
   // 6. softmax statistics: wave g for head g
@@ -402,7 +485,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
       msh[wave] = m;
     }
   }
-  __syncthreads();
+  barrier_lds();
 
   G2B_SSTAMP(6);
   // 7. V-accumulate, wave w over positions w, w + 4, ... (pos itself from LDS)
@@ -444,7 +527,7 @@ __global__ __launch_bounds__(kSThreads) void k_short(DecodeParams P) {
   for (int g = 0; g < kSMaxG; g++)
 #pragma unroll
     for (int i = 0; i < EPL; i++) accs[(wave * kSMaxG + g) * HD + e0 + i] = acc[g][i];
-  __syncthreads();
+  barrier_lds();
   if (nspans == 1) {
     for (int i = t; i < G * HD; i += kSThreads) {
       const int g = i / HD, e = i - g * HD;
