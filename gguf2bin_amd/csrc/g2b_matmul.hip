@@ -15,7 +15,9 @@
 // boundary at or before the block (blocks are 2-byte aligned), extracting
 // the bytes with v_perm.  Arithmetic is fp32 like the reference: per block
 // sum_j q_j x_j by FMA, times the fp16 scale, summed over the lane's blocks
-// and then across the row's lanes.
+// and then across the row's lanes.  Q8_0 over many rows (the lm head) takes
+// x as int8 digit planes instead (wg_x_digits): integer dot products per
+// block, then the same fp16 scale and sums.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -35,6 +37,7 @@ constexpr int kGemvGroup = 8;   // blocks per lane in flight (x in LDS or the ca
 constexpr int kGemvMinSteps = 8;            // wave-steps per wave, where there are enough
 constexpr int kGemvMaxXLds = 64 * 1024;     // x staged in LDS up to this many bytes
 constexpr int kGemvMmaMinRows = 32768;      // k_gemv_mma for Q4_0 matrices of this many rows
+constexpr int kGemvXdMinRows = 32768;       // Q8_0 with x as digit planes (XD) from this many rows
 
 template <typename T>
 __device__ __forceinline__ T nt_load(const void *p) {
@@ -255,6 +258,110 @@ __device__ __forceinline__ void lane_x(const GemvParams &P, const float *xs, int
   }
 }
 
+// x as four signed int8 digit planes of a 31-bit fixed point per 32-element
+// block (the Q8_0 XD form): m = rint(x * 2^(30-e)), 2^(e-1) <= max|x| < 2^e,
+// m = d0 + 256 d1 + 65536 d2 + 2^24 d3.  The workgroup makes every block's
+// planes once into LDS - dig[b][plane][chunk] (a dword = one plane of four
+// elements), then exps[b] and units[b] (1, or NaN for a block with a
+// non-finite x: its rows' sums are then NaN) - from x as the rows read it
+// (pro_x4), and each lane loads its blocks' planes into registers.  A
+// block's sum_j q_j x_j is then four chains of v_dot4_i32_i8 (exact in
+// int32), combined in fp32 and scaled by the fp16 scale and 2^(e-30): about
+// half the VALU operations of the convert-and-FMA form per weight.  x's
+// rounding (2^-31 of its block maximum) is far below fp32's.
+__device__ __forceinline__ void wg_x_digits(const GemvParams &P, const float *xs, float inv,
+                                            uint32_t *dig) {
+  const int nb = P.nb;
+  int32_t *exps = reinterpret_cast<int32_t *>(dig + nb * 32);
+  float *units = reinterpret_cast<float *>(exps + nb);
+  for (int it = threadIdx.x; it < nb * 8; it += kGemvThreads) {
+    const int b = it >> 3, j = it & 7;  // chunk j: elements 4j .. 4j+3 of block b
+    const float4 v = pro_x4(P, xs, 32 * b + 4 * j, inv);
+    float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    mx = fmaxf(mx, __shfl_xor(mx, 4));
+    int e = 0;
+    (void)frexpf(mx, &e);
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t pl[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      int m = (int)rintf(ldexpf(xv[k], 30 - e));  // |m| <= 2^30, exact scaling
+      int d[4];
+#pragma unroll
+      for (int q = 0; q < 3; q++) {
+        d[q] = ((m + 128) & 255) - 128;
+        m = (m - d[q]) >> 8;
+      }
+      d[3] = m;
+#pragma unroll
+      for (int q = 0; q < 4; q++) pl[q] |= ((uint32_t)d[q] & 0xFFu) << (8 * k);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) dig[(b * 4 + q) * 8 + j] = pl[q];
+    if (j == 0) {
+      exps[b] = e;
+      units[b] = (mx <= 3.402823466e38f) ? 1.f : __int_as_float(0x7fc00000);
+    }
+  }
+  __syncthreads();
+}
+
+// A lane's x blocks (KB of them, blocks b0 + LPR * k below nb) as digit
+// planes, their exponents and units (zero past nb).
+template <int LPR, int KB>
+__device__ __forceinline__ void lane_xd(const GemvParams &P, const uint32_t *dig, int b0,
+                                        uint32_t (&xd)[KB][4][8], int (&xe)[KB],
+                                        float (&xu)[KB]) {
+  const int nb = P.nb;
+  const int32_t *exps = reinterpret_cast<const int32_t *>(dig + nb * 32);
+  const float *units = reinterpret_cast<const float *>(exps + nb);
+#pragma unroll
+  for (int k = 0; k < KB; k++) {
+    const int b = b0 + LPR * k;
+    const bool on = b < nb;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint4 a = make_uint4(0u, 0u, 0u, 0u), c = make_uint4(0u, 0u, 0u, 0u);
+      if (on) {
+        a = *reinterpret_cast<const uint4 *>(dig + (b * 4 + q) * 8);
+        c = *reinterpret_cast<const uint4 *>(dig + (b * 4 + q) * 8 + 4);
+      }
+      xd[k][q][0] = a.x;
+      xd[k][q][1] = a.y;
+      xd[k][q][2] = a.z;
+      xd[k][q][3] = a.w;
+      xd[k][q][4] = c.x;
+      xd[k][q][5] = c.y;
+      xd[k][q][6] = c.z;
+      xd[k][q][7] = c.w;
+    }
+    xe[k] = on ? exps[b] : 0;
+    xu[k] = on ? units[b] : 0.f;
+  }
+}
+
+// sum_j q_j x_j of one Q8_0 block against x's digit planes.
+__device__ __forceinline__ float block_dot_xd(const BlockRaw<1> &r, const uint32_t (&d)[4][8],
+                                              int e, float u) {
+  int s[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) s[q] = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t w = payload_word(r.d, j, r.sh);
+#pragma unroll
+    for (int q = 0; q < 4; q++) s[q] = __builtin_amdgcn_sdot4((int)w, (int)d[q][j], s[q], false);
+  }
+  // |s3| <= 32*128*64, so s3*256 + s2 fits in int32
+  const float t = (float)(s[3] * 256 + s[2]);
+  const float sum = fmaf(fmaf(t, 256.f, (float)s[1]), 256.f, (float)s[0]);
+  // times the scale, then 2^(e-30) (ldexp: no overflow or early underflow
+  // for blocks of very large or very small x)
+  return ldexpf(sum * scale_of(r.d[0], r.sh), e - 30) * u;
+}
+
 // Row `row` of the launch's concatenated segments: its weights, and the
 // store of its result (segment 0 adds the residual res when given:
 // x[i] += xb[i], l5_model.c:583, :597).
@@ -281,10 +388,12 @@ __device__ __forceinline__ float lanes_sum(float v) {
 
 // Q8_0 / Q4_0.  KB > 0: the lane's x blocks (KB of them) live in registers,
 // prepared while the first weights are in flight (the fused forms: LDS of n
-// floats for SiLU x up); KB == -1: any nb, x staged once per workgroup in
+// floats for SiLU x up); with XD (Q8_0) as digit planes (wg_x_digits, after
+// those n floats in LDS); KB == -1: any nb, x staged once per workgroup in
 // LDS; KB == 0: any nb, x read per block through the cache.
-template <int FMT, int LPR, int KB>
+template <int FMT, int LPR, int KB, bool XD = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
+  static_assert(!XD || (FMT == 1 && KB > 0), "digit planes: Q8_0 with x in registers");
   extern __shared__ float xs[];
   constexpr int RPS = 64 / LPR;  // rows per wave-step
   constexpr int BB = block_bytes<FMT>();
@@ -292,7 +401,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
   const int gw = blockIdx.x * (kGemvThreads / 64) + (threadIdx.x >> 6);
   const int rr = lane / LPR, c = lane % LPR;
   const int nb = P.nb;
-  [[maybe_unused]] float xr[KB > 0 ? KB : 1][32];
+  [[maybe_unused]] float xr[(KB > 0 && !XD) ? KB : 1][32];
+  [[maybe_unused]] uint32_t xd[XD ? KB : 1][4][8];
+  [[maybe_unused]] int xe[XD ? KB : 1];
+  [[maybe_unused]] float xu[XD ? KB : 1];
   if constexpr (KB < 0) {
     const int n4 = nb * 8;
     for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * kGemvThreads) {
@@ -335,13 +447,24 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
         float inv = 1.f;
         if (P.pro == kProSiluMul) wg_silu_mul(P, xs);
         if (P.pro == kProRmsnorm) inv = wg_rms_stage(P, xs);
-        lane_x<LPR, KB>(P, xs, c, nb, inv, xr);
+        if constexpr (XD) {
+          uint32_t *dig = reinterpret_cast<uint32_t *>(xs + (P.pro != kProNone ? P.n : 0));
+          wg_x_digits(P, xs, inv, dig);
+          lane_xd<LPR, KB>(P, dig, c, xd, xe, xu);
+        } else {
+          lane_x<LPR, KB>(P, xs, c, nb, inv, xr);
+        }
       }
 #pragma unroll
       for (int u = 0; u < UN; u++) {
         float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < KB; k++) acc += block_dot<FMT>(raw[u][k], xr[k]);
+        for (int k = 0; k < KB; k++) {
+          if constexpr (XD)
+            acc += block_dot_xd(raw[u][k], xd[k], xe[k], xu[k]);
+          else
+            acc += block_dot<FMT>(raw[u][k], xr[k]);
+        }
         acc = lanes_sum<LPR>(acc);
         if (ok[u] && c == 0) seg_store(P, row[u], acc);
       }
@@ -674,13 +797,13 @@ inline size_t pro_lds(const GemvParams &p) {
 
 // Resident workgroups per CU of a k_gemv_q instance (with or without the
 // prologue's dynamic LDS), queried once.
-template <int FMT, int LPR, int KB>
+template <int FMT, int LPR, int KB, bool XD = false>
 int occ_q(size_t lds) {
   static int cached[2] = {0, 0};
   int &o = cached[lds ? 1 : 0];
   if (o == 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_q<FMT, LPR, KB>, kGemvThreads,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_q<FMT, LPR, KB, XD>, kGemvThreads,
                                                      lds) != hipSuccess || n < 1) {
       (void)hipGetLastError();
       n = 1;
@@ -690,8 +813,14 @@ int occ_q(size_t lds) {
   return o;
 }
 
+// kb: 1, 2 x in registers, -1 x in LDS, 0 x through the cache; Q8_0 only:
+// 11, 12 x as digit planes in registers (XD, one or two blocks per lane)
 template <int FMT, int LPR>
 int occ_q_lpr(int kb, size_t lds) {
+  if constexpr (FMT == 1 && LPR >= 16) {
+    if (kb == 11) return occ_q<FMT, LPR, 1, true>(lds);
+    if (kb == 12) return occ_q<FMT, LPR, 2, true>(lds);
+  }
   switch (kb) {
     case 1: return occ_q<FMT, LPR, 1>(lds);
     case 2: return occ_q<FMT, LPR, 2>(lds);
@@ -716,6 +845,16 @@ int occ_q_fmt(int lpr, int kb, size_t lds) {
 template <int FMT, int LPR>
 hipError_t launch_q_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t s) {
   const dim3 blk(kGemvThreads);
+  if constexpr (FMT == 1 && LPR >= 16) {
+    if (kb == 11 || kb == 12) {
+      const size_t lds = pro_lds(p) + (size_t)p.nb * 34u * 4u;  // + digit planes, exps, units
+      if (kb == 11)
+        hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 1, true>), grid, blk, lds, s, p);
+      else
+        hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 2, true>), grid, blk, lds, s, p);
+      return hipGetLastError();
+    }
+  }
   switch (kb) {
     case 1: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 1>), grid, blk, pro_lds(p), s, p); break;
     case 2: hipLaunchKernelGGL((k_gemv_q<FMT, LPR, 2>), grid, blk, pro_lds(p), s, p); break;
@@ -848,15 +987,21 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   const int kb = (p.nb + lpr - 1) / lpr;
   const int rps = 64 / lpr;
   p.steps = (p.d + rps - 1) / rps;
-  const int kbv = !p.x_vec4                     ? 0
-                  : kb <= 2                     ? kb
-                  : p.nb * 128 <= kGemvMaxXLds ? -1
-                                                : 0;
+  int kbv = !p.x_vec4                     ? 0
+            : kb <= 2                     ? kb
+            : p.nb * 128 <= kGemvMaxXLds ? -1
+                                          : 0;
+  // Q8_0 with x in registers over many rows: x as digit planes (the
+  // workgroup's digit prologue pays where every wave has many rows; LPR >=
+  // 16 keeps the instances few)
+  if (fmt == 1 && kbv > 0 && lpr >= 16 && p.d >= kGemvXdMinRows) kbv += 10;
   // every wave loads the x of its blocks once: at least kGemvMinSteps steps
   // per wave where there are enough, at least 4 waves per CU, at most one
   // resident round of workgroups (a partial second round would leave most
   // of the chip idle at the end)
-  const size_t lds = kbv < 0 ? (size_t)p.nb * 128u : pro_lds(p);
+  const size_t lds = kbv < 0    ? (size_t)p.nb * 128u
+                     : kbv > 10 ? pro_lds(p) + (size_t)p.nb * 34u * 4u
+                                : pro_lds(p);
   const int occ = fmt == 1   ? occ_q_fmt<1>(lpr, kbv, lds)
                   : fmt == 2 ? occ_q_fmt<2>(lpr, kbv, lds)
                              : occ_q_fmt<3>(lpr, kbv, lds);

@@ -162,3 +162,39 @@ def test_q4_matrix_core_path(gpu_device, case):
         finally:
             ctx.weights_free(wd)
     check(out, x, w, t, n, d, f"q4 matrix cores {case}")
+
+
+@pytest.mark.parametrize("n", [512, 1024, 2048, 3072])
+@pytest.mark.parametrize("case", ["normal", "outlier", "zero_blocks", "tiny", "huge"])
+def test_q8_digit_plane_path(gpu_device, n, case):
+    """Q8_0 products over at least 32768 rows of 16-96 blocks take x as four
+    int8 digit planes of a 31-bit fixed point per block (integer dot
+    products against the quants): the same bar as every GEMV, with the x
+    that stresses the digits (one channel 3e4 x the others, whole blocks of
+    zeros, x near the bottom of the normal range and near the top), one and
+    two blocks per lane."""
+    d, t = 33000, orc.T_Q8_0
+    rng = np.random.default_rng(77 + n)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    if case == "outlier":
+        x[37] = np.float32(3e4)
+    elif case == "zero_blocks":
+        x[64:160] = 0
+        x[n - 24:] = 0
+    elif case == "tiny":
+        x = (x * np.float32(1e-36)).astype(np.float32)
+    elif case == "huge":
+        x = (x * np.float32(1e30)).astype(np.float32)
+    print(f"[gemv] q8 digit planes n={n} {case}", flush=True)
+    with attn.Context(SHAPE) as ctx:
+        wd = ctx.weights_upload(w)
+        try:
+            xd = hip.to_device(x)
+            od = hip.DeviceBuffer(d * 4)
+            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+            ctx.sync()
+            out = od.download(np.float32, d)
+        finally:
+            ctx.weights_free(wd)
+    check(out, x, w, t, n, d, f"q8 digit planes n {n} {case}")

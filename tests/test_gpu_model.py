@@ -55,6 +55,11 @@ CASES = {
     "qwen3_q4_1_tied": (dict(dim=256, hidden_dim=512, n_layers=2, n_heads=4, n_kv_heads=2,
                              vocab=300, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
                         attn.ARCH_QWEN3, F_QK_NORM | F_TIE_EMBD, 3, 3, None),
+    # an output matrix of 40000 Q8_0 rows: rmsnorm + logits with x as digit
+    # planes (the lm-head form)
+    "qwen3_q8_big_vocab": (dict(dim=512, hidden_dim=1024, n_layers=1, n_heads=8, n_kv_heads=4,
+                                vocab=40000, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
+                           attn.ARCH_QWEN3, F_QK_NORM, 8, 8, 8),
     # rows of 132 blocks: rmsnorm + Q/K/V, rmsnorm + gate/up and rmsnorm +
     # logits on the split-row GEMV
     "wide_dim_q4": (dict(dim=4224, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=4,
@@ -134,7 +139,7 @@ def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_tied", "llama_q4_f16emb", "mixed_types",
-                                  "wide_dim_q4"])
+                                  "wide_dim_q4", "qwen3_q8_big_vocab"])
 def test_fused_launches_match_separate(gpu_device, tmp_path, name):
     """The fused GEMV launches (rmsnorm, SiLU x up and the residual inside
     them, Q/K/V and gate/up as segments of one launch) against the same step
