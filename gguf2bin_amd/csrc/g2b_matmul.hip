@@ -30,13 +30,15 @@ namespace {
 
 typedef float gemv_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t gemv_u32x4 __attribute__((ext_vector_type(4)));
+// four dwords at any 4-byte boundary (global memory takes multi-dword loads
+// at dword alignment)
+typedef uint32_t gemv_u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvUnroll = 4;  // steps whose loads are in flight together
 constexpr int kGemvGroup = 8;   // blocks per lane in flight (x in LDS or the cache)
 constexpr int kGemvMinSteps = 8;            // wave-steps per wave, where there are enough
 constexpr int kGemvMaxXLds = 64 * 1024;     // x staged in LDS up to this many bytes
-constexpr int kGemvMmaMinRows = 32768;      // k_gemv_mma for Q4_0 matrices of this many rows
 constexpr int kGemvXdMinRows = 32768;       // Q8_0 with x as digit planes (XD) from this many rows
 
 template <typename T>
@@ -539,6 +541,56 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
   float *units = reinterpret_cast<float *>(dig + NB * 32);
   int32_t *exps = reinterpret_cast<int32_t *>(units + NB);
   int32_t *dsum = exps + NB;
+  // x into digit planes, while the first trip's weights load
+  auto x_digits = [&]() {
+    for (int it = threadIdx.x; it < NB * 8; it += kGemvThreads) {
+      const int b = it >> 3, j = it & 7;  // chunk j: elements 4j .. 4j+3
+      const float4 v = *reinterpret_cast<const float4 *>(P.x + 32 * b + 4 * j);
+      float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+      mx = fmaxf(mx, __shfl_xor(mx, 1));
+      mx = fmaxf(mx, __shfl_xor(mx, 2));
+      mx = fmaxf(mx, __shfl_xor(mx, 4));
+      int e = 0;
+      (void)frexpf(mx, &e);
+      const float xv[4] = {v.x, v.y, v.z, v.w};
+      uint32_t pl[4] = {0u, 0u, 0u, 0u};
+      int ps[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        int m = (int)rintf(ldexpf(xv[k], 30 - e));  // |m| <= 2^30, exact scaling
+        int d[4];
+#pragma unroll
+        for (int q = 0; q < 3; q++) {
+          d[q] = ((m + 128) & 255) - 128;
+          m = (m - d[q]) >> 8;
+        }
+        d[3] = m;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          pl[q] |= ((uint32_t)d[q] & 0xFFu) << (8 * k);
+          ps[q] += d[q];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        dig[(b * 4 + q) * 8 + j] = pl[q];
+        int t = ps[q];
+        t += __shfl_xor(t, 1);
+        t += __shfl_xor(t, 2);
+        t += __shfl_xor(t, 4);
+        ps[q] = t;
+      }
+      if (j == 0) {
+        // the block's exponent, and 1 (NaN for a non-finite x: the rows'
+        // sums then are NaN)
+        exps[b] = e;
+        units[b] = (mx <= 3.402823466e38f) ? 1.f : __int_as_float(0x7fc00000);
+#pragma unroll
+        for (int q = 0; q < 4; q++) dsum[b * 4 + q] = ps[q];
+      }
+    }
+    __syncthreads();
+  };
   const int stride = P.n_waves;
   for (int s0 = gw, trip = 0;; s0 += stride * UN, trip++) {
     // this trip's spans: UN wave-steps of four rows, each lane its row's
@@ -552,62 +604,26 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
       const int st = s0 + u * stride;
       row[u] = st * 4 + r;
       ok[u] = st < P.steps && row[u] < P.d;
-      const uint32_t *src =
-          reinterpret_cast<const uint32_t *>(P.w + (size_t)(ok[u] ? row[u] : 0) * P.row_bytes +
-                                             g * (BPL * BB));
+      // (global-space 16-byte loads of the 4-byte aligned span, dwords for
+      // the rest: as generic-pointer dwords the compiler issued them one by
+      // one)
+      const __attribute__((address_space(1))) uint32_t *src =
+          (const __attribute__((address_space(1))) uint32_t *)(P.w +
+                                                              (size_t)(ok[u] ? row[u] : 0) *
+                                                                  P.row_bytes +
+                                                              g * (BPL * BB));
 #pragma unroll
-      for (int i = 0; i < NW; i++) wvs[u][i] = ok[u] ? src[i] : 0u;
-    }
-    if (trip == 0) {
-      // x into digit planes, while the weights load
-      for (int it = threadIdx.x; it < NB * 8; it += kGemvThreads) {
-        const int b = it >> 3, j = it & 7;  // chunk j: elements 4j .. 4j+3
-        const float4 v = *reinterpret_cast<const float4 *>(P.x + 32 * b + 4 * j);
-        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        mx = fmaxf(mx, __shfl_xor(mx, 4));
-        int e = 0;
-        (void)frexpf(mx, &e);
-        const float xv[4] = {v.x, v.y, v.z, v.w};
-        uint32_t pl[4] = {0u, 0u, 0u, 0u};
-        int ps[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          int m = (int)rintf(ldexpf(xv[k], 30 - e));  // |m| <= 2^30, exact scaling
-          int d[4];
-#pragma unroll
-          for (int q = 0; q < 3; q++) {
-            d[q] = ((m + 128) & 255) - 128;
-            m = (m - d[q]) >> 8;
-          }
-          d[3] = m;
-#pragma unroll
-          for (int q = 0; q < 4; q++) {
-            pl[q] |= ((uint32_t)d[q] & 0xFFu) << (8 * k);
-            ps[q] += d[q];
-          }
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-          dig[(b * 4 + q) * 8 + j] = pl[q];
-          int t = ps[q];
-          t += __shfl_xor(t, 1);
-          t += __shfl_xor(t, 2);
-          t += __shfl_xor(t, 4);
-          ps[q] = t;
-        }
-        if (j == 0) {
-          // the block's exponent, and 1 (NaN for a non-finite x: the rows'
-          // sums then are NaN)
-          exps[b] = e;
-          units[b] = (mx <= 3.402823466e38f) ? 1.f : __int_as_float(0x7fc00000);
-#pragma unroll
-          for (int q = 0; q < 4; q++) dsum[b * 4 + q] = ps[q];
-        }
+      for (int i = 0; i + 4 <= NW; i += 4) {
+        const gemv_u32x4_a4 v = *(const __attribute__((address_space(1))) gemv_u32x4_a4 *)(src + i);
+        wvs[u][i] = ok[u] ? v.x : 0u;
+        wvs[u][i + 1] = ok[u] ? v.y : 0u;
+        wvs[u][i + 2] = ok[u] ? v.z : 0u;
+        wvs[u][i + 3] = ok[u] ? v.w : 0u;
       }
-      __syncthreads();
+#pragma unroll
+      for (int i = NW & ~3; i < NW; i++) wvs[u][i] = ok[u] ? src[i] : 0u;
     }
+    if (trip == 0) x_digits();
 #pragma unroll
     for (int u = 0; u < UN; u++) {
       const uint32_t *wv = wvs[u];
@@ -875,20 +891,22 @@ hipError_t launch_split_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t 
   return hipGetLastError();
 }
 
-// k_gemv_mma<2, 2> (Q4_0, 1024-element rows): resident workgroups per CU,
-// queried once.
-int occ_mma_q4(size_t lds) {
+// k_gemv_mma<FMT, 2> (Q8_0 / Q4_0, 1024-element rows): resident workgroups
+// per CU, queried once per form.
+template <int FMT>
+int occ_mma(size_t lds) {
   static int cached = 0;
-  if (cached <= 0) {
+  int &o = cached;
+  if (o <= 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_mma<2, 2>, kGemvThreads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_mma<FMT, 2>, kGemvThreads, lds) !=
         hipSuccess) {
       (void)hipGetLastError();
       n = 1;
     }
-    cached = std::max(1, n);
+    o = std::max(1, n);
   }
-  return cached;
+  return o;
 }
 
 template <int FMT>
@@ -962,24 +980,30 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
            : fmt == 2 ? launch_split<2>(p, 64, kb, dim3(wgs), s)
                       : launch_split<3>(p, 64, kb, dim3(wgs), s);
   }
-  // The int8 matrix cores (k_gemv_mma) where they pay: plain (unfused) Q4_0
-  // products of 1024-element rows, at least kGemvMmaMinRows of them (the lm
-  // head: 18.7 against 26.2 us), x 16-byte and the weights 4-byte aligned.  Measured slower
-  // elsewhere (its per-lane dword loads; same box): Q8_0 lm head 34.4 against
-  // 31.1 us, Q4_0 4096 x 14336 29.6 against 13.8 us, 4096-row matrices
-  // 4.7-5.0 against 4.4 us (the digit prologue of every workgroup); a variant
-  // staging four rows per wave through LDS with 16-byte loads was slower still.
-  if (fmt == 2 && !fused && p.x_vec4 && p.nb == 32 && p.d >= kGemvMmaMinRows &&
-      ((uintptr_t)p.w & 3u) == 0) {
+  // The int8 matrix cores (k_gemv_mma) where they pay: plain (unfused) Q8_0
+  // and Q4_0 products of 1024-element rows, at least kGemvMmaMinRows of them
+  // (gemv_mma_plain; the lm head: Q8_0 26.0 against 30.6 us for x's digit
+  // planes on the VALU, Q4_0 16.7 against 26.2 us for the VALU form), x
+  // 16-byte and the weights 4-byte aligned.  Each lane loads its row span
+  // with 16-byte loads (as single dwords: 34.4 and 19.0 us).  The rmsnorm
+  // prologue inside it measured 34.8 us (every workgroup normalising and
+  // digitising x before its loads): the model runs its logits as rmsnorm
+  // and this plain product instead.  Measured slower elsewhere: Q4_0 4096 x
+  // 14336 29.6 against 13.8 us, 4096-row matrices 4.7-5.0 against 4.4 us
+  // (the digit prologue of every workgroup).
+  if (!fused && p.x_vec4 && gemv_mma_plain(type, p.n, p.d) && ((uintptr_t)p.w & 3u) == 0) {
     p.steps = (p.d + 3) / 4;
     const size_t lds = (size_t)p.nb * (32u * 4u + 4u + 4u + 16u);
-    const int occ = occ_mma_q4(lds);
+    const int occ = fmt == 1 ? occ_mma<1>(lds) : occ_mma<2>(lds);
     const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
                                         std::min(p.steps, n_cu * 4)),
                                n_cu * std::max(1, occ) * waves_per_wg);
     const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
     p.n_waves = wgs * waves_per_wg;
-    hipLaunchKernelGGL((k_gemv_mma<2, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    if (fmt == 1)
+      hipLaunchKernelGGL((k_gemv_mma<1, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    else
+      hipLaunchKernelGGL((k_gemv_mma<2, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
     return hipGetLastError();
   }
   int lpr = 1;

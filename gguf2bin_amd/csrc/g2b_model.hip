@@ -502,7 +502,11 @@ int enqueue_step(g2b_model *m, int32_t max_pos) {
   if (!on) return G2B_EINVAL;
   const g2b_slot *out = m->get(G2B_R_OUTPUT, -1);
   if (!out) out = emb;  // tied embeddings (l5_model.c:602)
-  if (m->fuse && gemv_fusable_pro(out->type, dim)) {
+  // (an output matrix the int8 matrix cores take - 1024-element rows, many
+  // of them - gets the rmsnorm as its own launch and the plain product:
+  // normalising and digitising x in every workgroup of the product cost more
+  // than the launch)
+  if (m->fuse && gemv_fusable_pro(out->type, dim) && !gemv_mma_plain(out->type, dim, c.vocab)) {
     GemvParams p{};
     p.out = m->logits;
     p.x = m->x;

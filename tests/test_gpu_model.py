@@ -60,6 +60,16 @@ CASES = {
     "qwen3_q8_big_vocab": (dict(dim=512, hidden_dim=1024, n_layers=1, n_heads=8, n_kv_heads=4,
                                 vocab=40000, seq_len=64, head_dim=64, eps=1e-6, rope_theta=1e6),
                            attn.ARCH_QWEN3, F_QK_NORM, 8, 8, 8),
+    # 1024-element rows and 33000 output rows: rmsnorm + logits on the int8
+    # matrix cores (tied Q8_0 embeddings; a Q4_0 output matrix)
+    "qwen3_q8_mma_lm_head": (dict(dim=1024, hidden_dim=1024, n_layers=1, n_heads=8, n_kv_heads=4,
+                                  vocab=33000, seq_len=64, head_dim=128, eps=1e-6,
+                                  rope_theta=1e6),
+                             attn.ARCH_QWEN3, F_QK_NORM | F_TIE_EMBD, 8, 8, None),
+    "llama_q4_mma_lm_head": (dict(dim=1024, hidden_dim=1024, n_layers=1, n_heads=8, n_kv_heads=2,
+                                  vocab=33000, seq_len=64, head_dim=128, eps=1e-5,
+                                  rope_theta=5e5),
+                             attn.ARCH_LLAMA, 0, 2, 2, 2),
     # rows of 132 blocks: rmsnorm + Q/K/V, rmsnorm + gate/up and rmsnorm +
     # logits on the split-row GEMV
     "wide_dim_q4": (dict(dim=4224, hidden_dim=512, n_layers=1, n_heads=4, n_kv_heads=4,
@@ -139,7 +149,8 @@ def test_graph_replays_match_eager(gpu_device, tmp_path, kv_q8):
 
 
 @pytest.mark.parametrize("name", ["qwen3_q8_tied", "llama_q4_f16emb", "mixed_types",
-                                  "wide_dim_q4", "qwen3_q8_big_vocab"])
+                                  "wide_dim_q4", "qwen3_q8_big_vocab", "qwen3_q8_mma_lm_head",
+                                  "llama_q4_mma_lm_head"])
 def test_fused_launches_match_separate(gpu_device, tmp_path, name):
     """The fused GEMV launches (rmsnorm, SiLU x up and the residual inside
     them, Q/K/V and gate/up as segments of one launch) against the same step
