@@ -307,11 +307,12 @@ inline bool gemv_fusable(int32_t type, int32_t n) {
   return (type == kTypeQ8_0 || type == kTypeQ4_0) && n > 0 && n % 32 == 0 && n / 32 <= 512;
 }
 // Whether launch_gemv runs a plain product of this type and shape on the
-// int8 matrix cores (k_gemv_mma: Q8_0 / Q4_0 rows of 1024 elements, at least
-// kGemvMmaMinRows rows - the lm head).
+// int8 matrix cores (k_gemv_mma: Q8_0 / Q4_0 / Q4_1 rows of 1024 elements,
+// at least kGemvMmaMinRows rows - the lm head).
 constexpr int32_t kGemvMmaMinRows = 32768;
 inline bool gemv_mma_plain(int32_t type, int32_t n, int32_t d) {
-  return (type == kTypeQ8_0 || type == kTypeQ4_0) && n == 1024 && d >= kGemvMmaMinRows;
+  return (type == kTypeQ8_0 || type == kTypeQ4_0 || type == kTypeQ4_1) && n == 1024 &&
+         d >= kGemvMmaMinRows;
 }
 // The prologues keep x * w or SiLU x up of all of x in LDS: n floats within
 // 60 KiB.

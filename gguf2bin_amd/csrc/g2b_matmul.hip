@@ -526,7 +526,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
 template <int FMT, int BPL>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
   extern __shared__ float xs[];  // the digit planes of x
-  constexpr int BB = FMT == 1 ? 34 : 18;
+  constexpr int BB = FMT == 1 ? 34 : FMT == 2 ? 18 : 20;
   constexpr int NB = 16 * BPL;
   constexpr int NW = BPL * BB / 4;  // dwords of a lane's span (BPL even)
   // wave-steps in flight: about 72 registers of weights
@@ -631,12 +631,15 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
 #pragma unroll
       for (int k = 0; k < BPL; k++) {
         const int b = g * BPL + k;
-        const int o = k * BB;  // the block's first byte in the span (o + 2: quants)
+        // the block's first byte in the span (quants from o + 2; Q4_1: d, m,
+        // then the nibbles from o + 4)
+        const int o = k * BB;
         typedef int v4i __attribute__((ext_vector_type(4)));
         v4i dd = {0, 0, 0, 0};
-        // quant word j of the block: bytes o + 2 + 4j .. (o is even)
+        // quant word j of the block: bytes o + 2 + 4j .. (o is even), Q4_1
+        // o + 4 + 4j (o a multiple of 4)
         auto qword = [&](int jw) -> uint32_t {
-          const int byte = o + 2 + 4 * jw;
+          const int byte = o + (FMT == 3 ? 4 : 2) + 4 * jw;
           const int wi = byte >> 2;
           return (byte & 2) ? __builtin_amdgcn_perm(wv[wi + 1], wv[wi], 0x05040302u) : wv[wi];
         };
@@ -657,17 +660,34 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
             dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[4 + jw], (int)((w >> 4) & 0x0F0F0F0Fu),
                                                    dd, 0, 0, 0);
           }
+          if constexpr (FMT == 2) {
 #pragma unroll
-          for (int q = 0; q < 4; q++) dd[q] -= 8 * dsum[b * 4 + q];
+            for (int q = 0; q < 4; q++) dd[q] -= 8 * dsum[b * 4 + q];
+          }
         }
-        // |D3| <= 32*128*64, so D3*256 + D2 fits in int32
-        const float t = (float)(dd[3] * 256 + dd[2]);
-        const float sum = fmaf(fmaf(t, 256.f, (float)dd[1]), 256.f, (float)dd[0]);
         const uint32_t sw = wv[o >> 2];
-        const float scl = half_bits_to_f32_hw((o & 2) ? (sw >> 16) : (sw & 0xFFFFu));
-        // times the scale, then 2^(e-30) (ldexp: no overflow or early
-        // underflow for blocks of very large or very small x)
-        acc += ldexpf(sum * scl, exps[b] - 30) * units[b];
+        if constexpr (FMT == 3) {
+          // Q4_1 (d q + m: gguf_dequant's deq_q4_1, l2_codec.c:65-75): d *
+          // sum q_j m_j + m * sum m_j, both sums exact integers (below 2^39
+          // and 2^35) and both products exact in float64, so the block
+          // rounds once - taken apart in fp32 the two terms could cancel
+          // (a weight d q + m near 0 against an outlier x) and leave their
+          // roundings larger than the product
+          const double sq = fma((double)(dd[3] * 256 + dd[2]), 65536.0, (double)(dd[1] * 256 + dd[0]));
+          const int32_t *ds = dsum + b * 4;
+          const double sm = fma((double)(ds[3] * 256 + ds[2]), 65536.0, (double)(ds[1] * 256 + ds[0]));
+          const double v = fma((double)half_bits_to_f32_hw(sw & 0xFFFFu), sq,
+                               (double)half_bits_to_f32_hw(sw >> 16) * sm);
+          acc += (float)ldexp(v, exps[b] - 30) * units[b];
+        } else {
+          // |D3| <= 32*128*64, so D3*256 + D2 fits in int32
+          const float t = (float)(dd[3] * 256 + dd[2]);
+          const float sum = fmaf(fmaf(t, 256.f, (float)dd[1]), 256.f, (float)dd[0]);
+          const float scl = half_bits_to_f32_hw((o & 2) ? (sw >> 16) : (sw & 0xFFFFu));
+          // times the scale, then 2^(e-30) (ldexp: no overflow or early
+          // underflow for blocks of very large or very small x)
+          acc += ldexpf(sum * scl, exps[b] - 30) * units[b];
+        }
       }
       // the row's 16 lanes (lanes r, r + 4, ..., r + 60)
       acc += __shfl_xor(acc, 4);
@@ -994,7 +1014,7 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   if (!fused && p.x_vec4 && gemv_mma_plain(type, p.n, p.d) && ((uintptr_t)p.w & 3u) == 0) {
     p.steps = (p.d + 3) / 4;
     const size_t lds = (size_t)p.nb * (32u * 4u + 4u + 4u + 16u);
-    const int occ = fmt == 1 ? occ_mma<1>(lds) : occ_mma<2>(lds);
+    const int occ = fmt == 1 ? occ_mma<1>(lds) : fmt == 2 ? occ_mma<2>(lds) : occ_mma<3>(lds);
     const int waves = std::min(std::max((p.steps + kGemvMinSteps - 1) / kGemvMinSteps,
                                         std::min(p.steps, n_cu * 4)),
                                n_cu * std::max(1, occ) * waves_per_wg);
@@ -1002,8 +1022,10 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
     p.n_waves = wgs * waves_per_wg;
     if (fmt == 1)
       hipLaunchKernelGGL((k_gemv_mma<1, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
-    else
+    else if (fmt == 2)
       hipLaunchKernelGGL((k_gemv_mma<2, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    else
+      hipLaunchKernelGGL((k_gemv_mma<3, 2>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
     return hipGetLastError();
   }
   int lpr = 1;

@@ -130,14 +130,16 @@ def test_matmul_lm_head_full_size(gpu_device, t):
     check(out, x, w, t, n, d, "lm head")
 
 
+@pytest.mark.parametrize("t", [orc.T_Q4_0, orc.T_Q4_1])
 @pytest.mark.parametrize("case", ["normal", "outlier", "zero_blocks", "tiny", "huge"])
-def test_q4_matrix_core_path(gpu_device, case):
-    """Plain Q4_0 products of 1024-element rows with at least 32768 rows run
-    on the int8 matrix cores (x as four int8 digit planes of a 31-bit fixed
-    point per block): the same bar as every GEMV, with x that stresses the
-    digits - one channel 3e4 x the others, whole blocks of zeros, x near the
-    bottom of the normal range (1e-36) and near the top (1e35)."""
-    n, d, t = 1024, 40000, orc.T_Q4_0
+def test_q4_matrix_core_path(gpu_device, case, t):
+    """Plain Q4_0 and Q4_1 products of 1024-element rows with at least 32768
+    rows run on the int8 matrix cores (x as four int8 digit planes of a
+    31-bit fixed point per block; Q4_1's m times each block's sum of x): the
+    same bar as every GEMV, with x that stresses the digits - one channel
+    3e4 x the others, whole blocks of zeros, x near the bottom of the normal
+    range (1e-36) and near the top (1e35)."""
+    n, d = 1024, 40000
     rng = np.random.default_rng(4321)
     w = orc.random_weights(rng, t, n, d)
     x = rng.standard_normal(n).astype(np.float32)
@@ -150,7 +152,7 @@ def test_q4_matrix_core_path(gpu_device, case):
         x = (x * np.float32(1e-36)).astype(np.float32)
     elif case == "huge":
         x = (x * np.float32(1e30)).astype(np.float32)
-    print(f"[gemv] q4 matrix cores {case}", flush=True)
+    print(f"[gemv] q4 matrix cores type={t} {case}", flush=True)
     with attn.Context(SHAPE) as ctx:
         wd = ctx.weights_upload(w)
         try:
@@ -161,18 +163,19 @@ def test_q4_matrix_core_path(gpu_device, case):
             out = od.download(np.float32, d)
         finally:
             ctx.weights_free(wd)
-    check(out, x, w, t, n, d, f"q4 matrix cores {case}")
+    check(out, x, w, t, n, d, f"q4 matrix cores type {t} {case}")
 
 
 @pytest.mark.parametrize("n", [512, 1024, 2048, 3072])
 @pytest.mark.parametrize("case", ["normal", "outlier", "zero_blocks", "tiny", "huge"])
 def test_q8_digit_plane_path(gpu_device, n, case):
     """Q8_0 products over at least 32768 rows of 16-96 blocks take x as four
-    int8 digit planes of a 31-bit fixed point per block (integer dot
-    products against the quants): the same bar as every GEMV, with the x
-    that stresses the digits (one channel 3e4 x the others, whole blocks of
-    zeros, x near the bottom of the normal range and near the top), one and
-    two blocks per lane."""
+    int8 digit planes of a 31-bit fixed point per block: integer dot
+    products against the quants on the VALU (16, 64 and 96 blocks: one and
+    two blocks per lane) or on the int8 matrix cores (32 blocks).  The same
+    bar as every GEMV, with the x that stresses the digits (one channel 3e4
+    x the others, whole blocks of zeros, x near the bottom of the normal
+    range and near the top)."""
     d, t = 33000, orc.T_Q8_0
     rng = np.random.default_rng(77 + n)
     w = orc.random_weights(rng, t, n, d)
@@ -198,3 +201,34 @@ def test_q8_digit_plane_path(gpu_device, n, case):
         finally:
             ctx.weights_free(wd)
     check(out, x, w, t, n, d, f"q8 digit planes n {n} {case}")
+
+
+@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0, orc.T_Q4_1])
+@pytest.mark.parametrize("case", ["outlier", "tiny", "huge"])
+def test_vector_path_hard_x(gpu_device, case, t):
+    """The VALU GEMVs (fewer rows than the matrix cores take) with the x that
+    stresses a summation order: one channel 3e4 x the others, x near the
+    bottom of the normal range and near the top - the same bar as every
+    GEMV."""
+    n, d = 1024, 4096
+    rng = np.random.default_rng(99 + t)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    if case == "outlier":
+        x[37] = np.float32(3e4)
+    elif case == "tiny":
+        x = (x * np.float32(1e-36)).astype(np.float32)
+    else:
+        x = (x * np.float32(1e30)).astype(np.float32)
+    print(f"[gemv] vector path type={t} {case}", flush=True)
+    with attn.Context(SHAPE) as ctx:
+        wd = ctx.weights_upload(w)
+        try:
+            xd = hip.to_device(x)
+            od = hip.DeviceBuffer(d * 4)
+            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+            ctx.sync()
+            out = od.download(np.float32, d)
+        finally:
+            ctx.weights_free(wd)
+    check(out, x, w, t, n, d, f"vector path type {t} {case}")
