@@ -74,9 +74,10 @@ typedef struct g2b_model g2b_model;
 /* model_load_g2bx (l5_model.c:393-408) onto `device`: parse, upload the blob
  * to HBM, build the attention context for the model's shape and allocate the
  * KV for `ctx` positions (ctx <= 0: seq_len, as model_set_ctx's clamp) in F32
- * or Q8_0 (kv_q8).  The device forward supports matrices in F32, Q8_0 or
- * Q4_0 and F32 norm vectors and token embeddings in F32, F16, Q8_0 or Q4_0;
- * other slot types are G2B_EUNSUP at load (the reference dequantises them). */
+ * or Q8_0 (kv_q8).  The device forward supports matrices and token
+ * embeddings in F32, F16, Q8_0, Q4_0 or Q4_1 and norm vectors in F32; other
+ * slot types (the K-quants, whose gguf_dequant output the reference leaves
+ * undefined, as include/g2b_matmul.h says) are G2B_EUNSUP at load. */
 int g2b_model_load_g2bx(g2b_model **out, int32_t device, const char *path, int32_t kv_q8,
                         int32_t ctx);
 int g2b_model_free(g2b_model *m);
