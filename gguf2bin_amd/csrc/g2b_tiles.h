@@ -21,9 +21,10 @@
 // the block's fp16 scale; blocks are summed in float64 and the score is
 // rounded to fp32 once.  Softmax stays in that layout (each lane one (head, position); the
 // running maximum of a head is shared by its 16 lanes through DPP), and V is
-// accumulated on the VALU: lane (KV head of the wave's pair, four dims) takes
-// p * v_scale for its block from a per-wave LDS exchange and does 4 x G FMAs
-// per position.
+// accumulated in fp32 on the matrix cores as well: lane (KV head of the
+// wave's pair, four dims) takes p * v_scale for its block from a per-wave LDS
+// exchange, and four v_mfma_f32_4x4x1_16b_f32 per position add p * v_scale *
+// v for every head of the group to the lane's four dims.
 //
 // Streaming: a workgroup streams tiles of 16 positions - the K and V rows of
 // 16 consecutive positions are two contiguous runs of 16 x 1088 bytes - from
@@ -76,7 +77,7 @@ __host__ __device__ inline bool tiles_shape_ok(const ShapeDev &sh) {
 }
 
 // k_tiles' dynamic LDS: tile buffer 0, each wave's exchange of p * v_scale
-// ([kv][block][position][head]) and rescale factors ([kv][head]), tile
+// ([kv][block][head][position]) and rescale factors ([kv][head]), tile
 // buffer 1.  The setup's scratch starts at the exchange and lies over it and
 // buffer 1 (never over buffer 0, whose loads the static schedule issues
 // before the setup): rotated q at 0, the new k after it, the digit planes
@@ -91,10 +92,10 @@ struct TilesLds {
   uint32_t kr, dig, vr, rows, row_pad, scr;  // (relative to scr0)
   uint32_t px, buf1, total;                   // (absolute)
 };
-// The exchange holds one group of kTileRows x 4 floats per (KV head, block),
-// kTilesPxGroup floats apart: the V loop's lanes read the eight groups at the
-// same position together, and at 64 floats (256 bytes) apart those reads all
-// fell on the same four banks.
+// The exchange holds one group of 4 heads x kTileRows floats per (KV head,
+// block), kTilesPxGroup floats apart: the V loop's lanes read the eight
+// groups together (four positions of one head each), and at 64 floats (256
+// bytes) apart such reads all fell on the same four banks.
 constexpr int kTilesPxGroup = kTileRows * 4 + 4;
 __host__ __device__ inline uint32_t tiles_px_floats() {
   return (uint32_t)(kTilesKvPerWave * (kTilesHd / 32) * kTilesPxGroup + kTilesKvPerWave * 4);
@@ -255,16 +256,17 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       }
     }
 
-    float m[KPW], l[KPW], acc[G][4];
+    // acc[j][h]: head h of the lane's KV head at dim 4*vd + j (the C/D
+    // layout of v_mfma_f32_4x4x1_16b_f32, below)
+    float m[KPW], l[KPW];
+    f32x4 acc[4];
 #pragma unroll
     for (int kk = 0; kk < KPW; kk++) {
       m[kk] = kNegBig;
       l[kk] = 0.f;
     }
 #pragma unroll
-    for (int h = 0; h < G; h++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) acc[h][j] = 0.f;
+    for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // V lane addressing inside a row: dims 4*vd.. of head (wave*KPW + vkv)
     const uint32_t voff = 34u * (uint32_t)((wave * KPW + vkv) * NB + vblk) + 2u + 4u * (vd & 7);
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
           const uint32_t blk = (uint32_t)(kvg * NB + b);
           const uint32_t sw = *reinterpret_cast<const uint32_t *>(vrow + ((34u * blk) & ~3u));
           const float vs = half_bits_to_f32_hw(sw >> ((blk & 1u) * 16u));
-          px[(kk * NB + b) * kTilesPxGroup + col * 4 + quarter] = p * vs;
+          px[(kk * NB + b) * kTilesPxGroup + quarter * TP + col] = p * vs;
         }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -355,30 +357,36 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (rescale) {
         const float4 f = *reinterpret_cast<const float4 *>(pfac + vkv * 4);
-        const float fa[4] = {f.x, f.y, f.z, f.w};
+        const f32x4 fa = {f.x, f.y, f.z, f.w};
 #pragma unroll
-        for (int h = 0; h < G; h++)
-#pragma unroll
-          for (int j = 0; j < 4; j++) acc[h][j] *= fa[h];
+        for (int j = 0; j < 4; j++) acc[j] *= fa;
       }
-      const float *pv = px + (vkv * NB + vblk) * kTilesPxGroup;
-      auto vstep = [&](int t) {
-        const float4 p4 = *reinterpret_cast<const float4 *>(pv + t * 4);
+      // V on the matrix cores: v_mfma_f32_4x4x1_16b_f32 is 16 blocks of
+      // D[i][n] += A[i] B[n] with block g = lanes 4g..4g+3, A[i] from lane
+      // 4g+i, B[n] from lane 4g+n and D[i][n] in register i of lane 4g+n.
+      // A lane's block shares its KV head and Q8_0 block, so A = p x v_scale
+      // of head (lane & 3) and B = the lane's own int8 at dim 4*vd + j put
+      // head i's sum over positions for that dim in register i of the lane
+      // (fp32 products accumulated in fp32, position by position).
+      const float *pv = px + (vkv * NB + vblk) * kTilesPxGroup + (lane & 3) * TP;
+      auto vstep = [&](int t, float a) {
         const uint32_t *w = reinterpret_cast<const uint32_t *>(V + (size_t)t * stride + valn);
         const uint32_t x = __builtin_amdgcn_perm(w[1], w[0], vsel);
-        const float pw[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float v = i8f(x, j);
-#pragma unroll
-          for (int h = 0; h < G; h++) acc[h][j] = fmaf(pw[h], v, acc[h][j]);
-        }
+        for (int j = 0; j < 4; j++)
+          acc[j] = __builtin_amdgcn_mfma_f32_4x4x1f32(a, i8f(x, j), acc[j], 0, 0, 0);
       };
       if (nrows == TP) {
 #pragma unroll
-        for (int t = 0; t < TP; t++) vstep(t);
+        for (int t = 0; t < TP; t += 4) {  // four positions' p x v_scale in one read
+          const float4 a4 = *reinterpret_cast<const float4 *>(pv + t);
+          vstep(t, a4.x);
+          vstep(t + 1, a4.y);
+          vstep(t + 2, a4.z);
+          vstep(t + 3, a4.w);
+        }
       } else {
-        for (int t = 0; t < nrows; t++) vstep(t);
+        for (int t = 0; t < nrows; t++) vstep(t, pv[t]);
       }
       // (px is written again only after these reads: the wave's next K
       // phase)
@@ -480,13 +488,13 @@ __global__ __launch_bounds__(kThreads) void k_tiles(DecodeParams P) {
         float *out = P.q_out + sidx * nq + (size_t)head * HD + 4 * vd;
         const double L = (double)lh;
         *reinterpret_cast<float4 *>(out) =
-            make_float4((float)((double)acc[h][0] / L), (float)((double)acc[h][1] / L),
-                        (float)((double)acc[h][2] / L), (float)((double)acc[h][3] / L));
+            make_float4((float)((double)acc[0][h] / L), (float)((double)acc[1][h] / L),
+                        (float)((double)acc[2][h] / L), (float)((double)acc[3][h] / L));
       } else {
         float *pp = P.part + ((sidx * (size_t)n_heads + (size_t)head) * (size_t)P.max_splits +
                               (size_t)pslot) * pstr;
         *reinterpret_cast<float4 *>(pp + kPartHead + 4 * vd) =
-            make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+            make_float4(acc[0][h], acc[1][h], acc[2][h], acc[3][h]);
         if (vd == 0) {
           pp[0] = mh;
           pp[1] = lh;
