@@ -49,6 +49,9 @@ from gguf2bin_amd import attn, hip  # noqa: E402
 
 METRIC = "decode-attention KV-read GB/s (% of HBM peak) + us/step, Qwen3-0.6B shape"
 HBM_PEAK_GBPS = 8000.0
+# the weight copies one GEMV measurement cycles through (more than MI355X's
+# 256 MB last-level cache holds)
+GEMV_COLD_BYTES = 1 << 30
 Q3, LL = attn.ARCH_QWEN3, attn.ARCH_LLAMA
 
 # name: (shape, n_seq, (ctx_lo, ctx_hi) cached positions, K-row x8 probability, description)
@@ -480,20 +483,26 @@ def gemv_leg(args):
     for t, name in ((attn.T_Q8_0, "q8_0"), (attn.T_Q4_0, "q4_0"), (attn.T_F32, "f32"),
                     (attn.T_F16, "f16"), (attn.T_Q4_1, "q4_1")):
         w = orc.random_weights(rng, t, n, d)
-        wd = ctx.weights_upload(w)
-        for _ in range(3):
-            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+        # Launches cycle through copies of the matrix totalling at least
+        # GEMV_COLD_BYTES, so that each reads its weights from HBM: a matrix
+        # under the 256 MB of MI355X's last-level cache, launched back to
+        # back, would otherwise be partly served from that cache.
+        ncopy = max(2, -(-GEMV_COLD_BYTES // w.nbytes))
+        wds = [ctx.weights_upload(w) for _ in range(ncopy)]
+        for k in range(ncopy):
+            ctx.matmul(od.ptr, xd.ptr, wds[k], t, n, d)
         ctx.sync()
         e0, e1 = hip.Event(), hip.Event()
-        K = max(20, args.steps * 5)
+        K = ncopy * max(1, -(-max(20, args.steps * 5) // ncopy))
         e0.record(ctx.stream)
-        for _ in range(K):
-            ctx.matmul(od.ptr, xd.ptr, wd, t, n, d)
+        for k in range(K):
+            ctx.matmul(od.ptr, xd.ptr, wds[k % ncopy], t, n, d)
         e1.record(ctx.stream)
         e1.synchronize()
         us = e0.elapsed_ms(e1) / K * 1e3
         out = od.download(np.float32, d)
-        ctx.weights_free(wd)
+        for wd in wds:
+            ctx.weights_free(wd)
         rows = np.sort(rng.choice(d, 4096, replace=False))
         wr = w.reshape(d, -1)[rows].reshape(-1)
         ex, ab = orc.matmul_exact(x, wr, t, n, len(rows))
@@ -510,6 +519,7 @@ def gemv_leg(args):
                 break
         cpu_s = (time.perf_counter() - t0) / reps
         res[name] = {"us": round(us, 2), "GBps": round(w.nbytes / us / 1e3, 1),
+                     "copies_cycled": ncopy,
                      "pct_hbm_peak": round(100 * w.nbytes / us / 1e3 / HBM_PEAK_GBPS, 1),
                      "weight_bytes": int(w.nbytes),
                      "max_err_over_sum_abs": rel,
