@@ -23,6 +23,7 @@
 #include <algorithm>
 
 #include "g2b_internal.h"
+#include "g2b_layer.h"  // LDS DMA (dma16, raw_rsrc, lds_addr, wait_vm0)
 
 namespace g2b {
 
@@ -523,7 +524,16 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_q(GemvParams P) {
 // outlier channels cost nothing.  Q4_0 quants go in as their nibbles (0..15)
 // with the -8 folded in as 8 x the block's digit sums.  Against the VALU path
 // (a convert and an FMA per weight) this is ~0.5 VALU operations per weight.
-template <int FMT, int BPL>
+// k_gemv_mma's LDS: x's digit planes, exponents, units and digit sums of nb
+// blocks (152 bytes a block), then with DMA two regions per wave of a pair of
+// wave-steps' rows (row_bytes x 8, in whole KiB).
+__host__ __device__ constexpr size_t mma_dma_lds_offset(int nb) {
+  return ((size_t)nb * 152u + 15u) & ~(size_t)15u;
+}
+__host__ __device__ constexpr size_t mma_dma_region(int block_bytes) {
+  return ((size_t)8 * 32 * block_bytes + 1023u) & ~(size_t)1023u;
+}
+template <int FMT, int BPL, bool DMA = false>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
   extern __shared__ float xs[];  // the digit planes of x
   constexpr int BB = FMT == 1 ? 34 : FMT == 2 ? 18 : 20;
@@ -592,6 +602,78 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
     __syncthreads();
   };
   const int stride = P.n_waves;
+  // one wave-step of four rows: the lane's span wv of row rw (stored if real)
+  auto step = [&](const uint32_t *wv, int rw, bool real) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < BPL; k++) {
+      const int b = g * BPL + k;
+      // the block's first byte in the span (quants from o + 2; Q4_1: d, m,
+      // then the nibbles from o + 4)
+      const int o = k * BB;
+      typedef int v4i __attribute__((ext_vector_type(4)));
+      v4i dd = {0, 0, 0, 0};
+      // quant word j of the block: bytes o + 2 + 4j .. (o is even), Q4_1
+      // o + 4 + 4j (o a multiple of 4)
+      auto qword = [&](int jw) -> uint32_t {
+        const int byte = o + (FMT == 3 ? 4 : 2) + 4 * jw;
+        const int wi = byte >> 2;
+        return (byte & 2) ? __builtin_amdgcn_perm(wv[wi + 1], wv[wi], 0x05040302u) : wv[wi];
+      };
+      // A: plane r of the block's eight chunks
+      const uint4 a03 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8);
+      const uint4 a47 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8 + 4);
+      const uint32_t av[8] = {a03.x, a03.y, a03.z, a03.w, a47.x, a47.y, a47.z, a47.w};
+      if constexpr (FMT == 1) {
+#pragma unroll
+        for (int jw = 0; jw < 8; jw++)
+          dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)qword(jw), dd, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int jw = 0; jw < 4; jw++) {
+          const uint32_t w = qword(jw);
+          dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)(w & 0x0F0F0F0Fu), dd, 0, 0,
+                                                 0);
+          dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[4 + jw], (int)((w >> 4) & 0x0F0F0F0Fu),
+                                                 dd, 0, 0, 0);
+        }
+        if constexpr (FMT == 2) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) dd[q] -= 8 * dsum[b * 4 + q];
+        }
+      }
+      const uint32_t sw = wv[o >> 2];
+      if constexpr (FMT == 3) {
+        // Q4_1 (d q + m: gguf_dequant's deq_q4_1, l2_codec.c:65-75): d *
+        // sum q_j m_j + m * sum m_j, both sums exact integers (below 2^39
+        // and 2^35) and both products exact in float64, so the block
+        // rounds once - taken apart in fp32 the two terms could cancel
+        // (a weight d q + m near 0 against an outlier x) and leave their
+        // roundings larger than the product
+        const double sq = fma((double)(dd[3] * 256 + dd[2]), 65536.0, (double)(dd[1] * 256 + dd[0]));
+        const int32_t *ds = dsum + b * 4;
+        const double sm = fma((double)(ds[3] * 256 + ds[2]), 65536.0, (double)(ds[1] * 256 + ds[0]));
+        const double v = fma((double)half_bits_to_f32_hw(sw & 0xFFFFu), sq,
+                             (double)half_bits_to_f32_hw(sw >> 16) * sm);
+        acc += (float)ldexp(v, exps[b] - 30) * units[b];
+      } else {
+        // |D3| <= 32*128*64, so D3*256 + D2 fits in int32
+        const float t = (float)(dd[3] * 256 + dd[2]);
+        const float sum = fmaf(fmaf(t, 256.f, (float)dd[1]), 256.f, (float)dd[0]);
+        const float scl = half_bits_to_f32_hw((o & 2) ? (sw >> 16) : (sw & 0xFFFFu));
+        // times the scale, then 2^(e-30) (ldexp: no overflow or early
+        // underflow for blocks of very large or very small x)
+        acc += ldexpf(sum * scl, exps[b] - 30) * units[b];
+      }
+    }
+    // the row's 16 lanes (lanes r, r + 4, ..., r + 60)
+    acc += __shfl_xor(acc, 4);
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (real && g == 0) P.out[rw] = acc;
+  };
+  if constexpr (!DMA) {
   for (int s0 = gw, trip = 0;; s0 += stride * UN, trip++) {
     // this trip's spans: UN wave-steps of four rows, each lane its row's
     // BPL blocks (dword loads; a row's 16 lanes cover it, so its lines are
@@ -625,78 +707,58 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_mma(GemvParams P) {
     }
     if (trip == 0) x_digits();
 #pragma unroll
-    for (int u = 0; u < UN; u++) {
-      const uint32_t *wv = wvs[u];
-      float acc = 0.f;
-#pragma unroll
-      for (int k = 0; k < BPL; k++) {
-        const int b = g * BPL + k;
-        // the block's first byte in the span (quants from o + 2; Q4_1: d, m,
-        // then the nibbles from o + 4)
-        const int o = k * BB;
-        typedef int v4i __attribute__((ext_vector_type(4)));
-        v4i dd = {0, 0, 0, 0};
-        // quant word j of the block: bytes o + 2 + 4j .. (o is even), Q4_1
-        // o + 4 + 4j (o a multiple of 4)
-        auto qword = [&](int jw) -> uint32_t {
-          const int byte = o + (FMT == 3 ? 4 : 2) + 4 * jw;
-          const int wi = byte >> 2;
-          return (byte & 2) ? __builtin_amdgcn_perm(wv[wi + 1], wv[wi], 0x05040302u) : wv[wi];
-        };
-        // A: plane r of the block's eight chunks
-        const uint4 a03 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8);
-        const uint4 a47 = *reinterpret_cast<const uint4 *>(dig + (b * 4 + r) * 8 + 4);
-        const uint32_t av[8] = {a03.x, a03.y, a03.z, a03.w, a47.x, a47.y, a47.z, a47.w};
-        if constexpr (FMT == 1) {
-#pragma unroll
-          for (int jw = 0; jw < 8; jw++)
-            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)qword(jw), dd, 0, 0, 0);
-        } else {
-#pragma unroll
-          for (int jw = 0; jw < 4; jw++) {
-            const uint32_t w = qword(jw);
-            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[jw], (int)(w & 0x0F0F0F0Fu), dd, 0, 0,
-                                                   0);
-            dd = __builtin_amdgcn_mfma_i32_4x4x4i8((int)av[4 + jw], (int)((w >> 4) & 0x0F0F0F0Fu),
-                                                   dd, 0, 0, 0);
-          }
-          if constexpr (FMT == 2) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) dd[q] -= 8 * dsum[b * 4 + q];
-          }
-        }
-        const uint32_t sw = wv[o >> 2];
-        if constexpr (FMT == 3) {
-          // Q4_1 (d q + m: gguf_dequant's deq_q4_1, l2_codec.c:65-75): d *
-          // sum q_j m_j + m * sum m_j, both sums exact integers (below 2^39
-          // and 2^35) and both products exact in float64, so the block
-          // rounds once - taken apart in fp32 the two terms could cancel
-          // (a weight d q + m near 0 against an outlier x) and leave their
-          // roundings larger than the product
-          const double sq = fma((double)(dd[3] * 256 + dd[2]), 65536.0, (double)(dd[1] * 256 + dd[0]));
-          const int32_t *ds = dsum + b * 4;
-          const double sm = fma((double)(ds[3] * 256 + ds[2]), 65536.0, (double)(ds[1] * 256 + ds[0]));
-          const double v = fma((double)half_bits_to_f32_hw(sw & 0xFFFFu), sq,
-                               (double)half_bits_to_f32_hw(sw >> 16) * sm);
-          acc += (float)ldexp(v, exps[b] - 30) * units[b];
-        } else {
-          // |D3| <= 32*128*64, so D3*256 + D2 fits in int32
-          const float t = (float)(dd[3] * 256 + dd[2]);
-          const float sum = fmaf(fmaf(t, 256.f, (float)dd[1]), 256.f, (float)dd[0]);
-          const float scl = half_bits_to_f32_hw((o & 2) ? (sw >> 16) : (sw & 0xFFFFu));
-          // times the scale, then 2^(e-30) (ldexp: no overflow or early
-          // underflow for blocks of very large or very small x)
-          acc += ldexpf(sum * scl, exps[b] - 30) * units[b];
-        }
-      }
-      // the row's 16 lanes (lanes r, r + 4, ..., r + 60)
-      acc += __shfl_xor(acc, 4);
-      acc += __shfl_xor(acc, 8);
-      acc += __shfl_xor(acc, 16);
-      acc += __shfl_xor(acc, 32);
-      if (ok[u] && g == 0) P.out[row[u]] = acc;
-    }
+    for (int u = 0; u < UN; u++) step(wvs[u], row[u], ok[u]);
     if (s0 + stride * UN >= P.steps) break;
+  }
+  } else {
+    // The weights through LDS: each wave streams pairs of adjacent
+    // wave-steps (eight contiguous rows) with LDS DMA into two regions of its
+    // own, 1 KiB per load and lane l taking bytes 16 l of each KiB, so every
+    // load is one contiguous run (the direct loads above, each lane a span
+    // of its row, touch every line of four rows per instruction).  The pair
+    // in one region is consumed while the next one lands in the other.
+    constexpr int RB = 32 * BB;                 // row bytes (1024-element rows)
+    constexpr int PB = 8 * RB;                  // a pair's bytes
+    constexpr int NI = (PB + 1023) / 1024;      // loads per pair
+    const int wave = threadIdx.x >> 6;
+    const uint32_t region0 =
+        lds_addr(xs) + (uint32_t)mma_dma_lds_offset(NB) + (uint32_t)wave * 2u * (uint32_t)(NI * 1024);
+    const int npairs = (P.steps + 1) / 2;
+    const i32x4 rsrc = raw_rsrc(P.w, (uint32_t)((size_t)P.d * RB));
+    auto issue = [&](int pr, int k) {
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(region0 + (uint32_t)k * (uint32_t)(NI * 1024));
+      const uint32_t b0 = (uint32_t)pr * (uint32_t)PB;
+#pragma unroll
+      for (int i = 0; i < NI; i++) {
+        const uint32_t off = 1024u * (uint32_t)i + 16u * (uint32_t)lane;
+        if (off < (uint32_t)PB) dma16(rsrc, dst + 1024u * (uint32_t)i, b0 + off);
+      }
+    };
+    const uint8_t *lds_w = reinterpret_cast<const uint8_t *>(xs) + mma_dma_lds_offset(NB) +
+                           (size_t)wave * 2 * (NI * 1024);
+    int pr = gw;
+    issue(pr, 0);
+    x_digits();  // (every wave: it holds a workgroup barrier)
+    for (int k = 0;; k ^= 1) {
+      wait_vm0();  // this pair has landed (nothing else of the wave is in flight)
+      __asm__ volatile("" ::: "memory");
+      const int pn = pr + stride;
+      const bool more = pn < npairs;
+      if (more) issue(pn, k ^ 1);
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int st = 2 * pr + u;
+        const int rw = st * 4 + r;
+        const uint32_t *sp = reinterpret_cast<const uint32_t *>(
+            lds_w + (size_t)k * (NI * 1024) + (size_t)(u * 4 + r) * RB + (size_t)g * (BPL * BB));
+        uint32_t wv[NW];
+#pragma unroll
+        for (int i = 0; i < NW; i++) wv[i] = sp[i];
+        step(wv, rw, st < P.steps && rw < P.d);
+      }
+      if (!more) break;
+      pr = pn;
+    }
   }
 }
 
@@ -941,13 +1003,13 @@ hipError_t launch_split_lpr(const GemvParams &p, int kb, dim3 grid, hipStream_t 
 
 // k_gemv_mma<FMT, 2> (Q8_0 / Q4_0, 1024-element rows): resident workgroups
 // per CU, queried once per form.
-template <int FMT>
+template <int FMT, bool DMA = false>
 int occ_mma(size_t lds) {
   static int cached = 0;
   int &o = cached;
   if (o <= 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_mma<FMT, 2>, kGemvThreads, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv_mma<FMT, 2, DMA>, kGemvThreads, lds) !=
         hipSuccess) {
       (void)hipGetLastError();
       n = 1;
@@ -1042,6 +1104,27 @@ hipError_t launch_gemv(GemvParams p, int32_t type, int n_cu, hipStream_t s) {
   // and this plain product instead.  Measured slower elsewhere: Q4_0 4096 x
   // 14336 29.6 against 13.8 us, 4096-row matrices 4.7-5.0 against 4.4 us
   // (the digit prologue of every workgroup).
+  if (!fused && p.x_vec4 && gemv_mma_plain(type, p.n, p.d) && ((uintptr_t)p.w & 15u) == 0 &&
+      (size_t)p.d * p.row_bytes < ((size_t)1 << 31)) {
+    // the LDS-DMA form: pairs of wave-steps per wave
+    p.steps = (p.d + 3) / 4;
+    const int bb = fmt == 1 ? 34 : fmt == 2 ? 18 : 20;
+    const size_t lds = mma_dma_lds_offset(p.nb) + (size_t)waves_per_wg * 2 * mma_dma_region(bb);
+    const int occ = fmt == 1   ? occ_mma<1, true>(lds)
+                    : fmt == 2 ? occ_mma<2, true>(lds)
+                               : occ_mma<3, true>(lds);
+    const int npairs = (p.steps + 1) / 2;
+    const int waves = std::min(npairs, n_cu * std::max(1, occ) * waves_per_wg);
+    const int wgs = std::max(1, (waves + waves_per_wg - 1) / waves_per_wg);
+    p.n_waves = wgs * waves_per_wg;
+    if (fmt == 1)
+      hipLaunchKernelGGL((k_gemv_mma<1, 2, true>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    else if (fmt == 2)
+      hipLaunchKernelGGL((k_gemv_mma<2, 2, true>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    else
+      hipLaunchKernelGGL((k_gemv_mma<3, 2, true>), dim3(wgs), dim3(kGemvThreads), lds, s, p);
+    return hipGetLastError();
+  }
   if (!fused && p.x_vec4 && gemv_mma_plain(type, p.n, p.d) && ((uintptr_t)p.w & 3u) == 0) {
     p.steps = (p.d + 3) / 4;
     const size_t lds = (size_t)p.nb * (32u * 4u + 4u + 4u + 16u);
