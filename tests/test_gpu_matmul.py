@@ -232,3 +232,32 @@ def test_vector_path_hard_x(gpu_device, case, t):
         finally:
             ctx.weights_free(wd)
     check(out, x, w, t, n, d, f"vector path type {t} {case}")
+
+
+@pytest.mark.parametrize("t", [orc.T_Q8_0, orc.T_Q4_0, orc.T_Q4_1])
+@pytest.mark.parametrize("form", ["lds_dma", "direct"])
+def test_matrix_core_ragged_rows(gpu_device, t, form):
+    """The matrix-core GEMV at a row count that ends inside a trip: 32771
+    rows are 8193 wave-steps of four, so the LDS-DMA form's last pair holds
+    one real wave-step of three rows and one past the matrix (its loads run
+    past the buffer's end and read zeros).  A 16-byte aligned matrix takes
+    the LDS-DMA form, one 4 bytes off takes the direct loads.  Every row
+    against the float64 product, and nothing stored past the last row."""
+    n, d = 1024, 32771
+    rng = np.random.default_rng(5150 + t)
+    w = orc.random_weights(rng, t, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    pad = 0 if form == "lds_dma" else 4
+    print(f"[gemv] ragged rows type={t} {form}", flush=True)
+    with attn.Context(SHAPE) as ctx:
+        wd = ctx.weights_upload(np.concatenate([np.zeros(pad, np.uint8), w]))
+        try:
+            xd = hip.to_device(x)
+            od = hip.to_device(np.full(d + 64, 7.0, np.float32))
+            ctx.matmul(od.ptr, xd.ptr, wd + pad, t, n, d)
+            ctx.sync()
+            full = od.download(np.float32, d + 64)
+        finally:
+            ctx.weights_free(wd)
+    assert np.all(full[d:] == 7.0), "stores past the last row"
+    check(full[:d], x, w, t, n, d, f"ragged rows type {t} {form}")
